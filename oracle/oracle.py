@@ -1,0 +1,128 @@
+"""ctypes wrapper of liboracle_sdpa.so — TEST INFRASTRUCTURE ONLY.
+
+The oracle is the parity checker (a CPU restatement of the reference's
+emitted SDPA, see sdpa_oracle.h). Only tests/, the smoke check and the
+CPU-baseline leg of bench.py load it; the product path never does.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "liboracle_sdpa.so")
+_lib = None
+
+
+class Spec(ctypes.Structure):
+    _fields_ = [("heads", ctypes.c_uint64), ("gqa", ctypes.c_uint64), ("head_dim", ctypes.c_uint64),
+                ("q_row", ctypes.c_uint64), ("q_head", ctypes.c_uint64), ("out_row", ctypes.c_uint64)]
+
+
+class Call(ctypes.Structure):
+    _fields_ = [("q", ctypes.c_void_p), ("keys", ctypes.c_void_p), ("values", ctypes.c_void_p),
+                ("output", ctypes.c_void_p), ("rows", ctypes.c_uint64), ("past", ctypes.c_uint64),
+                ("kv_stride", ctypes.c_uint64), ("scale", ctypes.c_float), ("sink", ctypes.c_float)]
+
+
+def build() -> None:
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        L = ctypes.CDLL(_LIB_PATH)
+        u16p = ctypes.c_void_p
+        L.oracle_bf16_to_f32.argtypes = [ctypes.c_uint16]
+        L.oracle_bf16_to_f32.restype = ctypes.c_float
+        L.oracle_f32_to_bf16_rne.argtypes = [ctypes.c_float]
+        L.oracle_f32_to_bf16_rne.restype = ctypes.c_uint16
+        L.oracle_cvtneps2bf16.argtypes = [ctypes.c_float]
+        L.oracle_cvtneps2bf16.restype = ctypes.c_uint16
+        L.oracle_dpbf16_lane.argtypes = [ctypes.c_float, ctypes.c_uint32, ctypes.c_uint32]
+        L.oracle_dpbf16_lane.restype = ctypes.c_float
+        L.oracle_exp_poly.argtypes = [ctypes.c_float]
+        L.oracle_exp_poly.restype = ctypes.c_float
+        L.oracle_qk_dot.argtypes = [u16p, u16p, ctypes.c_int]
+        L.oracle_qk_dot.restype = ctypes.c_float
+        L.oracle_sdpa_head.argtypes = [u16p, u16p, u16p, ctypes.c_void_p, u16p, ctypes.c_uint64,
+                                       ctypes.c_float, ctypes.c_int]
+        L.oracle_sdpa_head.restype = None
+        L.oracle_sdpa_prefill_block.argtypes = [u16p, u16p, u16p, ctypes.c_void_p, u16p, ctypes.c_uint64,
+                                                ctypes.c_float, ctypes.c_int, ctypes.c_int, ctypes.c_size_t,
+                                                ctypes.c_size_t]
+        L.oracle_sdpa_prefill_block.restype = None
+        L.oracle_attention_scalar.argtypes = [ctypes.POINTER(Spec), ctypes.POINTER(Call)]
+        L.oracle_attention_scalar.restype = ctypes.c_int
+        L.oracle_attention_avx512.argtypes = [ctypes.POINTER(Spec), ctypes.POINTER(Call), ctypes.c_int]
+        L.oracle_attention_avx512.restype = ctypes.c_int
+        L.oracle_avx512_available.restype = ctypes.c_int
+        L.oracle_physical_cores.restype = ctypes.c_int
+        L.oracle_dpbf16_selfcheck.argtypes = [ctypes.c_uint64, ctypes.c_long]
+        L.oracle_dpbf16_selfcheck.restype = ctypes.c_long
+        L.oracle_cvt_exp_selfcheck.argtypes = [ctypes.c_uint64, ctypes.c_long]
+        L.oracle_cvt_exp_selfcheck.restype = ctypes.c_long
+        _lib = L
+    return _lib
+
+
+def _ptr(a: np.ndarray) -> int:
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data
+
+
+def avx512_available() -> bool:
+    return bool(lib().oracle_avx512_available())
+
+
+def attention(w, impl: str = "auto", threads: int = 0) -> np.ndarray:
+    """Run the reference attention node on workload `w`; returns out bf16 bits
+    [rows][heads][head_dim]. impl: 'scalar', 'avx512' or 'auto' (AVX-512
+    when the host has it, which is bit-identical to the scalar one)."""
+    L = lib()
+    out = np.zeros((w.rows, w.heads, w.head_dim), dtype=np.uint16)
+    q = np.ascontiguousarray(w.q)
+    k = np.ascontiguousarray(w.k)
+    v = np.ascontiguousarray(w.v)
+    spec = Spec(w.heads, w.gqa, w.head_dim, w.q_row, w.head_dim, w.out_row)
+    call = Call(_ptr(q), _ptr(k), _ptr(v), _ptr(out), w.rows, w.past, w.kv_stride, w.scale, 0.0)
+    if impl == "auto":
+        impl = "avx512" if L.oracle_avx512_available() else "scalar"
+    if impl == "avx512":
+        rc = L.oracle_attention_avx512(ctypes.byref(spec), ctypes.byref(call), threads)
+    else:
+        rc = L.oracle_attention_scalar(ctypes.byref(spec), ctypes.byref(call))
+    if rc != 0:
+        raise RuntimeError(f"oracle attention failed rc={rc}")
+    return out
+
+
+def head(q: np.ndarray, k: np.ndarray, v: np.ndarray, n: int, scale: float) -> np.ndarray:
+    """One decode head (scalar emulation): q [d], k/v [>=n][d] -> out [d] bf16 bits."""
+    d = q.shape[-1]
+    q = np.ascontiguousarray(q, dtype=np.uint16)
+    k = np.ascontiguousarray(k, dtype=np.uint16)
+    v = np.ascontiguousarray(v, dtype=np.uint16)
+    sc = np.zeros(((n + 15) // 16) * 16, dtype=np.float32)
+    out = np.zeros(d, dtype=np.uint16)
+    lib().oracle_sdpa_head(_ptr(q), _ptr(k), _ptr(v), _ptr(sc), _ptr(out), n, scale, d)
+    return out
+
+
+def prefill_block(q: np.ndarray, k: np.ndarray, v: np.ndarray, past: int, scale: float) -> np.ndarray:
+    """The 8-row prefill block (scalar emulation): q [rows][d] -> out [rows][d]."""
+    rows, d = q.shape
+    q = np.ascontiguousarray(q, dtype=np.uint16)
+    k = np.ascontiguousarray(k, dtype=np.uint16)
+    v = np.ascontiguousarray(v, dtype=np.uint16)
+    N = past + rows
+    sc = np.zeros(rows * ((N + 15) // 16) * 16, dtype=np.float32)
+    out = np.zeros((rows, d), dtype=np.uint16)
+    lib().oracle_sdpa_prefill_block(_ptr(q), _ptr(k), _ptr(v), _ptr(sc), _ptr(out), past, scale, d, rows, d, d)
+    return out
