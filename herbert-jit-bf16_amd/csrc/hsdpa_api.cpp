@@ -1,0 +1,203 @@
+// hsdpa_api.cpp — the C ABI of include/hsdpa.h: geometry validation at plan
+// time, call validation on the host before any launch, workspace layout and
+// the choice between the decode and the prefill kernels.
+
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstring>
+#include <mutex>
+#include <new>
+
+#include "hsdpa.h"
+#include "hsdpa_kernels.h"
+
+struct hsdpa_plan {
+    hsdpa_spec spec;
+    uint64_t kv_heads;
+    // decode workspace (floats): scores, per-workgroup maxima, partials
+    uint64_t dec_npad;        // scores row length for a full cache
+    uint64_t dec_nwg;         // workgroups per KV head for a full cache
+    uint64_t off_scores, off_wgmax, off_part_o, off_part_l, dec_bytes;
+    // prefill workspace: V^T [kv_heads][head_dim][pre_ld] bf16
+    uint64_t pre_ld, pre_bytes;
+    uint64_t ws_bytes;
+};
+
+namespace {
+
+constexpr uint64_t kAlign = 256;
+uint64_t align_up(uint64_t x, uint64_t a) { return (x + a - 1) / a * a; }
+bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// SdpaShape::check (src/jit/ir.rs:130-148) and tile_selector's geometry
+// checks (src/jit/target/x86/execution/attention.rs:61-98), plus the cache
+// geometry of KvSpec::validate (src/jit/execution/abi.rs:75-103).
+hsdpa_status check_spec(const hsdpa_spec &s)
+{
+    if (s.heads == 0 || s.gqa == 0 || s.head_dim == 0) return HSDPA_ERR_EMPTY;
+    if (s.head_dim % 32 != 0 || s.head_dim > 512) return HSDPA_ERR_HEAD_DIM;
+    if (!hsdpa::head_dim_supported(static_cast<int>(s.head_dim))) return HSDPA_ERR_HEAD_DIM;
+    if (s.heads % s.gqa != 0) return HSDPA_ERR_GQA;
+    if (s.sink != 0) return HSDPA_ERR_SINK_UNSUPPORTED;
+    const uint64_t lim = static_cast<uint64_t>(INT32_MAX) / 2;
+    if (s.heads > lim || s.gqa > lim || s.q_row > lim || s.q_head > lim || s.out_row > lim)
+        return HSDPA_ERR_STRIDE;
+    if (s.q_head < s.head_dim || s.heads * s.q_head > s.q_row) return HSDPA_ERR_STRIDE;
+    if (s.heads * s.head_dim > s.out_row) return HSDPA_ERR_STRIDE;
+    if (s.kv_capacity == 0) return HSDPA_ERR_CAPACITY;
+    if (s.kv_capacity > (static_cast<uint64_t>(1) << 40) / s.head_dim) return HSDPA_ERR_CAPACITY;
+    if (s.kv_stride < s.kv_capacity * s.head_dim) return HSDPA_ERR_STRIDE;
+    // the kernels move 16-byte vectors
+    if (s.q_row % 8 || s.q_head % 8 || s.out_row % 8 || s.kv_stride % 8) return HSDPA_ERR_ALIGNMENT;
+    return HSDPA_OK;
+}
+
+// One architecture check per device, cached.
+std::mutex g_dev_mu;
+int g_dev_state[64];  // 0 unknown, 1 gfx950, 2 other
+
+hsdpa_status check_device()
+{
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return HSDPA_ERR_NO_DEVICE;
+    if (dev < 0 || dev >= 64) return HSDPA_ERR_NO_DEVICE;
+    std::lock_guard<std::mutex> lk(g_dev_mu);
+    if (g_dev_state[dev] == 0) {
+        hipDeviceProp_t p;
+        if (hipGetDeviceProperties(&p, dev) != hipSuccess) return HSDPA_ERR_NO_DEVICE;
+        g_dev_state[dev] = std::strncmp(p.gcnArchName, "gfx950", 6) == 0 ? 1 : 2;
+    }
+    return g_dev_state[dev] == 1 ? HSDPA_OK : HSDPA_ERR_NO_DEVICE;
+}
+
+}  // namespace
+
+extern "C" {
+
+hsdpa_status hsdpa_plan_create(const hsdpa_spec *spec, hsdpa_plan **out)
+{
+    if (!spec || !out) return HSDPA_ERR_NULL;
+    *out = nullptr;
+    const hsdpa_status st = check_spec(*spec);
+    if (st != HSDPA_OK) return st;
+    hsdpa_plan *p = new (std::nothrow) hsdpa_plan();
+    if (!p) return HSDPA_ERR_HIP;
+    p->spec = *spec;
+    const uint64_t d = spec->head_dim, g = spec->gqa, kvh = spec->heads / spec->gqa;
+    const uint64_t cap = spec->kv_capacity;
+    p->kv_heads = kvh;
+    p->dec_nwg = (cap + hsdpa::kDecodeKeysPerWG - 1) / hsdpa::kDecodeKeysPerWG;
+    p->dec_npad = p->dec_nwg * hsdpa::kDecodeKeysPerWG;
+    uint64_t off = 0;
+    p->off_scores = off;
+    off = align_up(off + kvh * g * p->dec_npad * 4, kAlign);
+    p->off_wgmax = off;
+    off = align_up(off + kvh * p->dec_nwg * g * 4, kAlign);
+    p->off_part_o = off;
+    off = align_up(off + kvh * p->dec_nwg * g * d * 4, kAlign);
+    p->off_part_l = off;
+    off = align_up(off + kvh * p->dec_nwg * g * 4, kAlign);
+    p->dec_bytes = off;
+    p->pre_ld = align_up(cap, hsdpa::kTransposeTile);
+    p->pre_bytes = align_up(kvh * d * p->pre_ld * 2, kAlign);
+    p->ws_bytes = p->dec_bytes > p->pre_bytes ? p->dec_bytes : p->pre_bytes;
+    *out = p;
+    return HSDPA_OK;
+}
+
+void hsdpa_plan_destroy(hsdpa_plan *plan) { delete plan; }
+
+uint64_t hsdpa_workspace_bytes(const hsdpa_plan *plan) { return plan ? plan->ws_bytes : 0; }
+
+hsdpa_status hsdpa_attention(const hsdpa_plan *plan, const hsdpa_call *call, void *stream)
+{
+    if (!plan || !call) return HSDPA_ERR_NULL;
+    const hsdpa_spec &s = plan->spec;
+    if (call->sink != 0.0f) return HSDPA_ERR_SINK_UNSUPPORTED;
+    if (call->rows == 0) return HSDPA_OK;  // the selector's empty call (attention.rs:129-130)
+    if (call->rows > s.kv_capacity || call->past > s.kv_capacity - call->rows) return HSDPA_ERR_CAPACITY;
+    if (!call->q || !call->keys || !call->values || !call->output || !call->workspace) return HSDPA_ERR_NULL;
+    if (!aligned16(call->q) || !aligned16(call->keys) || !aligned16(call->values) || !aligned16(call->output) ||
+        !aligned16(call->workspace))
+        return HSDPA_ERR_ALIGNMENT;
+    if (call->workspace_bytes < plan->ws_bytes) return HSDPA_ERR_WORKSPACE;
+    const hsdpa_status dev = check_device();
+    if (dev != HSDPA_OK) return dev;
+
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    char *ws = static_cast<char *>(call->workspace);
+    const uint64_t n = call->past + call->rows;
+    const int d = static_cast<int>(s.head_dim);
+    if (call->rows == 1 && s.gqa <= 32) {
+        hsdpa::DecodeArgs a{};
+        a.q = call->q;
+        a.k = call->keys;
+        a.v = call->values;
+        a.out = call->output;
+        a.scores = reinterpret_cast<float *>(ws + plan->off_scores);
+        a.wgmax = reinterpret_cast<float *>(ws + plan->off_wgmax);
+        a.part_o = reinterpret_cast<float *>(ws + plan->off_part_o);
+        a.part_l = reinterpret_cast<float *>(ws + plan->off_part_l);
+        a.n = n;
+        a.npad = plan->dec_npad;
+        a.kv_stride = s.kv_stride;
+        a.q_head = s.q_head;
+        a.g = static_cast<int>(s.gqa);
+        a.keys_qk = hsdpa::kDecodeKeysPerWG;
+        a.keys_pv = hsdpa::kDecodeKeysPerWG;
+        a.nwg_qk = static_cast<int>((n + a.keys_qk - 1) / a.keys_qk);
+        a.nwg_pv = static_cast<int>((n + a.keys_pv - 1) / a.keys_pv);
+        a.scale = call->scale;
+        const hipError_t e = hsdpa::launch_decode(a, d, static_cast<int>(plan->kv_heads), st);
+        return e == hipSuccess ? HSDPA_OK : HSDPA_ERR_HIP;
+    }
+    hsdpa::PrefillArgs a{};
+    a.q = call->q;
+    a.k = call->keys;
+    a.vt = reinterpret_cast<const uint16_t *>(ws);
+    a.out = call->output;
+    a.rows = call->rows;
+    a.past = call->past;
+    a.n = n;
+    a.q_row = s.q_row;
+    a.q_head = s.q_head;
+    a.out_row = s.out_row;
+    a.kv_stride = s.kv_stride;
+    a.vt_ld = align_up(n, hsdpa::kTransposeTile);
+    a.vt_stride = s.head_dim * a.vt_ld;
+    a.gqa = static_cast<int>(s.gqa);
+    a.scale = call->scale;
+    hsdpa::TransposeArgs t{};
+    t.v = call->values;
+    t.vt = reinterpret_cast<uint16_t *>(ws);
+    t.n = n;
+    t.kv_stride = s.kv_stride;
+    t.vt_ld = a.vt_ld;
+    t.vt_stride = a.vt_stride;
+    const hipError_t e = hsdpa::launch_prefill(a, t, d, static_cast<int>(s.heads), static_cast<int>(plan->kv_heads), st);
+    return e == hipSuccess ? HSDPA_OK : HSDPA_ERR_HIP;
+}
+
+const char *hsdpa_status_string(hsdpa_status status)
+{
+    switch (status) {
+    case HSDPA_OK: return "ok";
+    case HSDPA_ERR_EMPTY: return "empty shape (heads, gqa or head_dim is 0)";
+    case HSDPA_ERR_HEAD_DIM: return "head_dim out of domain (multiple of 32; 64, 128 or 256 on gfx950)";
+    case HSDPA_ERR_GQA: return "heads is not a multiple of gqa";
+    case HSDPA_ERR_STRIDE: return "invalid q/out/kv strides for this geometry";
+    case HSDPA_ERR_SINK_UNSUPPORTED: return "softmax sink is not supported";
+    case HSDPA_ERR_CAPACITY: return "past + rows exceeds the KV capacity";
+    case HSDPA_ERR_WORKSPACE: return "workspace missing or too small";
+    case HSDPA_ERR_ALIGNMENT: return "pointer or stride not 16-byte aligned";
+    case HSDPA_ERR_NULL: return "null pointer";
+    case HSDPA_ERR_HIP: return "HIP launch or runtime error";
+    case HSDPA_ERR_NO_DEVICE: return "no gfx950 device is current";
+    }
+    return "unknown status";
+}
+
+uint32_t hsdpa_version(void) { return 100; }
+
+}  // extern "C"

@@ -1,0 +1,59 @@
+// hsdpa_kernels.h — launch interface between the C ABI layer and the gfx950
+// kernels. Internal to libhsdpa.so.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace hsdpa {
+
+// Decode: one query row, g query heads per KV head, n visible keys.
+struct DecodeArgs {
+    const uint16_t *q;      // row 0; head h at q + h*q_head
+    const uint16_t *k;      // cache, head kvh at k + kvh*kv_stride
+    const uint16_t *v;
+    uint16_t *out;          // head h at out + h*head_dim
+    float *scores;          // [kv_heads][g][npad] scaled scores
+    float *wgmax;           // [kv_heads][nwg_qk][g] per-workgroup maxima
+    float *part_o;          // [kv_heads][nwg_pv][g][head_dim] unnormalised partial outputs
+    float *part_l;          // [kv_heads][nwg_pv][g] partial sums of exponentials
+    uint64_t n;             // visible keys (past + 1)
+    uint64_t npad;          // scores row length, a multiple of the key tile
+    uint64_t kv_stride;
+    uint64_t q_head;
+    int g;                  // query heads per KV head (<= 32)
+    int nwg_qk, nwg_pv;     // workgroups per KV head of the two passes
+    int keys_qk, keys_pv;   // keys per workgroup of the two passes
+    float scale;
+};
+
+// Causal prefill: `rows` query rows after `past` cached positions.
+struct PrefillArgs {
+    const uint16_t *q;
+    const uint16_t *k;
+    const uint16_t *vt;     // V transposed into the workspace: [kv_heads][head_dim][vt_ld]
+    uint16_t *out;
+    uint64_t rows, past, n; // n = past + rows
+    uint64_t q_row, q_head, out_row, kv_stride;
+    uint64_t vt_ld, vt_stride;
+    int gqa;
+    float scale;
+};
+
+struct TransposeArgs {
+    const uint16_t *v;
+    uint16_t *vt;
+    uint64_t n, kv_stride, vt_ld, vt_stride;
+};
+
+// Constants of the kernels the host needs to size grids and workspaces.
+constexpr int kKeyTile = 32;          // keys per MFMA key block
+constexpr int kDecodeKeysPerWG = 256; // keys per decode workgroup (4 waves x 2 tiles)
+constexpr int kTransposeTile = 32;
+
+bool head_dim_supported(int d);
+hipError_t launch_decode(const DecodeArgs &a, int head_dim, int kv_heads, hipStream_t s);
+hipError_t launch_prefill(const PrefillArgs &a, const TransposeArgs &t, int head_dim, int heads,
+                          int kv_heads, hipStream_t s);
+
+}  // namespace hsdpa

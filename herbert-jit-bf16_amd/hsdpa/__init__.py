@@ -1,0 +1,11 @@
+"""hsdpa: the MI355X (gfx950) attention step of herbert-jit-bf16 behind a C ABI.
+
+The compute path is libhsdpa.so (hand-written HIP kernels, include/hsdpa.h).
+This package holds its ctypes binding (binding.py), which mirrors the
+reference's AttentionSpec / AttentionCall records, and the seeded synthetic
+workloads (workloads.py) used by the tests and the benchmark.
+"""
+from . import workloads  # noqa: F401
+from .binding import (  # noqa: F401
+    HsdpaError, Plan, Spec, Call, STATUS, library, library_path, attention_torch,
+)

@@ -1,0 +1,131 @@
+"""ctypes binding of libhsdpa.so (include/hsdpa.h).
+
+The structures mirror the reference's per-layer geometry and per-call records
+(src/jit/execution/abi.rs:136-180); the status codes mirror its named
+refusals (Decline, src/jit/ir.rs:177-230). Device memory and streams come
+from PyTorch, as plumbing only: the arithmetic is the HIP kernels'. There is
+no fallback: if libhsdpa.so is missing or fails to load, every call raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_NAME = "libhsdpa.so"
+_lib = None
+
+STATUS = {
+    0: "HSDPA_OK", 1: "HSDPA_ERR_EMPTY", 2: "HSDPA_ERR_HEAD_DIM", 3: "HSDPA_ERR_GQA",
+    4: "HSDPA_ERR_STRIDE", 5: "HSDPA_ERR_SINK_UNSUPPORTED", 6: "HSDPA_ERR_CAPACITY",
+    7: "HSDPA_ERR_WORKSPACE", 8: "HSDPA_ERR_ALIGNMENT", 9: "HSDPA_ERR_NULL", 10: "HSDPA_ERR_HIP",
+    11: "HSDPA_ERR_NO_DEVICE",
+}
+EXPORTS = ["hsdpa_plan_create", "hsdpa_plan_destroy", "hsdpa_workspace_bytes", "hsdpa_attention",
+           "hsdpa_status_string", "hsdpa_version"]
+
+
+class HsdpaError(RuntimeError):
+    def __init__(self, code: int, what: str):
+        self.code = code
+        self.name = STATUS.get(code, f"status {code}")
+        super().__init__(f"{what}: {self.name} ({library().hsdpa_status_string(code).decode()})")
+
+
+class Spec(ctypes.Structure):
+    _fields_ = [("heads", ctypes.c_uint64), ("gqa", ctypes.c_uint64), ("head_dim", ctypes.c_uint64),
+                ("q_row", ctypes.c_uint64), ("q_head", ctypes.c_uint64), ("out_row", ctypes.c_uint64),
+                ("kv_capacity", ctypes.c_uint64), ("kv_stride", ctypes.c_uint64),
+                ("grouped", ctypes.c_uint32), ("sink", ctypes.c_uint32)]
+
+
+class Call(ctypes.Structure):
+    _fields_ = [("q", ctypes.c_void_p), ("keys", ctypes.c_void_p), ("values", ctypes.c_void_p),
+                ("output", ctypes.c_void_p), ("rows", ctypes.c_uint64), ("past", ctypes.c_uint64),
+                ("scale", ctypes.c_float), ("sink", ctypes.c_float), ("workspace", ctypes.c_void_p),
+                ("workspace_bytes", ctypes.c_uint64)]
+
+
+def library_path() -> str:
+    return os.path.join(_HERE, _LIB_NAME)
+
+
+def library():
+    """Load libhsdpa.so (raises OSError when it is not built)."""
+    global _lib
+    if _lib is None:
+        path = library_path()
+        if not os.path.exists(path):
+            raise OSError(f"{path} is not built: run herbert-jit-bf16_amd/build.py")
+        L = ctypes.CDLL(path)
+        L.hsdpa_plan_create.argtypes = [ctypes.POINTER(Spec), ctypes.POINTER(ctypes.c_void_p)]
+        L.hsdpa_plan_create.restype = ctypes.c_int
+        L.hsdpa_plan_destroy.argtypes = [ctypes.c_void_p]
+        L.hsdpa_plan_destroy.restype = None
+        L.hsdpa_workspace_bytes.argtypes = [ctypes.c_void_p]
+        L.hsdpa_workspace_bytes.restype = ctypes.c_uint64
+        L.hsdpa_attention.argtypes = [ctypes.c_void_p, ctypes.POINTER(Call), ctypes.c_void_p]
+        L.hsdpa_attention.restype = ctypes.c_int
+        L.hsdpa_status_string.argtypes = [ctypes.c_int]
+        L.hsdpa_status_string.restype = ctypes.c_char_p
+        L.hsdpa_version.restype = ctypes.c_uint32
+        _lib = L
+    return _lib
+
+
+class Plan:
+    """A validated per-layer geometry (hsdpa_plan_create). Mirrors the
+    reference's mount: AttentionSpec plus the cache reserve."""
+
+    def __init__(self, heads: int, gqa: int, head_dim: int, kv_capacity: int, q_row: int | None = None,
+                 q_head: int | None = None, out_row: int | None = None, kv_stride: int | None = None,
+                 grouped: bool = False, sink: bool = False):
+        self.spec = Spec(heads, gqa, head_dim,
+                         heads * head_dim if q_row is None else q_row,
+                         head_dim if q_head is None else q_head,
+                         heads * head_dim if out_row is None else out_row,
+                         kv_capacity, kv_capacity * head_dim if kv_stride is None else kv_stride,
+                         int(grouped), int(sink))
+        self._h = ctypes.c_void_p()
+        rc = library().hsdpa_plan_create(ctypes.byref(self.spec), ctypes.byref(self._h))
+        if rc != 0:
+            raise HsdpaError(rc, "hsdpa_plan_create")
+
+    @property
+    def handle(self):
+        return self._h
+
+    @property
+    def workspace_bytes(self) -> int:
+        return int(library().hsdpa_workspace_bytes(self._h))
+
+    def attention_raw(self, q: int, keys: int, values: int, output: int, rows: int, past: int, scale: float,
+                      workspace: int, workspace_bytes: int, stream: int = 0, sink: float = 0.0) -> None:
+        call = Call(q, keys, values, output, rows, past, scale, sink, workspace, workspace_bytes)
+        rc = library().hsdpa_attention(self._h, ctypes.byref(call), ctypes.c_void_p(stream))
+        if rc != 0:
+            raise HsdpaError(rc, "hsdpa_attention")
+
+    def close(self) -> None:
+        if self._h:
+            library().hsdpa_plan_destroy(self._h)
+            self._h = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def attention_torch(plan: Plan, q, k, v, out, rows: int, past: int, scale: float, workspace, stream=None) -> None:
+    """Enqueue the node on torch device tensors (uint16/int16/bfloat16 views of
+    bf16 data). `workspace` is a uint8 device tensor of plan.workspace_bytes."""
+    import torch
+
+    for t in (q, k, v, out, workspace):
+        if not t.is_cuda or not t.is_contiguous():
+            raise ValueError("tensors must be contiguous device tensors")
+    s = torch.cuda.current_stream() if stream is None else stream
+    plan.attention_raw(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), rows, past, scale,
+                       workspace.data_ptr(), workspace.numel() * workspace.element_size(), s.cuda_stream)

@@ -1,0 +1,46 @@
+"""GPU parity: libhsdpa.so (called through its C ABI) against the oracle, the
+CPU restatement of the reference's emitted SDPA, on identical seeded inputs."""
+import numpy as np
+import pytest
+
+import oracle
+from hsdpa import workloads as W
+from parity import assert_parity
+
+from gpu_util import run_hsdpa
+
+pytestmark = pytest.mark.gpu
+
+SMALL = [
+    # name, heads, kv_heads, head_dim, rows, past
+    ("decode_d256_n1", 8, 2, 256, 1, 0),
+    ("decode_d256_n37", 8, 2, 256, 1, 36),
+    ("decode_d128_n300", 16, 4, 128, 1, 299),
+    ("decode_d64_g1", 4, 4, 64, 1, 77),
+    ("prefill_d256_r2", 8, 2, 256, 2, 0),
+    ("prefill_d256_r19_p37", 8, 2, 256, 19, 37),
+    ("prefill_d128_r70_p5", 8, 8, 128, 70, 5),
+    ("prefill_d64_r33_p100_g2", 8, 4, 64, 33, 100),
+    ("prefill_d256_r129_p0_g3", 6, 2, 256, 129, 0),
+]
+
+
+@pytest.mark.parametrize("case", SMALL, ids=[c[0] for c in SMALL])
+def test_small_shapes(torch_cuda, case):
+    name, h, kvh, d, rows, past = case
+    w = W.make(name, heads=h, kv_heads=kvh, head_dim=d, rows=rows, past=past, seed=11)
+    print(f"case {name}", flush=True)
+    out = run_hsdpa(w)
+    ref = oracle.attention(w)
+    r = assert_parity(out, ref, w, name)
+    print(name, r, flush=True)
+
+
+@pytest.mark.parametrize("name", ["decode_1k", "prefill_512"])
+def test_configs_small(torch_cuda, name):
+    w = W.config(name, seed=1)
+    print(f"config {name}", flush=True)
+    out = run_hsdpa(w)
+    ref = oracle.attention(w)
+    r = assert_parity(out, ref, w, name)
+    print(name, r, flush=True)
