@@ -19,9 +19,7 @@ struct hsdpa_plan {
     uint64_t dec_npad;        // scores row length for a full cache
     uint64_t dec_nwg;         // workgroups per KV head for a full cache
     uint64_t off_scores, off_wgmax, off_part_o, off_part_l, dec_bytes;
-    // prefill workspace: V^T [kv_heads][head_dim][pre_ld] bf16
-    uint64_t pre_ld, pre_bytes;
-    uint64_t ws_bytes;
+    uint64_t ws_bytes;       // prefill needs no workspace
 };
 
 namespace {
@@ -87,8 +85,8 @@ hsdpa_status hsdpa_plan_create(const hsdpa_spec *spec, hsdpa_plan **out)
     const uint64_t d = spec->head_dim, g = spec->gqa, kvh = spec->heads / spec->gqa;
     const uint64_t cap = spec->kv_capacity;
     p->kv_heads = kvh;
-    p->dec_nwg = (cap + hsdpa::kDecodeKeysPerWG - 1) / hsdpa::kDecodeKeysPerWG;
-    p->dec_npad = p->dec_nwg * hsdpa::kDecodeKeysPerWG;
+    p->dec_nwg = (cap + hsdpa::kDecodeKeysQK - 1) / hsdpa::kDecodeKeysQK;  // the larger of the two counts
+    p->dec_npad = align_up(cap, hsdpa::kDecodeKeysPV);
     uint64_t off = 0;
     p->off_scores = off;
     off = align_up(off + kvh * g * p->dec_npad * 4, kAlign);
@@ -99,9 +97,7 @@ hsdpa_status hsdpa_plan_create(const hsdpa_spec *spec, hsdpa_plan **out)
     p->off_part_l = off;
     off = align_up(off + kvh * p->dec_nwg * g * 4, kAlign);
     p->dec_bytes = off;
-    p->pre_ld = align_up(cap, hsdpa::kTransposeTile);
-    p->pre_bytes = align_up(kvh * d * p->pre_ld * 2, kAlign);
-    p->ws_bytes = p->dec_bytes > p->pre_bytes ? p->dec_bytes : p->pre_bytes;
+    p->ws_bytes = p->dec_bytes;
     *out = p;
     return HSDPA_OK;
 }
@@ -129,7 +125,10 @@ hsdpa_status hsdpa_attention(const hsdpa_plan *plan, const hsdpa_call *call, voi
     char *ws = static_cast<char *>(call->workspace);
     const uint64_t n = call->past + call->rows;
     const int d = static_cast<int>(s.head_dim);
-    if (call->rows == 1 && s.gqa <= 32) {
+    // decode kernels: one query row and at most kDecodeMaxGroup query heads per
+    // KV head (their LDS holds the group's exponentials); otherwise the causal
+    // kernel serves the row.
+    if (call->rows == 1 && s.gqa <= static_cast<uint64_t>(hsdpa::kDecodeMaxGroup)) {
         hsdpa::DecodeArgs a{};
         a.q = call->q;
         a.k = call->keys;
@@ -144,8 +143,8 @@ hsdpa_status hsdpa_attention(const hsdpa_plan *plan, const hsdpa_call *call, voi
         a.kv_stride = s.kv_stride;
         a.q_head = s.q_head;
         a.g = static_cast<int>(s.gqa);
-        a.keys_qk = hsdpa::kDecodeKeysPerWG;
-        a.keys_pv = hsdpa::kDecodeKeysPerWG;
+        a.keys_qk = hsdpa::kDecodeKeysQK;
+        a.keys_pv = hsdpa::kDecodeKeysPV;
         a.nwg_qk = static_cast<int>((n + a.keys_qk - 1) / a.keys_qk);
         a.nwg_pv = static_cast<int>((n + a.keys_pv - 1) / a.keys_pv);
         a.scale = call->scale;
@@ -155,7 +154,7 @@ hsdpa_status hsdpa_attention(const hsdpa_plan *plan, const hsdpa_call *call, voi
     hsdpa::PrefillArgs a{};
     a.q = call->q;
     a.k = call->keys;
-    a.vt = reinterpret_cast<const uint16_t *>(ws);
+    a.v = call->values;
     a.out = call->output;
     a.rows = call->rows;
     a.past = call->past;
@@ -164,18 +163,9 @@ hsdpa_status hsdpa_attention(const hsdpa_plan *plan, const hsdpa_call *call, voi
     a.q_head = s.q_head;
     a.out_row = s.out_row;
     a.kv_stride = s.kv_stride;
-    a.vt_ld = align_up(n, hsdpa::kTransposeTile);
-    a.vt_stride = s.head_dim * a.vt_ld;
     a.gqa = static_cast<int>(s.gqa);
     a.scale = call->scale;
-    hsdpa::TransposeArgs t{};
-    t.v = call->values;
-    t.vt = reinterpret_cast<uint16_t *>(ws);
-    t.n = n;
-    t.kv_stride = s.kv_stride;
-    t.vt_ld = a.vt_ld;
-    t.vt_stride = a.vt_stride;
-    const hipError_t e = hsdpa::launch_prefill(a, t, d, static_cast<int>(s.heads), static_cast<int>(plan->kv_heads), st);
+    const hipError_t e = hsdpa::launch_prefill(a, d, static_cast<int>(s.heads), st);
     return e == hipSuccess ? HSDPA_OK : HSDPA_ERR_HIP;
 }
 

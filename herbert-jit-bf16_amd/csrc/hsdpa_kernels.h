@@ -14,14 +14,14 @@ struct DecodeArgs {
     const uint16_t *v;
     uint16_t *out;          // head h at out + h*head_dim
     float *scores;          // [kv_heads][g][npad] scaled scores
-    float *wgmax;           // [kv_heads][nwg_qk][g] per-workgroup maxima
+    float *wgmax;           // [kv_heads][g][nwg_qk] per-workgroup maxima
     float *part_o;          // [kv_heads][nwg_pv][g][head_dim] unnormalised partial outputs
     float *part_l;          // [kv_heads][nwg_pv][g] partial sums of exponentials
     uint64_t n;             // visible keys (past + 1)
     uint64_t npad;          // scores row length, a multiple of the key tile
     uint64_t kv_stride;
     uint64_t q_head;
-    int g;                  // query heads per KV head (<= 32)
+    int g;                  // query heads per KV head (<= kDecodeMaxGroup)
     int nwg_qk, nwg_pv;     // workgroups per KV head of the two passes
     int keys_qk, keys_pv;   // keys per workgroup of the two passes
     float scale;
@@ -31,29 +31,22 @@ struct DecodeArgs {
 struct PrefillArgs {
     const uint16_t *q;
     const uint16_t *k;
-    const uint16_t *vt;     // V transposed into the workspace: [kv_heads][head_dim][vt_ld]
+    const uint16_t *v;
     uint16_t *out;
     uint64_t rows, past, n; // n = past + rows
     uint64_t q_row, q_head, out_row, kv_stride;
-    uint64_t vt_ld, vt_stride;
     int gqa;
     float scale;
 };
 
-struct TransposeArgs {
-    const uint16_t *v;
-    uint16_t *vt;
-    uint64_t n, kv_stride, vt_ld, vt_stride;
-};
-
 // Constants of the kernels the host needs to size grids and workspaces.
 constexpr int kKeyTile = 32;          // keys per MFMA key block
-constexpr int kDecodeKeysPerWG = 256; // keys per decode workgroup (4 waves x 2 tiles)
-constexpr int kTransposeTile = 32;
+constexpr int kDecodeKeysQK = 128;    // keys per decode pass-1 workgroup (4 waves x 1 tile)
+constexpr int kDecodeKeysPV = 256;    // keys per decode pass-2 workgroup (8 waves x 1 tile)
+constexpr int kDecodeMaxGroup = 16;   // query heads per KV head the decode kernels take
 
 bool head_dim_supported(int d);
 hipError_t launch_decode(const DecodeArgs &a, int head_dim, int kv_heads, hipStream_t s);
-hipError_t launch_prefill(const PrefillArgs &a, const TransposeArgs &t, int head_dim, int heads,
-                          int kv_heads, hipStream_t s);
+hipError_t launch_prefill(const PrefillArgs &a, int head_dim, int heads, hipStream_t s);
 
 }  // namespace hsdpa

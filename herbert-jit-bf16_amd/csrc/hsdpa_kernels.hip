@@ -24,7 +24,13 @@
 // the P.V MFMA (O^T = V^T . P^T) with no data movement. The A-operand rows
 // are loaded as K row swap23(i) (bits 2 and 3 of the row swapped), which
 // makes score register r of lane group g hold key 16(r/8) + 8g + r%8: eight
-// consecutive keys per P.V k-block, read from V^T as one 16-byte LDS load.
+// consecutive keys per P.V k-block.
+//
+// V stays row-major in LDS; its V^T operands come from the gfx950 transpose
+// read ds_read_b64_tr_b16. In each 16-lane group, lane j supplies the address
+// of four consecutive b16 and lane i receives element i%4 of the chunks of
+// lanes i/4 + 4k, k = 0..3. Pointing lane j at V[base + j/4][d0 + 4(j%4)]
+// hands lane i the four keys base..base+3 of dimension d0 + i.
 
 #include "hsdpa_kernels.h"
 
@@ -99,146 +105,220 @@ __device__ __forceinline__ int swap23(int i) { return (i & ~12) | ((i & 4) << 1)
 // Key offset inside a 32-key tile of score register r for lane group g.
 __device__ __forceinline__ int key_of(int r, int g) { return 16 * (r >> 3) + 8 * g + (r & 7); }
 
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ u32x2 tr_read(const uint16_t *p)
+{
+    const v4i16 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4i16 *)(p));
+    return __builtin_bit_cast(u32x2, r);
+}
+
+// The V^T A operand of v_mfma_f32_32x32x16_bf16 for dimensions [d0, d0+32)
+// and keys [kb + 8g, +8) (g = lane / 32), from a row-major V tile in LDS with
+// row stride vs elements: two transpose reads of four keys each.
+__device__ __forceinline__ u32x4 vt_operand(const uint16_t *vtile, int vs, int kb, int d0, int l)
+{
+    const int j = l & 15, G = l >> 4;
+    const int key = kb + 8 * (G >> 1) + (j >> 2);
+    const int dim = d0 + 16 * (G & 1) + 4 * (j & 3);
+    const u32x2 a = tr_read(vtile + key * vs + dim);
+    const u32x2 b = tr_read(vtile + (key + 4) * vs + dim);
+    return u32x4{a.x, a.y, b.x, b.y};
+}
+
+// A 32-key tile of K or V is 32 * D/8 chunks of 16 bytes. Lanes (or threads)
+// take consecutive chunks so every load instruction reads whole rows.
+template <int D, int THREADS> struct Tile {
+    static constexpr int kChunks = kKeyTile * (D / 8);
+    static constexpr int kPer = (kChunks + THREADS - 1) / THREADS;
+};
+
+template <int D, int THREADS>
+__device__ __forceinline__ void tile_gload(const uint16_t *base, uint64_t t0, uint64_t lim, int tid,
+                                           u32x4 (&r)[Tile<D, THREADS>::kPer])
+{
+#pragma unroll
+    for (int i = 0; i < Tile<D, THREADS>::kPer; i++) {
+        const int c = tid + THREADS * i, key = c / (D / 8), dc = c % (D / 8);
+        const uint64_t gk = t0 + key;
+        r[i] = (c < Tile<D, THREADS>::kChunks && gk < lim) ? load16(base + gk * D + 8 * dc) : u32x4{0, 0, 0, 0};
+    }
+}
+
+template <int D, int THREADS>
+__device__ __forceinline__ void tile_lstore(uint16_t *tile, int tid, const u32x4 (&r)[Tile<D, THREADS>::kPer])
+{
+    constexpr int S = D + 16;
+#pragma unroll
+    for (int i = 0; i < Tile<D, THREADS>::kPer; i++) {
+        const int c = tid + THREADS * i, key = c / (D / 8), dc = c % (D / 8);
+        if (c < Tile<D, THREADS>::kChunks) store16(tile + key * S + 8 * dc, r[i]);
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Decode pass 1: scores and per-workgroup maxima.
-// grid (nwg_qk, kv_heads), 256 threads. Workgroup wg takes keys
-// [wg*keys_qk, +keys_qk); wave w takes the 32-key tiles w, w+4, ...
-// Q^T columns are the g query heads of the KV head (padded to 32).
+// grid (nwg_qk, kv_heads), 256 threads, keys_qk = 128: wave w stages the
+// 32-key tile j0 + 32w through its own LDS rows with whole-row loads, then
+// reads the MFMA A operands from there. Q^T columns are the g query heads of
+// the KV head (padded to 32).
 // ---------------------------------------------------------------------------
 template <int D>
 __global__ __launch_bounds__(256) void decode_qk(DecodeArgs a)
 {
+    constexpr int S = D + 16;
+    __shared__ __attribute__((aligned(16))) uint16_t kt[4][kKeyTile * S];
     __shared__ float red[4][32];
     const int kvh = blockIdx.y, wg = blockIdx.x;
     const int wave = threadIdx.x >> 6, l = threadIdx.x & 63, col = l & 31, grp = l >> 5;
+    const uint64_t j0 = static_cast<uint64_t>(wg) * a.keys_qk;
+    const uint64_t j1 = j0 + a.keys_qk < a.n ? j0 + a.keys_qk : a.n;
+    const uint64_t t0 = j0 + kKeyTile * wave;
+    const uint16_t *kbase = a.k + static_cast<uint64_t>(kvh) * a.kv_stride;
+    u32x4 kr[Tile<D, 64>::kPer];
+    tile_gload<D, 64>(kbase, t0, j1, l, kr);
     const bool colv = col < a.g;
     u32x4 qb[D / 16];
     const uint16_t *qp = a.q + static_cast<uint64_t>(kvh * a.g + (colv ? col : 0)) * a.q_head;
 #pragma unroll
     for (int ks = 0; ks < D / 16; ks++) qb[ks] = colv ? load16(qp + 16 * ks + 8 * grp) : u32x4{0, 0, 0, 0};
-    const uint16_t *kbase = a.k + static_cast<uint64_t>(kvh) * a.kv_stride;
-    const uint64_t j0 = static_cast<uint64_t>(wg) * a.keys_qk;
-    const uint64_t j1 = j0 + a.keys_qk < a.n ? j0 + a.keys_qk : a.n;
+    uint16_t *my = kt[wave];
+    tile_lstore<D, 64>(my, l, kr);
+    __syncthreads();
+    f32x16 acc0 = {}, acc1 = {};
+    const int arow = swap23(col);
+#pragma unroll
+    for (int ks = 0; ks < D / 16; ks += 2) {
+        acc0 = mfma(load16(my + arow * S + 16 * ks + 8 * grp), qb[ks], acc0);
+        acc1 = mfma(load16(my + arow * S + 16 * (ks + 1) + 8 * grp), qb[ks + 1], acc1);
+    }
     float m = kNegInf;
-    for (uint64_t t0 = j0 + kKeyTile * wave; t0 < j1; t0 += 4 * kKeyTile) {
-        const uint64_t key = t0 + swap23(col);
-        const bool kv = key < a.n;
-        const uint16_t *kp = kbase + (kv ? key : 0) * D;
-        f32x16 acc = {};
+    if (colv && t0 < j1) {
+        float *sp = a.scores + static_cast<uint64_t>(kvh * a.g + col) * a.npad + t0 + 8 * grp;
 #pragma unroll
-        for (int ks = 0; ks < D / 16; ks++) {
-            const u32x4 av = kv ? load16(kp + 16 * ks + 8 * grp) : u32x4{0, 0, 0, 0};
-            acc = mfma(av, qb[ks], acc);
-        }
-        if (colv) {
-            float *sp = a.scores + static_cast<uint64_t>(kvh * a.g + col) * a.npad + t0 + 8 * grp;
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const uint64_t kk = t0 + key_of(r, grp);
-                const float s = acc[r] * a.scale;
-                const bool valid = kk < a.n;
-                sp[16 * (r >> 3) + (r & 7)] = valid ? s : kNegInf;
-                if (valid) m = s > m ? s : m;
-            }
+        for (int r = 0; r < 16; r++) {
+            const uint64_t kk = t0 + key_of(r, grp);
+            const float s = (acc0[r] + acc1[r]) * a.scale;
+            const bool valid = kk < j1;
+            sp[16 * (r >> 3) + (r & 7)] = valid ? s : kNegInf;
+            if (valid) m = s > m ? s : m;
         }
     }
     const float mo = __shfl_xor(m, 32);
     m = mo > m ? mo : m;
     if (grp == 0) red[wave][col] = m;
     __syncthreads();
-    if (threadIdx.x < 32 && threadIdx.x < a.g) {
+    if (threadIdx.x < 32 && static_cast<int>(threadIdx.x) < a.g) {
         float r = red[0][threadIdx.x];
 #pragma unroll
         for (int w = 1; w < 4; w++) r = red[w][threadIdx.x] > r ? red[w][threadIdx.x] : r;
-        a.wgmax[(static_cast<uint64_t>(kvh) * a.nwg_qk + wg) * a.g + threadIdx.x] = r;
+        a.wgmax[(static_cast<uint64_t>(kvh) * a.g + threadIdx.x) * a.nwg_qk + wg] = r;
     }
 }
 
 // ---------------------------------------------------------------------------
 // Decode pass 2: exponentials at the exact maximum and P.V partial sums.
-// grid (nwg_pv, kv_heads), 256 threads, keys_pv = 256 keys per workgroup, two
-// 32-key tiles per wave. V tiles are transposed through wave-private LDS.
+// grid (nwg_pv, kv_heads), 512 threads, keys_pv = 256: wave w owns the 32-key
+// tile j0 + 32w. Its V rows are loaded first (whole rows), the exact maximum
+// is reduced from the pass-1 maxima, the workgroup's g x 256 exponentials are
+// computed once in a dense layout in LDS, then each wave runs the P.V MFMAs
+// with V^T operands from transpose reads of its row-major tile.
+// Dynamic LDS: 8 V tiles, then e[g][256 + 4] f32.
 // ---------------------------------------------------------------------------
+constexpr int kPvWaves = 8;
+
 template <int D>
-__global__ __launch_bounds__(256) void decode_pv(DecodeArgs a)
+__global__ __launch_bounds__(512, 2) void decode_pv(DecodeArgs a)
 {
-    constexpr int VP = kKeyTile + 8;                  // padded V^T row, elements
-    __shared__ __attribute__((aligned(16))) uint16_t vt[4][D * VP];
+    constexpr int S = D + 16;
+    constexpr int KEYS = kPvWaves * kKeyTile;         // 256
+    constexpr int ES = KEYS + 4;                      // e row stride, floats
+    extern __shared__ __attribute__((aligned(16))) uint16_t dyn[];
+    uint16_t *vtl = dyn;                               // [8][32 * S]
+    float *ep = reinterpret_cast<float *>(dyn + kPvWaves * kKeyTile * S);   // [g][ES]
+    __shared__ float mred[512];
     __shared__ float smax[32];
-    __shared__ float lred[4][32];
-    const int kvh = blockIdx.y, wg = blockIdx.x;
-    const int wave = threadIdx.x >> 6, l = threadIdx.x & 63, col = l & 31, grp = l >> 5;
-    if (threadIdx.x < 32) {
-        float m = kNegInf;
-        if (static_cast<int>(threadIdx.x) < a.g)
-            for (int w = 0; w < a.nwg_qk; w++) {
-                const float x = a.wgmax[(static_cast<uint64_t>(kvh) * a.nwg_qk + w) * a.g + threadIdx.x];
-                m = x > m ? x : m;
-            }
-        smax[threadIdx.x] = m;
-    }
-    __syncthreads();
-    const bool colv = col < a.g;
-    const float M = smax[col];
+    __shared__ float lred[kPvWaves][32];
+    const int kvh = blockIdx.y, wg = blockIdx.x, tid = threadIdx.x;
+    const int wave = tid >> 6, l = tid & 63, col = l & 31, grp = l >> 5;
+    const uint64_t j0 = static_cast<uint64_t>(wg) * KEYS;
+    const uint64_t j1 = j0 + KEYS < a.n ? j0 + KEYS : a.n;
+    const uint64_t t0 = j0 + kKeyTile * wave;
     const uint16_t *vbase = a.v + static_cast<uint64_t>(kvh) * a.kv_stride;
-    const float *srow = a.scores + static_cast<uint64_t>(kvh * a.g + (colv ? col : 0)) * a.npad;
-    uint16_t *my = vt[wave];
+    u32x4 vr[Tile<D, 64>::kPer];
+    tile_gload<D, 64>(vbase, t0, j1, l, vr);
+
+    // exact maximum per query head, from the pass-1 workgroup maxima
+    {
+        const int tph = 512 / a.g;
+        const int jh = tid / tph, u = tid % tph;
+        float m = kNegInf;
+        if (jh < a.g) {
+            const float *src = a.wgmax + (static_cast<uint64_t>(kvh) * a.g + jh) * a.nwg_qk;
+            for (int w = u; w < a.nwg_qk; w += tph) m = src[w] > m ? src[w] : m;
+        }
+        mred[tid] = m;
+        __syncthreads();
+        if (tid < 32) {
+            float r = kNegInf;
+            if (tid < a.g)
+                for (int i = 0; i < tph; i++) {
+                    const float x = mred[tid * tph + i];
+                    r = x > r ? x : r;
+                }
+            smax[tid] = r;
+        }
+        __syncthreads();
+    }
+    // dense exponentials: thread t owns key j0 + t % 256 for heads t/256, +2, ...
+    {
+        const int key = tid % KEYS;
+        const uint64_t gk = j0 + key;
+        for (int h = tid / KEYS; h < a.g; h += 512 / KEYS) {
+            const float *srow = a.scores + static_cast<uint64_t>(kvh * a.g + h) * a.npad;
+            ep[h * ES + key] = gk < j1 ? exp_poly(srow[gk] - smax[h]) : 0.0f;
+        }
+    }
+    uint16_t *my = vtl + wave * (kKeyTile * S);
+    tile_lstore<D, 64>(my, l, vr);
+    __syncthreads();
+
+    const bool colv = col < a.g;
+    float lsum = 0.0f;
+    u32x4 hi[2], lo[2];
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        float ev[8];
+        if (colv) {
+            const float *e = ep + col * ES + kKeyTile * wave + 16 * h + 8 * grp;
+#pragma unroll
+            for (int s2 = 0; s2 < 8; s2++) ev[s2] = e[s2];
+        } else {
+#pragma unroll
+            for (int s2 = 0; s2 < 8; s2++) ev[s2] = 0.0f;
+        }
+#pragma unroll
+        for (int s2 = 0; s2 < 8; s2++) lsum += ev[s2];
+        split_pack(ev, hi[h], lo[h]);
+    }
     f32x16 o[D / 32];
 #pragma unroll
     for (int dt = 0; dt < D / 32; dt++) o[dt] = f32x16{};
-    float lsum = 0.0f;
-    const uint64_t j0 = static_cast<uint64_t>(wg) * a.keys_pv;
-    const uint64_t j1 = j0 + a.keys_pv < a.n ? j0 + a.keys_pv : a.n;
-    for (int it = 0; it < a.keys_pv / (4 * kKeyTile); it++) {
-        const uint64_t t0 = j0 + kKeyTile * (wave + 4 * it);
-        // V tile -> registers (8 keys x 8 dims per task), transpose, -> LDS [dim][key]
-        for (int task = l; task < 4 * (D / 8); task += 64) {
-            const int b8 = task / (D / 8), dc = task % (D / 8);
-            u32x4 r[8];
 #pragma unroll
-            for (int i = 0; i < 8; i++) {
-                const uint64_t key = t0 + 8 * b8 + i;
-                r[i] = key < j1 ? load16(vbase + key * D + 8 * dc) : u32x4{0, 0, 0, 0};
-            }
+    for (int h = 0; h < 2; h++)
 #pragma unroll
-            for (int e = 0; e < 8; e++) {
-                const int sh = 16 * (e & 1);
-                u32x4 w;
-#pragma unroll
-                for (int s = 0; s < 4; s++)
-                    w[s] = ((r[2 * s][e >> 1] >> sh) & 0xFFFFu) | (((r[2 * s + 1][e >> 1] >> sh) & 0xFFFFu) << 16);
-                store16(my + (8 * dc + e) * VP + 8 * b8, w);
-            }
+        for (int dt = 0; dt < D / 32; dt++) {
+            const u32x4 av = vt_operand(my, S, 16 * h, 32 * dt, l);
+            o[dt] = mfma(av, hi[h], o[dt]);
+            o[dt] = mfma(av, lo[h], o[dt]);
         }
-        // exponentials for this lane's query head and keys
-        float ev[16];
-#pragma unroll
-        for (int r = 0; r < 16; r++) {
-            const uint64_t kk = t0 + key_of(r, grp);
-            const bool valid = colv && kk < j1;
-            ev[r] = valid ? exp_poly(srow[kk] - M) : 0.0f;
-            lsum += ev[r];
-        }
-        u32x4 hi[2], lo[2];
-        split_pack(ev, hi[0], lo[0]);
-        split_pack(ev + 8, hi[1], lo[1]);
-        __syncthreads();  // the trip count is the same for every wave
-#pragma unroll
-        for (int h = 0; h < 2; h++)
-#pragma unroll
-            for (int dt = 0; dt < D / 32; dt++) {
-                const u32x4 av = load16(my + (32 * dt + col) * VP + 16 * h + 8 * grp);
-                o[dt] = mfma(av, hi[h], o[dt]);
-                o[dt] = mfma(av, lo[h], o[dt]);
-            }
-        __syncthreads();
-    }
     lsum += __shfl_xor(lsum, 32);
     if (grp == 0) lred[wave][col] = lsum;
-    // cross-wave reduction of O^T (valid columns only) through the V^T buffer
-    float *red = reinterpret_cast<float *>(&vt[0][0]);
+    // cross-wave reduction of O^T (valid columns only) through the V tiles
+    float *red = reinterpret_cast<float *>(vtl);
     const int slab = a.g * D;                          // floats per wave
-    for (int step = 2; step >= 1; step >>= 1) {
+    for (int step = kPvWaves / 2; step >= 1; step >>= 1) {
         __syncthreads();
         if (wave >= step && wave < 2 * step && colv) {
             float *dst = red + (wave - step) * slab + col * D;
@@ -266,69 +346,71 @@ __global__ __launch_bounds__(256) void decode_pv(DecodeArgs a)
                 float4 v4 = {o[dt][4 * c], o[dt][4 * c + 1], o[dt][4 * c + 2], o[dt][4 * c + 3]};
                 *reinterpret_cast<float4 *>(dst + 32 * dt + 8 * c + 4 * grp) = v4;
             }
-        if (grp == 0) a.part_l[part] = lred[0][col] + lred[1][col] + lred[2][col] + lred[3][col];
+        if (grp == 0) {
+            float L = 0.0f;
+#pragma unroll
+            for (int w = 0; w < kPvWaves; w++) L += lred[w][col];
+            a.part_l[part] = L;
+        }
     }
 }
 
+// Dynamic LDS of decode_pv: at D = 256 and g = 16, 139 264 + 16 640 bytes,
+// plus 3 200 static, within the 160 KiB of a gfx950 workgroup.
+template <int D> constexpr size_t decode_pv_lds(int g)
+{
+    return static_cast<size_t>(kPvWaves) * kKeyTile * (D + 16) * 2 + static_cast<size_t>(g) * (kPvWaves * kKeyTile + 4) * 4;
+}
+
 // ---------------------------------------------------------------------------
-// Decode pass 3: out[h] = bf16(sum_w O_w / sum_w l_w). grid (heads), D threads.
+// Decode pass 3: out[h] = bf16(sum_w O_w / sum_w l_w).
+// grid (heads, D/64), 256 threads: 64 dimensions x 4 interleaved partial sets,
+// summed in a fixed order (deterministic).
 // ---------------------------------------------------------------------------
 template <int D>
 __global__ __launch_bounds__(256) void decode_combine(DecodeArgs a)
 {
-    const int h = blockIdx.x, kvh = h / a.g, jh = h % a.g, t = threadIdx.x;
+    __shared__ float ored[4][64];
+    __shared__ float lred[4];
+    const int h = blockIdx.x, kvh = h / a.g, jh = h % a.g;
+    const int t = threadIdx.x & 63, sub = threadIdx.x >> 6, dim = blockIdx.y * 64 + t;
     float o = 0.0f, L = 0.0f;
-    for (int w = 0; w < a.nwg_pv; w++) {
-        const uint64_t part = (static_cast<uint64_t>(kvh) * a.nwg_pv + w) * a.g + jh;
-        o += a.part_o[part * D + t];
+    const uint64_t base = static_cast<uint64_t>(kvh) * a.nwg_pv * a.g + jh;
+#pragma unroll 8
+    for (int w = sub; w < a.nwg_pv; w += 4) {
+        const uint64_t part = base + static_cast<uint64_t>(w) * a.g;
+        o += a.part_o[part * D + dim];
         L += a.part_l[part];
     }
-    a.out[static_cast<uint64_t>(h) * D + t] = static_cast<uint16_t>(cvt_out(o / L));
-}
-
-// ---------------------------------------------------------------------------
-// Prefill step 1: V^T into the workspace, zero beyond n up to vt_ld.
-// grid (vt_ld/32, D/32, kv_heads), 256 threads, 32x32 tiles through LDS.
-// ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void transpose_v(TransposeArgs a, int D)
-{
-    __shared__ uint16_t tile[32][33];
-    const uint64_t p0 = static_cast<uint64_t>(blockIdx.x) * 32;
-    const int d0 = blockIdx.y * 32, kvh = blockIdx.z;
-    const uint16_t *vb = a.v + static_cast<uint64_t>(kvh) * a.kv_stride;
-    uint16_t *tb = a.vt + static_cast<uint64_t>(kvh) * a.vt_stride;
-    const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int pr = ty + 8 * i;
-        const uint64_t p = p0 + pr;
-        tile[pr][tx] = p < a.n ? vb[p * D + d0 + tx] : static_cast<uint16_t>(0);
-    }
+    ored[sub][t] = o;
+    if (t == 0) lred[sub] = L;
     __syncthreads();
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int dr = ty + 8 * i;
-        tb[static_cast<uint64_t>(d0 + dr) * a.vt_ld + p0 + tx] = tile[tx][dr];
+    if (sub == 0) {
+        const float os = (ored[0][t] + ored[1][t]) + (ored[2][t] + ored[3][t]);
+        const float ls = (lred[0] + lred[1]) + (lred[2] + lred[3]);
+        a.out[static_cast<uint64_t>(h) * D + dim] = static_cast<uint16_t>(cvt_out(os / ls));
     }
 }
 
 // ---------------------------------------------------------------------------
-// Prefill step 2: the causal attention of a chunk, two passes over the keys
-// in one workgroup: the exact row maxima, then exponentials and P.V.
+// Prefill: the causal attention of a chunk, two passes over the keys in one
+// workgroup: the exact row maxima, then exponentials and P.V.
 // grid (row groups, heads/HPW), 256 threads. Wave w serves query head
 // blockIdx.y*HPW + w%HPW and rows [r0 + 32*(w/HPW), +32), r0 the group's
 // first row; the HPW heads of a group share one KV head, so all four waves
-// read the same K and V^T tiles from LDS.
+// read the same K and V tiles from LDS. Tiles are double-buffered: the global
+// loads of tile t+1 are in flight while tile t is computed.
 // ---------------------------------------------------------------------------
 template <int D, int HPW>
-__global__ __launch_bounds__(256, 2) void prefill_attn(PrefillArgs a)
+__global__ __launch_bounds__(256, 1) void prefill_attn(PrefillArgs a)
 {
     constexpr int RB = 4 / HPW;
-    constexpr int KP = D + 8;
-    constexpr int VP = kKeyTile + 8;
-    __shared__ __attribute__((aligned(16))) uint16_t ks[kKeyTile * KP];
-    __shared__ __attribute__((aligned(16))) uint16_t vs[D * VP];
-    const int wave = threadIdx.x >> 6, l = threadIdx.x & 63, col = l & 31, grp = l >> 5;
+    constexpr int S = D + 16;
+    constexpr int TE = kKeyTile * S;
+    __shared__ __attribute__((aligned(16))) uint16_t kb[2][TE];
+    __shared__ __attribute__((aligned(16))) uint16_t vb[2][TE];
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6, l = tid & 63, col = l & 31, grp = l >> 5;
     const int head = blockIdx.y * HPW + (wave % HPW);
     const int kvh = head / a.gqa;
     const uint64_t rgroup = gridDim.x - 1 - blockIdx.x;       // heaviest rows first
@@ -342,43 +424,39 @@ __global__ __launch_bounds__(256, 2) void prefill_attn(PrefillArgs a)
     const int ntiles = static_cast<int>((wg_kend + kKeyTile - 1) / kKeyTile);
     const uint64_t lim = a.past + row;                         // last visible key of this row
 
+    const uint16_t *kg = a.k + static_cast<uint64_t>(kvh) * a.kv_stride;
+    const uint16_t *vg = a.v + static_cast<uint64_t>(kvh) * a.kv_stride;
+    u32x4 kr[Tile<D, 256>::kPer], vr[Tile<D, 256>::kPer];
+    tile_gload<D, 256>(kg, 0, a.n, tid, kr);
+
     u32x4 qb[D / 16];
     const uint16_t *qp = a.q + (rowv ? row : 0) * a.q_row + static_cast<uint64_t>(head) * a.q_head;
 #pragma unroll
-    for (int ks_ = 0; ks_ < D / 16; ks_++) qb[ks_] = rowv ? load16(qp + 16 * ks_ + 8 * grp) : u32x4{0, 0, 0, 0};
-    const uint16_t *kg = a.k + static_cast<uint64_t>(kvh) * a.kv_stride;
-    const uint16_t *vg = a.vt + static_cast<uint64_t>(kvh) * a.vt_stride;
+    for (int s = 0; s < D / 16; s++) qb[s] = rowv ? load16(qp + 16 * s + 8 * grp) : u32x4{0, 0, 0, 0};
     const int arow = swap23(col);
-
-    auto load_k = [&](uint64_t t0) {
-        for (int c = threadIdx.x; c < kKeyTile * (D / 8); c += 256) {
-            const int key = c / (D / 8), dc = c % (D / 8);
-            const uint64_t gk = t0 + key;
-            store16(ks + key * KP + 8 * dc, gk < a.n ? load16(kg + gk * D + 8 * dc) : u32x4{0, 0, 0, 0});
-        }
-    };
-    auto load_v = [&](uint64_t t0) {
-        for (int c = threadIdx.x; c < D * (kKeyTile / 8); c += 256) {
-            const int dim = c / (kKeyTile / 8), kc = c % (kKeyTile / 8);
-            store16(vs + dim * VP + 8 * kc, load16(vg + static_cast<uint64_t>(dim) * a.vt_ld + t0 + 8 * kc));
-        }
-    };
-    auto qk = [&]() {
-        f32x16 acc = {};
+    auto qk = [&](const uint16_t *kt) {
+        f32x16 acc0 = {}, acc1 = {};
 #pragma unroll
-        for (int s = 0; s < D / 16; s++) acc = mfma(load16(ks + arow * KP + 16 * s + 8 * grp), qb[s], acc);
-        return acc;
+        for (int s = 0; s < D / 16; s += 2) {
+            acc0 = mfma(load16(kt + arow * S + 16 * s + 8 * grp), qb[s], acc0);
+            acc1 = mfma(load16(kt + arow * S + 16 * (s + 1) + 8 * grp), qb[s + 1], acc1);
+        }
+        return acc0 + acc1;
     };
 
     // pass 1: exact row maxima
+    tile_lstore<D, 256>(kb[0], tid, kr);
+    __syncthreads();
     float m = kNegInf;
     for (int t = 0; t < ntiles; t++) {
         const uint64_t t0 = static_cast<uint64_t>(t) * kKeyTile;
-        __syncthreads();
-        load_k(t0);
-        __syncthreads();
+        if (t + 1 < ntiles) tile_gload<D, 256>(kg, t0 + kKeyTile, a.n, tid, kr);
+        else {
+            tile_gload<D, 256>(kg, 0, a.n, tid, kr);          // pass 2's first tile
+            tile_gload<D, 256>(vg, 0, a.n, tid, vr);
+        }
         if (t0 < w_kend) {
-            const f32x16 acc = qk();
+            const f32x16 acc = qk(kb[t & 1]);
 #pragma unroll
             for (int r = 0; r < 16; r++) {
                 const uint64_t key = t0 + key_of(r, grp);
@@ -386,6 +464,8 @@ __global__ __launch_bounds__(256, 2) void prefill_attn(PrefillArgs a)
                 if (rowv && key <= lim) m = s > m ? s : m;
             }
         }
+        if (t + 1 < ntiles) tile_lstore<D, 256>(kb[(t + 1) & 1], tid, kr);
+        __syncthreads();
     }
     {
         const float mo = __shfl_xor(m, 32);
@@ -393,18 +473,22 @@ __global__ __launch_bounds__(256, 2) void prefill_attn(PrefillArgs a)
     }
 
     // pass 2: exponentials at the exact maximum, P.V with P = hi + lo
+    tile_lstore<D, 256>(kb[0], tid, kr);
+    tile_lstore<D, 256>(vb[0], tid, vr);
+    __syncthreads();
     f32x16 o[D / 32];
 #pragma unroll
     for (int dt = 0; dt < D / 32; dt++) o[dt] = f32x16{};
     float lsum = 0.0f;
     for (int t = 0; t < ntiles; t++) {
         const uint64_t t0 = static_cast<uint64_t>(t) * kKeyTile;
-        __syncthreads();
-        load_k(t0);
-        load_v(t0);
-        __syncthreads();
+        const int b = t & 1;
+        if (t + 1 < ntiles) {
+            tile_gload<D, 256>(kg, t0 + kKeyTile, a.n, tid, kr);
+            tile_gload<D, 256>(vg, t0 + kKeyTile, a.n, tid, vr);
+        }
         if (t0 < w_kend) {
-            const f32x16 acc = qk();
+            const f32x16 acc = qk(kb[b]);
             float ev[16];
 #pragma unroll
             for (int r = 0; r < 16; r++) {
@@ -420,11 +504,16 @@ __global__ __launch_bounds__(256, 2) void prefill_attn(PrefillArgs a)
             for (int h = 0; h < 2; h++)
 #pragma unroll
                 for (int dt = 0; dt < D / 32; dt++) {
-                    const u32x4 av = load16(vs + (32 * dt + col) * VP + 16 * h + 8 * grp);
+                    const u32x4 av = vt_operand(vb[b], S, 16 * h, 32 * dt, l);
                     o[dt] = mfma(av, hi[h], o[dt]);
                     o[dt] = mfma(av, lo[h], o[dt]);
                 }
         }
+        if (t + 1 < ntiles) {
+            tile_lstore<D, 256>(kb[b ^ 1], tid, kr);
+            tile_lstore<D, 256>(vb[b ^ 1], tid, vr);
+        }
+        __syncthreads();
     }
     lsum += __shfl_xor(lsum, 32);
     if (rowv) {
@@ -450,8 +539,8 @@ template <int D>
 static hipError_t decode_d(const DecodeArgs &a, int kv_heads, hipStream_t s)
 {
     hipLaunchKernelGGL(decode_qk<D>, dim3(a.nwg_qk, kv_heads), dim3(256), 0, s, a);
-    hipLaunchKernelGGL(decode_pv<D>, dim3(a.nwg_pv, kv_heads), dim3(256), 0, s, a);
-    hipLaunchKernelGGL(decode_combine<D>, dim3(kv_heads * a.g), dim3(D), 0, s, a);
+    hipLaunchKernelGGL(decode_pv<D>, dim3(a.nwg_pv, kv_heads), dim3(64 * kPvWaves), decode_pv_lds<D>(a.g), s, a);
+    hipLaunchKernelGGL(decode_combine<D>, dim3(kv_heads * a.g, D / 64), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 
@@ -481,11 +570,8 @@ static void prefill_d(const PrefillArgs &a, int heads, hipStream_t s)
     else prefill_dh<D, 1>(a, heads, s);
 }
 
-hipError_t launch_prefill(const PrefillArgs &a, const TransposeArgs &t, int head_dim, int heads,
-                          int kv_heads, hipStream_t s)
+hipError_t launch_prefill(const PrefillArgs &a, int head_dim, int heads, hipStream_t s)
 {
-    const dim3 tg(static_cast<unsigned>(t.vt_ld / kTransposeTile), head_dim / kTransposeTile, kv_heads);
-    hipLaunchKernelGGL(transpose_v, tg, dim3(256), 0, s, t, head_dim);
     switch (head_dim) {
     case 64: prefill_d<64>(a, heads, s); break;
     case 128: prefill_d<128>(a, heads, s); break;

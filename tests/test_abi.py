@@ -1,0 +1,145 @@
+"""CPU tests of the C ABI of libhsdpa.so: it loads, exports every entry point
+include/hsdpa.h declares, and refuses every invalid plan or call on the host
+with the named status, before any device work."""
+import ctypes
+import os
+import re
+import subprocess
+
+import numpy as np
+import pytest
+
+import hsdpa
+from hsdpa import binding
+from hsdpa import workloads as W
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "hsdpa.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*[a-z_ 0-9*]*?\b(hsdpa_[a-z_]+)\s*\(", text, re.M)))
+
+
+def test_header_declares_the_abi():
+    assert declared_functions() == sorted(binding.EXPORTS)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = hsdpa.library()
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+    out = subprocess.run(["nm", "-D", "--defined-only", hsdpa.library_path()], capture_output=True, text=True).stdout
+    for name in declared_functions():
+        assert re.search(rf"\bT {name}$", out, re.M), name
+
+
+def test_library_has_gfx950_code():
+    """The fat binary embedded in libhsdpa.so carries a gfx950 code object."""
+    out = subprocess.run(["objdump", "-h", hsdpa.library_path()], capture_output=True, text=True).stdout
+    assert ".hip_fatbin" in out
+    data = open(hsdpa.library_path(), "rb").read()
+    assert b"amdgcn-amd-amdhsa--gfx950" in data
+
+
+def test_status_strings_and_version():
+    lib = hsdpa.library()
+    for code in range(12):
+        assert lib.hsdpa_status_string(code)
+    assert lib.hsdpa_version() >= 100
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(heads=16, gqa=3, head_dim=256, kv_capacity=10), "HSDPA_ERR_GQA"),
+    (dict(heads=16, gqa=8, head_dim=96, kv_capacity=10), "HSDPA_ERR_HEAD_DIM"),
+    (dict(heads=16, gqa=8, head_dim=48, kv_capacity=10), "HSDPA_ERR_HEAD_DIM"),
+    (dict(heads=16, gqa=8, head_dim=1024, kv_capacity=10), "HSDPA_ERR_HEAD_DIM"),
+    (dict(heads=16, gqa=8, head_dim=256, kv_capacity=10, sink=True), "HSDPA_ERR_SINK_UNSUPPORTED"),
+    (dict(heads=0, gqa=1, head_dim=256, kv_capacity=1), "HSDPA_ERR_EMPTY"),
+    (dict(heads=16, gqa=8, head_dim=0, kv_capacity=1), "HSDPA_ERR_EMPTY"),
+    (dict(heads=16, gqa=8, head_dim=256, kv_capacity=10, q_head=128), "HSDPA_ERR_STRIDE"),
+    (dict(heads=16, gqa=8, head_dim=256, kv_capacity=10, q_row=1024), "HSDPA_ERR_STRIDE"),
+    (dict(heads=16, gqa=8, head_dim=256, kv_capacity=10, out_row=256), "HSDPA_ERR_STRIDE"),
+    (dict(heads=16, gqa=8, head_dim=256, kv_capacity=10, kv_stride=2000), "HSDPA_ERR_STRIDE"),
+    (dict(heads=16, gqa=8, head_dim=256, kv_capacity=0), "HSDPA_ERR_CAPACITY"),
+    (dict(heads=16, gqa=8, head_dim=256, kv_capacity=10, q_row=16 * 256 + 4), "HSDPA_ERR_ALIGNMENT"),
+])
+def test_plan_refusals(kw, code):
+    with pytest.raises(hsdpa.HsdpaError) as e:
+        hsdpa.Plan(**kw)
+    assert e.value.name == code
+
+
+def test_plan_accepts_engine_geometries():
+    # the gated layout: q rows carry Q then the gate, 2*q_dim apart
+    p = hsdpa.Plan(16, 8, 256, 8192, q_row=2 * 16 * 256, out_row=16 * 256, grouped=True)
+    assert p.workspace_bytes > 0
+    for d in (64, 128, 256):
+        hsdpa.Plan(8, 2, d, 1024)
+
+
+def test_workspace_grows_with_capacity():
+    a = hsdpa.Plan(16, 8, 256, 1024).workspace_bytes
+    b = hsdpa.Plan(16, 8, 256, 32768).workspace_bytes
+    assert b > a and b % 256 == 0
+
+
+def _call(plan, rows=1, past=0, scale=0.0625, sink=0.0, ws_bytes=None, q=0x10000, k=0x20000, v=0x30000,
+          out=0x40000, ws=0x50000):
+    nb = plan.workspace_bytes if ws_bytes is None else ws_bytes
+    c = binding.Call(q, k, v, out, rows, past, scale, sink, ws, nb)
+    return hsdpa.library().hsdpa_attention(plan.handle, ctypes.byref(c), None)
+
+
+def _name(rc):
+    return binding.STATUS[rc]
+
+
+def test_call_refusals_before_any_device_work():
+    p = hsdpa.Plan(16, 8, 256, 100)
+    assert _name(_call(p, rows=0)) == "HSDPA_OK"                     # the empty call is a no-op
+    assert _name(_call(p, rows=2, past=99)) == "HSDPA_ERR_CAPACITY"
+    assert _name(_call(p, rows=101)) == "HSDPA_ERR_CAPACITY"
+    assert _name(_call(p, rows=1, past=2**63)) == "HSDPA_ERR_CAPACITY"
+    assert _name(_call(p, sink=0.5)) == "HSDPA_ERR_SINK_UNSUPPORTED"
+    assert _name(_call(p, q=0)) == "HSDPA_ERR_NULL"
+    assert _name(_call(p, ws=0)) == "HSDPA_ERR_NULL"
+    assert _name(_call(p, k=0x20002)) == "HSDPA_ERR_ALIGNMENT"
+    assert _name(_call(p, ws_bytes=16)) == "HSDPA_ERR_WORKSPACE"
+    assert hsdpa.library().hsdpa_attention(None, None, None) == 9
+
+
+def test_call_without_gpu_fails_loudly():
+    import torch
+
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present")
+    p = hsdpa.Plan(16, 8, 256, 100)
+    assert _name(_call(p)) == "HSDPA_ERR_NO_DEVICE"
+
+
+def test_workloads_are_deterministic_and_shaped():
+    a = W.config("decode_1k", seed=4)
+    b = W.config("decode_1k", seed=4)
+    assert np.array_equal(a.q, b.q) and np.array_equal(a.k, b.k) and np.array_equal(a.v, b.v)
+    assert a.q.shape == (1, 8, 256) and a.k.shape == (2, 1024, 256)
+    assert a.decode_bytes() == 2105344
+    c = W.config("decode_32k", seed=0)
+    assert c.decode_bytes() == 67125248
+    p = W.make("p", heads=16, kv_heads=2, head_dim=256, rows=4096, past=8192, capacity=12288)
+    assert p.prefill_flops() == 687228321792
+    x = W.normal_f32(9, 1 << 16)
+    assert abs(float(x.mean())) < 0.02 and abs(float(x.std()) - 1) < 0.02
+
+
+def test_outlier_workload():
+    w = W.make("o", heads=4, kv_heads=2, head_dim=64, rows=1, past=999, seed=3, outlier_keys=4,
+               outlier_rows_frac=0.01)
+    k = W.bf16_to_f32(w.k)
+    v = W.bf16_to_f32(w.v)
+    for h in range(2):
+        std = k[h].std(axis=0)
+        assert (std > 10).sum() == 4
+        rows = np.abs(v[h]).max(axis=1)
+        assert (rows > 12).sum() >= 5

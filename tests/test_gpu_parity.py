@@ -44,3 +44,36 @@ def test_configs_small(torch_cuda, name):
     ref = oracle.attention(w)
     r = assert_parity(out, ref, w, name)
     print(name, r, flush=True)
+
+
+@pytest.mark.parametrize("name", ["decode_32k", "prefill_4096_after_8192", "decode_128k_outliers"])
+def test_configs_full(torch_cuda, name):
+    """The benchmark configurations at full size (the oracle runs on the host's
+    AVX-512 BF16 restatement, bit-identical to the scalar emulation)."""
+    if not oracle.avx512_available():
+        pytest.skip("host lacks AVX-512 BF16: the scalar oracle is too slow at this size")
+    w = W.config(name, seed=3)
+    print(f"config {name}", flush=True)
+    out = run_hsdpa(w)
+    ref = oracle.attention(w, "avx512")
+    r = assert_parity(out, ref, w, name)
+    print(name, r, flush=True)
+
+
+GROUPS = [
+    # GQA groups beyond the decode kernels' limit take the causal kernel for rows == 1
+    ("decode_g32_d128", 32, 1, 128, 1, 500),
+    ("decode_g16_d256", 32, 2, 256, 1, 999),
+    ("decode_g12_d256", 12, 1, 256, 1, 40),
+]
+
+
+@pytest.mark.parametrize("case", GROUPS, ids=[c[0] for c in GROUPS])
+def test_gqa_groups(torch_cuda, case):
+    name, h, kvh, d, rows, past = case
+    w = W.make(name, heads=h, kv_heads=kvh, head_dim=d, rows=rows, past=past, seed=5)
+    print(f"case {name}", flush=True)
+    out = run_hsdpa(w)
+    ref = oracle.attention(w)
+    r = assert_parity(out, ref, w, name)
+    print(name, r, flush=True)
