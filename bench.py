@@ -214,7 +214,7 @@ def main():
                        "algorithmic_flops": flops},
             "roofline": {"bound": "mfma", "achieved": round(tfs, 2), "peak": MFMA_BF16_PEAK_TFS, "unit": "TFLOP/s",
                          "frac": round(tfs / MFMA_BF16_PEAK_TFS, 4), "traffic": None,
-                         "kernel": "prefill step (transpose_v + prefill_attn)"},
+                         "kernel": "prefill_attn"},
         }
         del ks, vs, q, out
         torch.cuda.empty_cache()

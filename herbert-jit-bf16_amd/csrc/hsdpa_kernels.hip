@@ -82,9 +82,10 @@ __device__ __forceinline__ uint32_t cvt_out(float x)
 {
     const uint32_t b = __float_as_uint(x);
     const uint32_t e = b & 0x7F800000u;
-    if (e == 0) return (b >> 16) & 0x8000u;
-    if (e == 0x7F800000u) return (b & 0x7FFFFFu) ? ((b >> 16) | 0x40u) : (b >> 16);
-    return (b + 0x7FFFu + ((b >> 16) & 1u)) >> 16;
+    const uint32_t rne = (b + 0x7FFFu + ((b >> 16) & 1u)) >> 16;
+    const uint32_t special = (b & 0x7FFFFFu) ? ((b >> 16) | 0x40u) : (b >> 16);
+    const uint32_t r = e == 0x7F800000u ? special : rne;
+    return e == 0 ? ((b >> 16) & 0x8000u) : r;
 }
 
 // Split eight exponentials into hi and lo bf16 halves, packed in k order.
@@ -114,18 +115,7 @@ __device__ __forceinline__ u32x2 tr_read(const uint16_t *p)
     return __builtin_bit_cast(u32x2, r);
 }
 
-// The V^T A operand of v_mfma_f32_32x32x16_bf16 for dimensions [d0, d0+32)
-// and keys [kb + 8g, +8) (g = lane / 32), from a row-major V tile in LDS with
-// row stride vs elements: two transpose reads of four keys each.
-__device__ __forceinline__ u32x4 vt_operand(const uint16_t *vtile, int vs, int kb, int d0, int l)
-{
-    const int j = l & 15, G = l >> 4;
-    const int key = kb + 8 * (G >> 1) + (j >> 2);
-    const int dim = d0 + 16 * (G & 1) + 4 * (j & 3);
-    const u32x2 a = tr_read(vtile + key * vs + dim);
-    const u32x2 b = tr_read(vtile + (key + 4) * vs + dim);
-    return u32x4{a.x, a.y, b.x, b.y};
-}
+
 
 // A 32-key tile of K or V is 32 * D/8 chunks of 16 bytes. Lanes (or threads)
 // take consecutive chunks so every load instruction reads whole rows.
@@ -134,6 +124,9 @@ template <int D, int THREADS> struct Tile {
     static constexpr int kPer = (kChunks + THREADS - 1) / THREADS;
 };
 
+// Loads are unconditional from a clamped in-bounds address (row 0 of the head
+// when the chunk is out of range) and masked afterwards: a conditional load
+// becomes control flow that waits on each load before issuing the next.
 template <int D, int THREADS>
 __device__ __forceinline__ void tile_gload(const uint16_t *base, uint64_t t0, uint64_t lim, int tid,
                                            u32x4 (&r)[Tile<D, THREADS>::kPer])
@@ -142,19 +135,89 @@ __device__ __forceinline__ void tile_gload(const uint16_t *base, uint64_t t0, ui
     for (int i = 0; i < Tile<D, THREADS>::kPer; i++) {
         const int c = tid + THREADS * i, key = c / (D / 8), dc = c % (D / 8);
         const uint64_t gk = t0 + key;
-        r[i] = (c < Tile<D, THREADS>::kChunks && gk < lim) ? load16(base + gk * D + 8 * dc) : u32x4{0, 0, 0, 0};
+        const bool ok = c < Tile<D, THREADS>::kChunks && gk < lim;
+        const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(base + (ok ? gk * D + 8 * dc : 0)));
+        r[i] = ok ? v : u32x4{0, 0, 0, 0};
     }
 }
 
-template <int D, int THREADS>
+// LDS tiles are [32 keys][D] bf16 without padding; bank conflicts are avoided
+// by XOR-swizzling the 16-byte chunk index of each row:
+//  * K tiles (KSW): chunk ^ (key % 16). The QK A operand reads 32 rows at one
+//    chunk; the swizzle spreads them over all 16 chunk slots of the 64 banks.
+//  * V tiles (VSW): chunk ^ 4 (key % 4). A transpose read covers 4 consecutive
+//    rows x 4 consecutive chunks per 32 lanes; the swizzle gives each row its
+//    own 64-byte quarter of the banks.
+enum Swizzle { KSW, VSW };
+
+template <int D, Swizzle Z> __device__ __forceinline__ int swz(int key, int chunk)
+{
+    constexpr int C = D / 8;                     // chunks per row
+    if (Z == KSW) return chunk ^ (key & ((C < 16 ? C : 16) - 1));
+    return chunk ^ ((4 * (key & 3)) & (C - 1));
+}
+
+// Address of element `dim` of row `key` in a swizzled tile.
+template <int D, Swizzle Z> __device__ __forceinline__ const uint16_t *tile_at(const uint16_t *t, int key, int dim)
+{
+    return t + key * D + 8 * swz<D, Z>(key, dim >> 3) + (dim & 7);
+}
+
+template <int D, int THREADS, Swizzle Z>
 __device__ __forceinline__ void tile_lstore(uint16_t *tile, int tid, const u32x4 (&r)[Tile<D, THREADS>::kPer])
 {
-    constexpr int S = D + 16;
 #pragma unroll
     for (int i = 0; i < Tile<D, THREADS>::kPer; i++) {
         const int c = tid + THREADS * i, key = c / (D / 8), dc = c % (D / 8);
-        if (c < Tile<D, THREADS>::kChunks) store16(tile + key * S + 8 * dc, r[i]);
+        if (c < Tile<D, THREADS>::kChunks) store16(tile + key * D + 8 * swz<D, Z>(key, dc), r[i]);
     }
+}
+
+// Padded tiles: row stride D + 8 for K (a read of 32 rows at one 16-byte
+// chunk walks all 16 chunk slots of the banks) and D + 32 for V (the 4 rows
+// of a transpose read land in the 4 quarters of the banks). Addresses stay
+// affine, so per-access offsets fold into immediates.
+template <int D> struct Pad {
+    static constexpr int K = D + 8;
+    static constexpr int V = D + 32;
+};
+
+template <int D, int THREADS>
+__device__ __forceinline__ void tile_lstore_padded(uint16_t *tile, int stride, int tid,
+                                                   const u32x4 (&r)[Tile<D, THREADS>::kPer])
+{
+#pragma unroll
+    for (int i = 0; i < Tile<D, THREADS>::kPer; i++) {
+        const int c = tid + THREADS * i, key = c / (D / 8), dc = c % (D / 8);
+        if (c < Tile<D, THREADS>::kChunks) store16(tile + key * stride + 8 * dc, r[i]);
+    }
+}
+
+// V^T operand from a padded V tile (row stride Pad<D>::V).
+template <int D>
+__device__ __forceinline__ u32x4 vt_operand_padded(const uint16_t *vtile, int kb, int d0, int l)
+{
+    constexpr int S = Pad<D>::V;
+    const int j = l & 15, G = l >> 4;
+    const int key = kb + 8 * (G >> 1) + (j >> 2);
+    const int dim = d0 + 16 * (G & 1) + 4 * (j & 3);
+    const u32x2 a = tr_read(vtile + key * S + dim);
+    const u32x2 b = tr_read(vtile + (key + 4) * S + dim);
+    return u32x4{a.x, a.y, b.x, b.y};
+}
+
+// The V^T A operand of v_mfma_f32_32x32x16_bf16 for dimensions [d0, d0+32)
+// and keys [kb + 8g, +8) (g = lane / 32), from a swizzled V tile in LDS: two
+// transpose reads of four keys each.
+template <int D>
+__device__ __forceinline__ u32x4 vt_operand(const uint16_t *vtile, int kb, int d0, int l)
+{
+    const int j = l & 15, G = l >> 4;
+    const int key = kb + 8 * (G >> 1) + (j >> 2);
+    const int dim = d0 + 16 * (G & 1) + 4 * (j & 3);
+    const u32x2 a = tr_read(tile_at<D, VSW>(vtile, key, dim));
+    const u32x2 b = tr_read(tile_at<D, VSW>(vtile, key + 4, dim));
+    return u32x4{a.x, a.y, b.x, b.y};
 }
 
 // ---------------------------------------------------------------------------
@@ -167,7 +230,7 @@ __device__ __forceinline__ void tile_lstore(uint16_t *tile, int tid, const u32x4
 template <int D>
 __global__ __launch_bounds__(256) void decode_qk(DecodeArgs a)
 {
-    constexpr int S = D + 16;
+    constexpr int S = Pad<D>::K;
     __shared__ __attribute__((aligned(16))) uint16_t kt[4][kKeyTile * S];
     __shared__ float red[4][32];
     const int kvh = blockIdx.y, wg = blockIdx.x;
@@ -176,22 +239,25 @@ __global__ __launch_bounds__(256) void decode_qk(DecodeArgs a)
     const uint64_t j1 = j0 + a.keys_qk < a.n ? j0 + a.keys_qk : a.n;
     const uint64_t t0 = j0 + kKeyTile * wave;
     const uint16_t *kbase = a.k + static_cast<uint64_t>(kvh) * a.kv_stride;
-    u32x4 kr[Tile<D, 64>::kPer];
-    tile_gload<D, 64>(kbase, t0, j1, l, kr);
     const bool colv = col < a.g;
     u32x4 qb[D / 16];
     const uint16_t *qp = a.q + static_cast<uint64_t>(kvh * a.g + (colv ? col : 0)) * a.q_head;
 #pragma unroll
-    for (int ks = 0; ks < D / 16; ks++) qb[ks] = colv ? load16(qp + 16 * ks + 8 * grp) : u32x4{0, 0, 0, 0};
+    for (int ks = 0; ks < D / 16; ks++) {
+        const u32x4 v = load16(qp + 16 * ks + 8 * grp);
+        qb[ks] = colv ? v : u32x4{0, 0, 0, 0};
+    }
+    u32x4 kr[Tile<D, 64>::kPer];
+    tile_gload<D, 64>(kbase, t0, j1, l, kr);
     uint16_t *my = kt[wave];
-    tile_lstore<D, 64>(my, l, kr);
+    tile_lstore_padded<D, 64>(my, S, l, kr);
     __syncthreads();
     f32x16 acc0 = {}, acc1 = {};
-    const int arow = swap23(col);
+    const uint16_t *arow = my + swap23(col) * S + 8 * grp;
 #pragma unroll
     for (int ks = 0; ks < D / 16; ks += 2) {
-        acc0 = mfma(load16(my + arow * S + 16 * ks + 8 * grp), qb[ks], acc0);
-        acc1 = mfma(load16(my + arow * S + 16 * (ks + 1) + 8 * grp), qb[ks + 1], acc1);
+        acc0 = mfma(load16(arow + 16 * ks), qb[ks], acc0);
+        acc1 = mfma(load16(arow + 16 * (ks + 1)), qb[ks + 1], acc1);
     }
     float m = kNegInf;
     if (colv && t0 < j1) {
@@ -219,175 +285,202 @@ __global__ __launch_bounds__(256) void decode_qk(DecodeArgs a)
 
 // ---------------------------------------------------------------------------
 // Decode pass 2: exponentials at the exact maximum and P.V partial sums.
-// grid (nwg_pv, kv_heads), 512 threads, keys_pv = 256: wave w owns the 32-key
-// tile j0 + 32w. Its V rows are loaded first (whole rows), the exact maximum
-// is reduced from the pass-1 maxima, the workgroup's g x 256 exponentials are
-// computed once in a dense layout in LDS, then each wave runs the P.V MFMAs
-// with V^T operands from transpose reads of its row-major tile.
-// Dynamic LDS: 8 V tiles, then e[g][256 + 4] f32.
+// grid (nwg_pv, kv_heads), 512 threads, keys_pv = 256 (8 tiles of 32).
+//  1. wave w loads V tile w (whole rows) into registers;
+//  2. the exact maximum per query head is reduced from the pass-1 maxima;
+//  3. the g x 256 exponentials are computed once, split into hi + lo bf16 and
+//     stored in LDS (rows padded by 16 bytes), with per-head sums;
+//  4. the V tiles go to LDS (swizzled);
+//  5. wave w computes O for the dimension slice w % (D/32) over its share of
+//     the tiles (all 8 at D = 256): V^T from transpose reads, P^T from LDS.
+// Static LDS at D = 256, g = 16: 131 072 + 16 896 + ~2 400 bytes.
 // ---------------------------------------------------------------------------
 constexpr int kPvWaves = 8;
 
 template <int D>
-__global__ __launch_bounds__(512, 2) void decode_pv(DecodeArgs a)
+__global__ __launch_bounds__(512, 1) void decode_pv(DecodeArgs a)
 {
-    constexpr int S = D + 16;
-    constexpr int KEYS = kPvWaves * kKeyTile;         // 256
-    constexpr int ES = KEYS + 4;                      // e row stride, floats
-    extern __shared__ __attribute__((aligned(16))) uint16_t dyn[];
-    uint16_t *vtl = dyn;                               // [8][32 * S]
-    float *ep = reinterpret_cast<float *>(dyn + kPvWaves * kKeyTile * S);   // [g][ES]
+    constexpr int KEYS = kPvWaves * kKeyTile;          // 256
+    constexpr int PS = KEYS + 8;                       // P row stride, bf16
+    constexpr int SLICES = D / 32;                      // dimension slices
+    constexpr int PARTS = kPvWaves / SLICES;            // waves per slice
+    constexpr int TPP = kPvWaves / PARTS;               // tiles per wave
+    __shared__ __attribute__((aligned(16))) uint16_t vt[kPvWaves][kKeyTile * D];
+    __shared__ __attribute__((aligned(16))) uint16_t phi[kDecodeMaxGroup * PS];
+    __shared__ __attribute__((aligned(16))) uint16_t plo[kDecodeMaxGroup * PS];
     __shared__ float mred[512];
-    __shared__ float smax[32];
-    __shared__ float lred[kPvWaves][32];
+    __shared__ float smax[kDecodeMaxGroup];
+    __shared__ float lpart[kPvWaves][kDecodeMaxGroup];
+    __shared__ __attribute__((aligned(16))) float ored[PARTS > 1 ? (PARTS - 1) * SLICES * 16 * 64 : 1];
     const int kvh = blockIdx.y, wg = blockIdx.x, tid = threadIdx.x;
     const int wave = tid >> 6, l = tid & 63, col = l & 31, grp = l >> 5;
     const uint64_t j0 = static_cast<uint64_t>(wg) * KEYS;
     const uint64_t j1 = j0 + KEYS < a.n ? j0 + KEYS : a.n;
-    const uint64_t t0 = j0 + kKeyTile * wave;
     const uint16_t *vbase = a.v + static_cast<uint64_t>(kvh) * a.kv_stride;
-    u32x4 vr[Tile<D, 64>::kPer];
-    tile_gload<D, 64>(vbase, t0, j1, l, vr);
-
-    // exact maximum per query head, from the pass-1 workgroup maxima
+    // The small loads go first: the vector-memory counter completes in order,
+    // so anything issued after the V tile would wait for all of it.
+    const int key_e = tid % KEYS;
+    const uint64_t gk_e = j0 + key_e;
+    const bool kv_e = gk_e < j1;
+    float sv[kDecodeMaxGroup / 2];
+#pragma unroll
+    for (int i = 0; i < kDecodeMaxGroup / 2; i++) {
+        const int h = tid / KEYS + 2 * i;
+        const int hc = h < a.g ? h : 0;
+        sv[i] = a.scores[static_cast<uint64_t>(kvh * a.g + hc) * a.npad + (kv_e ? gk_e : 0)];
+    }
+    const int tph = 512 / a.g;
+    const int jh = tid / tph, u = tid % tph;
+    float m = kNegInf;
     {
-        const int tph = 512 / a.g;
-        const int jh = tid / tph, u = tid % tph;
-        float m = kNegInf;
-        if (jh < a.g) {
-            const float *src = a.wgmax + (static_cast<uint64_t>(kvh) * a.g + jh) * a.nwg_qk;
-            for (int w = u; w < a.nwg_qk; w += tph) m = src[w] > m ? src[w] : m;
+        const float *src = a.wgmax + (static_cast<uint64_t>(kvh) * a.g + (jh < a.g ? jh : 0)) * a.nwg_qk;
+        constexpr int BATCH = 8;
+        for (int w0 = u; w0 < a.nwg_qk; w0 += BATCH * tph) {
+            float x[BATCH];
+#pragma unroll
+            for (int b = 0; b < BATCH; b++) {
+                const int w = w0 + b * tph;
+                x[b] = src[w < a.nwg_qk ? w : 0];
+            }
+#pragma unroll
+            for (int b = 0; b < BATCH; b++) m = (w0 + b * tph < a.nwg_qk && x[b] > m) ? x[b] : m;
         }
+        if (jh >= a.g) m = kNegInf;
+    }
+    u32x4 vr[Tile<D, 64>::kPer];
+    tile_gload<D, 64>(vbase, j0 + kKeyTile * wave, j1, l, vr);
+
+    // 2. exact maximum per query head, from the pass-1 workgroup maxima
+    {
         mred[tid] = m;
         __syncthreads();
-        if (tid < 32) {
+        if (tid < a.g) {
             float r = kNegInf;
-            if (tid < a.g)
-                for (int i = 0; i < tph; i++) {
-                    const float x = mred[tid * tph + i];
-                    r = x > r ? x : r;
-                }
+            for (int i = 0; i < tph; i++) {
+                const float x = mred[tid * tph + i];
+                r = x > r ? x : r;
+            }
             smax[tid] = r;
         }
         __syncthreads();
     }
-    // dense exponentials: thread t owns key j0 + t % 256 for heads t/256, +2, ...
+    // 3. dense exponentials: thread t owns key j0 + t % 256 for heads t/256,
+    //    t/256 + 2, ...; a wave covers 64 consecutive keys of one head set
     {
-        const int key = tid % KEYS;
-        const uint64_t gk = j0 + key;
-        for (int h = tid / KEYS; h < a.g; h += 512 / KEYS) {
-            const float *srow = a.scores + static_cast<uint64_t>(kvh * a.g + h) * a.npad;
-            ep[h * ES + key] = gk < j1 ? exp_poly(srow[gk] - smax[h]) : 0.0f;
+        const int key = key_e;
+        const bool kv = kv_e;
+#pragma unroll
+        for (int i = 0; i < kDecodeMaxGroup / 2; i++) {
+            const int h = tid / KEYS + 2 * i;
+            if (h >= a.g) break;
+            const float e = kv ? exp_poly(sv[i] - smax[h]) : 0.0f;
+            const uint32_t hb = bf16_rne(e);
+            phi[h * PS + key] = static_cast<uint16_t>(hb);
+            plo[h * PS + key] = static_cast<uint16_t>(bf16_rne(e - __uint_as_float(hb << 16)));
+            float sum = e;
+#pragma unroll
+            for (int off = 32; off >= 1; off >>= 1) sum += __shfl_xor(sum, off);
+            if (l == 0) lpart[wave][h] = sum;
         }
     }
-    uint16_t *my = vtl + wave * (kKeyTile * S);
-    tile_lstore<D, 64>(my, l, vr);
+    // 4. V tile to LDS
+    tile_lstore<D, 64, VSW>(vt[wave], l, vr);
     __syncthreads();
 
+    // 5. P.V for one dimension slice
+    const int slice = wave % SLICES, part = wave / SLICES;
     const bool colv = col < a.g;
-    float lsum = 0.0f;
-    u32x4 hi[2], lo[2];
+    f32x16 o = {};
 #pragma unroll
-    for (int h = 0; h < 2; h++) {
-        float ev[8];
-        if (colv) {
-            const float *e = ep + col * ES + kKeyTile * wave + 16 * h + 8 * grp;
+    for (int tt = 0; tt < TPP; tt++) {
+        const int t = part * TPP + tt;
 #pragma unroll
-            for (int s2 = 0; s2 < 8; s2++) ev[s2] = e[s2];
-        } else {
-#pragma unroll
-            for (int s2 = 0; s2 < 8; s2++) ev[s2] = 0.0f;
-        }
-#pragma unroll
-        for (int s2 = 0; s2 < 8; s2++) lsum += ev[s2];
-        split_pack(ev, hi[h], lo[h]);
-    }
-    f32x16 o[D / 32];
-#pragma unroll
-    for (int dt = 0; dt < D / 32; dt++) o[dt] = f32x16{};
-#pragma unroll
-    for (int h = 0; h < 2; h++)
-#pragma unroll
-        for (int dt = 0; dt < D / 32; dt++) {
-            const u32x4 av = vt_operand(my, S, 16 * h, 32 * dt, l);
-            o[dt] = mfma(av, hi[h], o[dt]);
-            o[dt] = mfma(av, lo[h], o[dt]);
-        }
-    lsum += __shfl_xor(lsum, 32);
-    if (grp == 0) lred[wave][col] = lsum;
-    // cross-wave reduction of O^T (valid columns only) through the V tiles
-    float *red = reinterpret_cast<float *>(vtl);
-    const int slab = a.g * D;                          // floats per wave
-    for (int step = kPvWaves / 2; step >= 1; step >>= 1) {
-        __syncthreads();
-        if (wave >= step && wave < 2 * step && colv) {
-            float *dst = red + (wave - step) * slab + col * D;
-#pragma unroll
-            for (int dt = 0; dt < D / 32; dt++)
-#pragma unroll
-                for (int r = 0; r < 16; r++) dst[32 * dt + 8 * (r >> 2) + 4 * grp + (r & 3)] = o[dt][r];
-        }
-        __syncthreads();
-        if (wave < step && colv) {
-            const float *src = red + wave * slab + col * D;
-#pragma unroll
-            for (int dt = 0; dt < D / 32; dt++)
-#pragma unroll
-                for (int r = 0; r < 16; r++) o[dt][r] += src[32 * dt + 8 * (r >> 2) + 4 * grp + (r & 3)];
+        for (int h = 0; h < 2; h++) {
+            const int k0 = kKeyTile * t + 16 * h + 8 * grp;
+            const u32x4 ph = load16(phi + (colv ? col : 0) * PS + k0);
+            const u32x4 pl = load16(plo + (colv ? col : 0) * PS + k0);
+            const u32x4 zero = {0, 0, 0, 0};
+            const u32x4 av = vt_operand<D>(vt[t], 16 * h, 32 * slice, l);
+            o = mfma(av, colv ? ph : zero, o);
+            o = mfma(av, colv ? pl : zero, o);
         }
     }
-    if (wave == 0 && colv) {
-        const uint64_t part = (static_cast<uint64_t>(kvh) * a.nwg_pv + wg) * a.g + col;
-        float *dst = a.part_o + part * D;
+    if (PARTS > 1) {
+        if (part > 0) {
+            float *dst = ored + ((part - 1) * SLICES + slice) * 1024;
 #pragma unroll
-        for (int dt = 0; dt < D / 32; dt++)
+            for (int r = 0; r < 16; r++) dst[r * 64 + l] = o[r];
+        }
+        __syncthreads();
+        if (part == 0)
+            for (int p = 1; p < PARTS; p++) {
+                const float *src = ored + ((p - 1) * SLICES + slice) * 1024;
 #pragma unroll
-            for (int c = 0; c < 4; c++) {
-                float4 v4 = {o[dt][4 * c], o[dt][4 * c + 1], o[dt][4 * c + 2], o[dt][4 * c + 3]};
-                *reinterpret_cast<float4 *>(dst + 32 * dt + 8 * c + 4 * grp) = v4;
+                for (int r = 0; r < 16; r++) o[r] += src[r * 64 + l];
             }
-        if (grp == 0) {
-            float L = 0.0f;
+    }
+    const uint64_t pbase = (static_cast<uint64_t>(kvh) * a.nwg_pv + wg) * a.g;
+    if (part == 0 && colv) {
+        float *dst = a.part_o + (pbase + col) * D + 32 * slice + 4 * grp;
 #pragma unroll
-            for (int w = 0; w < kPvWaves; w++) L += lred[w][col];
-            a.part_l[part] = L;
+        for (int c = 0; c < 4; c++) {
+            float4 v4 = {o[4 * c], o[4 * c + 1], o[4 * c + 2], o[4 * c + 3]};
+            *reinterpret_cast<float4 *>(dst + 8 * c) = v4;
         }
     }
-}
-
-// Dynamic LDS of decode_pv: at D = 256 and g = 16, 139 264 + 16 640 bytes,
-// plus 3 200 static, within the 160 KiB of a gfx950 workgroup.
-template <int D> constexpr size_t decode_pv_lds(int g)
-{
-    return static_cast<size_t>(kPvWaves) * kKeyTile * (D + 16) * 2 + static_cast<size_t>(g) * (kPvWaves * kKeyTile + 4) * 4;
+    if (tid < a.g) {
+        // heads of parity p were summed by waves 4p .. 4p+3, 64 keys each
+        const int p0 = (tid % (512 / KEYS)) * (KEYS / 64);
+        float L = 0.0f;
+        for (int w = 0; w < KEYS / 64; w++) L += lpart[p0 + w][tid];
+        a.part_l[pbase + tid] = L;
+    }
 }
 
 // ---------------------------------------------------------------------------
 // Decode pass 3: out[h] = bf16(sum_w O_w / sum_w l_w).
-// grid (heads, D/64), 256 threads: 64 dimensions x 4 interleaved partial sets,
-// summed in a fixed order (deterministic).
+// grid (heads, D/64), 512 threads: 64 dimensions x 8 interleaved partial
+// subsets; every thread issues all its loads before adding (one round trip
+// for up to 8 * 16 partials), and the subsets are summed in a fixed order.
 // ---------------------------------------------------------------------------
+constexpr int kCombineSubs = 8;
+
 template <int D>
-__global__ __launch_bounds__(256) void decode_combine(DecodeArgs a)
+__global__ __launch_bounds__(512) void decode_combine(DecodeArgs a)
 {
-    __shared__ float ored[4][64];
-    __shared__ float lred[4];
+    __shared__ float ored[kCombineSubs][64];
+    __shared__ float lred[kCombineSubs];
     const int h = blockIdx.x, kvh = h / a.g, jh = h % a.g;
     const int t = threadIdx.x & 63, sub = threadIdx.x >> 6, dim = blockIdx.y * 64 + t;
     float o = 0.0f, L = 0.0f;
     const uint64_t base = static_cast<uint64_t>(kvh) * a.nwg_pv * a.g + jh;
-#pragma unroll 8
-    for (int w = sub; w < a.nwg_pv; w += 4) {
-        const uint64_t part = base + static_cast<uint64_t>(w) * a.g;
-        o += a.part_o[part * D + dim];
-        L += a.part_l[part];
+    constexpr int BATCH = 16;
+    for (int w0 = sub; w0 < a.nwg_pv; w0 += kCombineSubs * BATCH) {
+        float xo[BATCH], xl[BATCH];
+#pragma unroll
+        for (int b = 0; b < BATCH; b++) {
+            const int w = w0 + kCombineSubs * b;
+            const uint64_t part = base + static_cast<uint64_t>(w < a.nwg_pv ? w : 0) * a.g;
+            xo[b] = a.part_o[part * D + dim];
+            xl[b] = a.part_l[part];
+        }
+#pragma unroll
+        for (int b = 0; b < BATCH; b++)
+            if (w0 + kCombineSubs * b < a.nwg_pv) {
+                o += xo[b];
+                L += xl[b];
+            }
     }
     ored[sub][t] = o;
     if (t == 0) lred[sub] = L;
     __syncthreads();
     if (sub == 0) {
-        const float os = (ored[0][t] + ored[1][t]) + (ored[2][t] + ored[3][t]);
-        const float ls = (lred[0] + lred[1]) + (lred[2] + lred[3]);
+        float os = 0.0f, ls = 0.0f;
+#pragma unroll
+        for (int i = 0; i < kCombineSubs; i++) {
+            os += ored[i][t];
+            ls += lred[i];
+        }
         a.out[static_cast<uint64_t>(h) * D + dim] = static_cast<uint16_t>(cvt_out(os / ls));
     }
 }
@@ -405,10 +498,9 @@ template <int D, int HPW>
 __global__ __launch_bounds__(256, 1) void prefill_attn(PrefillArgs a)
 {
     constexpr int RB = 4 / HPW;
-    constexpr int S = D + 16;
-    constexpr int TE = kKeyTile * S;
-    __shared__ __attribute__((aligned(16))) uint16_t kb[2][TE];
-    __shared__ __attribute__((aligned(16))) uint16_t vb[2][TE];
+    constexpr int SK = Pad<D>::K, SV = Pad<D>::V;
+    __shared__ __attribute__((aligned(16))) uint16_t kb[2][kKeyTile * SK];
+    __shared__ __attribute__((aligned(16))) uint16_t vb[2][kKeyTile * SV];
     const int tid = threadIdx.x;
     const int wave = tid >> 6, l = tid & 63, col = l & 31, grp = l >> 5;
     const int head = blockIdx.y * HPW + (wave % HPW);
@@ -432,20 +524,23 @@ __global__ __launch_bounds__(256, 1) void prefill_attn(PrefillArgs a)
     u32x4 qb[D / 16];
     const uint16_t *qp = a.q + (rowv ? row : 0) * a.q_row + static_cast<uint64_t>(head) * a.q_head;
 #pragma unroll
-    for (int s = 0; s < D / 16; s++) qb[s] = rowv ? load16(qp + 16 * s + 8 * grp) : u32x4{0, 0, 0, 0};
-    const int arow = swap23(col);
+    for (int s = 0; s < D / 16; s++) {
+        const u32x4 v = load16(qp + 16 * s + 8 * grp);
+        qb[s] = rowv ? v : u32x4{0, 0, 0, 0};
+    }
+    const int arow = swap23(col) * SK + 8 * grp;
     auto qk = [&](const uint16_t *kt) {
         f32x16 acc0 = {}, acc1 = {};
 #pragma unroll
         for (int s = 0; s < D / 16; s += 2) {
-            acc0 = mfma(load16(kt + arow * S + 16 * s + 8 * grp), qb[s], acc0);
-            acc1 = mfma(load16(kt + arow * S + 16 * (s + 1) + 8 * grp), qb[s + 1], acc1);
+            acc0 = mfma(load16(kt + arow + 16 * s), qb[s], acc0);
+            acc1 = mfma(load16(kt + arow + 16 * (s + 1)), qb[s + 1], acc1);
         }
         return acc0 + acc1;
     };
 
     // pass 1: exact row maxima
-    tile_lstore<D, 256>(kb[0], tid, kr);
+    tile_lstore_padded<D, 256>(kb[0], SK, tid, kr);
     __syncthreads();
     float m = kNegInf;
     for (int t = 0; t < ntiles; t++) {
@@ -464,7 +559,7 @@ __global__ __launch_bounds__(256, 1) void prefill_attn(PrefillArgs a)
                 if (rowv && key <= lim) m = s > m ? s : m;
             }
         }
-        if (t + 1 < ntiles) tile_lstore<D, 256>(kb[(t + 1) & 1], tid, kr);
+        if (t + 1 < ntiles) tile_lstore_padded<D, 256>(kb[(t + 1) & 1], SK, tid, kr);
         __syncthreads();
     }
     {
@@ -473,8 +568,8 @@ __global__ __launch_bounds__(256, 1) void prefill_attn(PrefillArgs a)
     }
 
     // pass 2: exponentials at the exact maximum, P.V with P = hi + lo
-    tile_lstore<D, 256>(kb[0], tid, kr);
-    tile_lstore<D, 256>(vb[0], tid, vr);
+    tile_lstore_padded<D, 256>(kb[0], SK, tid, kr);
+    tile_lstore_padded<D, 256>(vb[0], SV, tid, vr);
     __syncthreads();
     f32x16 o[D / 32];
 #pragma unroll
@@ -504,14 +599,14 @@ __global__ __launch_bounds__(256, 1) void prefill_attn(PrefillArgs a)
             for (int h = 0; h < 2; h++)
 #pragma unroll
                 for (int dt = 0; dt < D / 32; dt++) {
-                    const u32x4 av = vt_operand(vb[b], S, 16 * h, 32 * dt, l);
+                    const u32x4 av = vt_operand_padded<D>(vb[b], 16 * h, 32 * dt, l);
                     o[dt] = mfma(av, hi[h], o[dt]);
                     o[dt] = mfma(av, lo[h], o[dt]);
                 }
         }
         if (t + 1 < ntiles) {
-            tile_lstore<D, 256>(kb[b ^ 1], tid, kr);
-            tile_lstore<D, 256>(vb[b ^ 1], tid, vr);
+            tile_lstore_padded<D, 256>(kb[b ^ 1], SK, tid, kr);
+            tile_lstore_padded<D, 256>(vb[b ^ 1], SV, tid, vr);
         }
         __syncthreads();
     }
@@ -539,8 +634,8 @@ template <int D>
 static hipError_t decode_d(const DecodeArgs &a, int kv_heads, hipStream_t s)
 {
     hipLaunchKernelGGL(decode_qk<D>, dim3(a.nwg_qk, kv_heads), dim3(256), 0, s, a);
-    hipLaunchKernelGGL(decode_pv<D>, dim3(a.nwg_pv, kv_heads), dim3(64 * kPvWaves), decode_pv_lds<D>(a.g), s, a);
-    hipLaunchKernelGGL(decode_combine<D>, dim3(kv_heads * a.g, D / 64), dim3(256), 0, s, a);
+    hipLaunchKernelGGL(decode_pv<D>, dim3(a.nwg_pv, kv_heads), dim3(64 * kPvWaves), 0, s, a);
+    hipLaunchKernelGGL(decode_combine<D>, dim3(kv_heads * a.g, D / 64), dim3(64 * kCombineSubs), 0, s, a);
     return hipGetLastError();
 }
 
