@@ -39,12 +39,21 @@ namespace hsdpa {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 static constexpr float kNegInf = -__builtin_huge_valf();
 
 __device__ __forceinline__ f32x16 mfma(u32x4 a, u32x4 b, f32x16 c)
 {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+
+// v_mfma_f32_16x16x32_bf16, lane l, i = l % 16, G = l / 16: A[i][k] and
+// B[k][i] for k = 8G..8G+7; D[4G + r][i] in register r.
+__device__ __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c)
+{
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
                                                    __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
 }
 
@@ -103,6 +112,56 @@ __device__ __forceinline__ void split_pack(const float *e, u32x4 &hi, u32x4 &lo)
 
 __device__ __forceinline__ int swap23(int i) { return (i & ~12) | ((i & 4) << 1) | ((i & 8) >> 1); }
 
+// Wave reductions on the DPP paths (no LDS round trips). Within each row of
+// 16 lanes: swap neighbours, swap pairs, half-row mirror, row mirror; every
+// lane of a row then holds the row's result. Across rows, row_bcast:15 folds
+// row 0 into row 1 and row 2 into row 3, row_bcast:31 folds lane 31 into rows
+// 2 and 3: lane 31 holds the result of lanes 0..31, lane 63 of all 64.
+template <int CTRL, int ROWS>
+__device__ __forceinline__ float dpp(float x, float old)
+{
+    return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(old), __float_as_int(x), CTRL, ROWS, 0xF, false));
+}
+
+__device__ __forceinline__ float row_sum16(float x)
+{
+    x += dpp<0xB1, 0xF>(x, 0.0f);    // quad_perm [1,0,3,2]
+    x += dpp<0x4E, 0xF>(x, 0.0f);    // quad_perm [2,3,0,1]
+    x += dpp<0x141, 0xF>(x, 0.0f);   // row_half_mirror
+    x += dpp<0x140, 0xF>(x, 0.0f);   // row_mirror
+    return x;
+}
+
+// Sum over the 64 lanes, valid in lane 63.
+__device__ __forceinline__ float wave_sum_hi(float x)
+{
+    x = row_sum16(x);
+    x += dpp<0x142, 0xA>(x, 0.0f);   // row_bcast:15 into rows 1 and 3
+    x += dpp<0x143, 0xC>(x, 0.0f);   // row_bcast:31 into rows 2 and 3
+    return x;
+}
+
+__device__ __forceinline__ float fmaxnn(float a, float b) { return b > a ? b : a; }
+
+// Maximum over each half wave (lanes 0..31 in lane 31, 32..63 in lane 63) and
+// over the whole wave (in lane 63) when `whole`. -inf is the identity; NaN
+// inputs are ignored like in the scalar reductions.
+__device__ __forceinline__ float wave_max_hi(float x, bool whole)
+{
+    x = fmaxnn(x, dpp<0xB1, 0xF>(x, kNegInf));
+    x = fmaxnn(x, dpp<0x4E, 0xF>(x, kNegInf));
+    x = fmaxnn(x, dpp<0x141, 0xF>(x, kNegInf));
+    x = fmaxnn(x, dpp<0x140, 0xF>(x, kNegInf));
+    x = fmaxnn(x, dpp<0x142, 0xA>(x, kNegInf));
+    if (whole) x = fmaxnn(x, dpp<0x143, 0xC>(x, kNegInf));
+    return x;
+}
+
+__device__ __forceinline__ float lane_value(float x, int lane)
+{
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), lane));
+}
+
 // Key offset inside a 32-key tile of score register r for lane group g.
 __device__ __forceinline__ int key_of(int r, int g) { return 16 * (r >> 3) + 8 * g + (r & 7); }
 
@@ -125,8 +184,10 @@ template <int D, int THREADS> struct Tile {
 };
 
 // Loads are unconditional from a clamped in-bounds address (row 0 of the head
-// when the chunk is out of range) and masked afterwards: a conditional load
-// becomes control flow that waits on each load before issuing the next.
+// when the chunk is out of range): a conditional load becomes control flow
+// that waits on each load before issuing the next. tile_mask zeroes the
+// out-of-range chunks afterwards; it waits on the loads, so it goes where the
+// data is consumed, not next to the loads.
 template <int D, int THREADS>
 __device__ __forceinline__ void tile_gload(const uint16_t *base, uint64_t t0, uint64_t lim, int tid,
                                            u32x4 (&r)[Tile<D, THREADS>::kPer])
@@ -136,41 +197,56 @@ __device__ __forceinline__ void tile_gload(const uint16_t *base, uint64_t t0, ui
         const int c = tid + THREADS * i, key = c / (D / 8), dc = c % (D / 8);
         const uint64_t gk = t0 + key;
         const bool ok = c < Tile<D, THREADS>::kChunks && gk < lim;
-        const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(base + (ok ? gk * D + 8 * dc : 0)));
-        r[i] = ok ? v : u32x4{0, 0, 0, 0};
+        r[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(base + (ok ? gk * D + 8 * dc : 0)));
     }
 }
 
-// LDS tiles are [32 keys][D] bf16 without padding; bank conflicts are avoided
-// by XOR-swizzling the 16-byte chunk index of each row:
-//  * K tiles (KSW): chunk ^ (key % 16). The QK A operand reads 32 rows at one
-//    chunk; the swizzle spreads them over all 16 chunk slots of the 64 banks.
-//  * V tiles (VSW): chunk ^ 4 (key % 4). A transpose read covers 4 consecutive
-//    rows x 4 consecutive chunks per 32 lanes; the swizzle gives each row its
-//    own 64-byte quarter of the banks.
-enum Swizzle { KSW, VSW };
-
-template <int D, Swizzle Z> __device__ __forceinline__ int swz(int key, int chunk)
+template <int D, int THREADS>
+__device__ __forceinline__ void tile_mask(uint64_t t0, uint64_t lim, int tid, u32x4 (&r)[Tile<D, THREADS>::kPer])
 {
-    constexpr int C = D / 8;                     // chunks per row
-    if (Z == KSW) return chunk ^ (key & ((C < 16 ? C : 16) - 1));
-    return chunk ^ ((4 * (key & 3)) & (C - 1));
+#pragma unroll
+    for (int i = 0; i < Tile<D, THREADS>::kPer; i++) {
+        const int c = tid + THREADS * i;
+        const bool ok = c < Tile<D, THREADS>::kChunks && t0 + c / (D / 8) < lim;
+        r[i] = ok ? r[i] : u32x4{0, 0, 0, 0};
+    }
 }
 
-// Address of element `dim` of row `key` in a swizzled tile.
-template <int D, Swizzle Z> __device__ __forceinline__ const uint16_t *tile_at(const uint16_t *t, int key, int dim)
+// Decode V tiles are [32 keys][D] bf16 without padding. The V^T operand of
+// v_mfma_f32_16x16x32_bf16 is two transpose reads; half a wave of one read
+// covers rows {k, k+1, k+2, k+3, k+8, .., k+11} (k a multiple of 16) at the
+// same 32 bytes of dimensions. XOR-ing the 32-byte slot index of each row
+// with f(key) = key % 4 + 4 ((key / 8) % 2) puts those eight rows on eight
+// distinct 32-byte bank slots.
+template <int D> __device__ __forceinline__ int swz16(int key, int chunk)
 {
-    return t + key * D + 8 * swz<D, Z>(key, dim >> 3) + (dim & 7);
+    constexpr int C = D / 8;                     // 16-byte chunks per row
+    const int f = (key & 3) | (((key >> 3) & 1) << 2);
+    return chunk ^ ((2 * f) & (C - 1));
 }
 
-template <int D, int THREADS, Swizzle Z>
-__device__ __forceinline__ void tile_lstore(uint16_t *tile, int tid, const u32x4 (&r)[Tile<D, THREADS>::kPer])
+template <int D, int THREADS>
+__device__ __forceinline__ void tile_lstore_v16(uint16_t *tile, int tid, const u32x4 (&r)[Tile<D, THREADS>::kPer])
 {
 #pragma unroll
     for (int i = 0; i < Tile<D, THREADS>::kPer; i++) {
         const int c = tid + THREADS * i, key = c / (D / 8), dc = c % (D / 8);
-        if (c < Tile<D, THREADS>::kChunks) store16(tile + key * D + 8 * swz<D, Z>(key, dc), r[i]);
+        if (c < Tile<D, THREADS>::kChunks) store16(tile + key * D + 8 * swz16<D>(key, dc), r[i]);
     }
+}
+
+// The V^T A operand of v_mfma_f32_16x16x32_bf16 for dimensions [d0, d0+16)
+// and the 32 keys of a swizzled tile: lane (i, G) receives keys 8G..8G+7 of
+// dimension d0 + i from two transpose reads of four keys each.
+template <int D>
+__device__ __forceinline__ u32x4 vt16_operand(const uint16_t *vtile, int d0, int l)
+{
+    const int j = l & 15, G = l >> 4;
+    const int key = 8 * G + (j >> 2);
+    const int dim = d0 + 4 * (j & 3);
+    const u32x2 a = tr_read(vtile + key * D + 8 * swz16<D>(key, dim >> 3) + (dim & 7));
+    const u32x2 b = tr_read(vtile + (key + 4) * D + 8 * swz16<D>(key + 4, dim >> 3) + (dim & 7));
+    return u32x4{a.x, a.y, b.x, b.y};
 }
 
 // Padded tiles: row stride D + 8 for K (a read of 32 rows at one 16-byte
@@ -206,76 +282,91 @@ __device__ __forceinline__ u32x4 vt_operand_padded(const uint16_t *vtile, int kb
     return u32x4{a.x, a.y, b.x, b.y};
 }
 
-// The V^T A operand of v_mfma_f32_32x32x16_bf16 for dimensions [d0, d0+32)
-// and keys [kb + 8g, +8) (g = lane / 32), from a swizzled V tile in LDS: two
-// transpose reads of four keys each.
-template <int D>
-__device__ __forceinline__ u32x4 vt_operand(const uint16_t *vtile, int kb, int d0, int l)
-{
-    const int j = l & 15, G = l >> 4;
-    const int key = kb + 8 * (G >> 1) + (j >> 2);
-    const int dim = d0 + 16 * (G & 1) + 4 * (j & 3);
-    const u32x2 a = tr_read(tile_at<D, VSW>(vtile, key, dim));
-    const u32x2 b = tr_read(tile_at<D, VSW>(vtile, key + 4, dim));
-    return u32x4{a.x, a.y, b.x, b.y};
-}
-
 // ---------------------------------------------------------------------------
 // Decode pass 1: scores and per-workgroup maxima.
-// grid (nwg_qk, kv_heads), 256 threads, keys_qk = 128: wave w stages the
-// 32-key tile j0 + 32w through its own LDS rows with whole-row loads, then
-// reads the MFMA A operands from there. Q^T columns are the g query heads of
-// the KV head (padded to 32).
+// grid (nwg_qk, kv_heads), 256 threads, keys_qk = 128: wave w computes the
+// 32 keys j0 + 32w .. +32 as two 16-key blocks of v_mfma_f32_16x16x32_bf16
+// (S^T = K . Q^T, the g <= 16 query heads of the KV head as the columns).
+// The wave loads its 32 K rows whole (each load instruction reads 1 KB of
+// contiguous cache), stages them through its own LDS rows with the 16-byte
+// chunks XOR-swizzled by key % 16, and reads the A operands from there:
+// lane (i, G) takes row i, dimensions 32s + 8G .. +8. Loading the operands
+// straight from HBM would request 64 bytes of 16 rows per instruction, which
+// streams measurably slower than whole rows.
 // ---------------------------------------------------------------------------
 template <int D>
 __global__ __launch_bounds__(256) void decode_qk(DecodeArgs a)
 {
-    constexpr int S = Pad<D>::K;
-    __shared__ __attribute__((aligned(16))) uint16_t kt[4][kKeyTile * S];
-    __shared__ float red[4][32];
+    constexpr int KS = D / 32;
+    constexpr int C = D / 8, KM = (C < 16 ? C : 16) - 1;        // chunks per row, swizzle mask
+    __shared__ __attribute__((aligned(16))) uint16_t kt[4][kKeyTile * D];
+    __shared__ float red[4][16];
     const int kvh = blockIdx.y, wg = blockIdx.x;
-    const int wave = threadIdx.x >> 6, l = threadIdx.x & 63, col = l & 31, grp = l >> 5;
+    const int wave = threadIdx.x >> 6, l = threadIdx.x & 63, i = l & 15, G = l >> 4;
     const uint64_t j0 = static_cast<uint64_t>(wg) * a.keys_qk;
     const uint64_t j1 = j0 + a.keys_qk < a.n ? j0 + a.keys_qk : a.n;
     const uint64_t t0 = j0 + kKeyTile * wave;
-    const uint16_t *kbase = a.k + static_cast<uint64_t>(kvh) * a.kv_stride;
-    const bool colv = col < a.g;
-    u32x4 qb[D / 16];
-    const uint16_t *qp = a.q + static_cast<uint64_t>(kvh * a.g + (colv ? col : 0)) * a.q_head;
+    const bool colv = i < a.g;
+    // Rows past the visible keys (loaded from row 0) and columns past g are
+    // computed and discarded: an MFMA output element depends only on its own
+    // A row and B column.
+    const uint16_t *qp = a.q + static_cast<uint64_t>(kvh * a.g + (colv ? i : 0)) * a.q_head + 8 * G;
+    u32x4 qb[KS];
 #pragma unroll
-    for (int ks = 0; ks < D / 16; ks++) {
-        const u32x4 v = load16(qp + 16 * ks + 8 * grp);
-        qb[ks] = colv ? v : u32x4{0, 0, 0, 0};
-    }
+    for (int s = 0; s < KS; s++) qb[s] = load16(qp + 32 * s);
     u32x4 kr[Tile<D, 64>::kPer];
-    tile_gload<D, 64>(kbase, t0, j1, l, kr);
+    tile_gload<D, 64>(a.k + static_cast<uint64_t>(kvh) * a.kv_stride, t0, j1, l, kr);
+    // Every load is in flight before the first use waits on one: left to
+    // itself the scheduler interleaves them and keeps only a few outstanding.
+    __builtin_amdgcn_sched_barrier(0);
     uint16_t *my = kt[wave];
-    tile_lstore_padded<D, 64>(my, S, l, kr);
-    __syncthreads();
-    f32x16 acc0 = {}, acc1 = {};
-    const uint16_t *arow = my + swap23(col) * S + 8 * grp;
 #pragma unroll
-    for (int ks = 0; ks < D / 16; ks += 2) {
-        acc0 = mfma(load16(arow + 16 * ks), qb[ks], acc0);
-        acc1 = mfma(load16(arow + 16 * (ks + 1)), qb[ks + 1], acc1);
+    for (int c0 = 0; c0 < Tile<D, 64>::kPer; c0++) {
+        const int c = l + 64 * c0, key = c / C, dc = c % C;
+        store16(my + key * D + 8 * (dc ^ (key & KM)), kr[c0]);
     }
+    // The rows are this wave's own: LDS operations of one wave complete in
+    // order, so only the compiler has to be kept from reordering them.
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    u32x4 ka[2][KS];
+#pragma unroll
+    for (int b = 0; b < 2; b++)
+#pragma unroll
+        for (int s = 0; s < KS; s++) {
+            const int row = 16 * b + i;
+            ka[b][s] = load16(my + row * D + 8 * ((4 * s + G) ^ (row & KM)));
+        }
+    f32x4 acc[2] = {};
+#pragma unroll
+    for (int s = 0; s < KS; s++)
+#pragma unroll
+        for (int b = 0; b < 2; b++) acc[b] = mfma16(ka[b][s], qb[s], acc[b]);
     float m = kNegInf;
     if (colv && t0 < j1) {
-        float *sp = a.scores + static_cast<uint64_t>(kvh * a.g + col) * a.npad + t0 + 8 * grp;
+        float *sp = a.scores + static_cast<uint64_t>(kvh * a.g + i) * a.npad + t0 + 4 * G;
 #pragma unroll
-        for (int r = 0; r < 16; r++) {
-            const uint64_t kk = t0 + key_of(r, grp);
-            const float s = (acc0[r] + acc1[r]) * a.scale;
-            const bool valid = kk < j1;
-            sp[16 * (r >> 3) + (r & 7)] = valid ? s : kNegInf;
-            if (valid) m = s > m ? s : m;
+        for (int b = 0; b < 2; b++) {
+            float4 v4;
+            float *v = reinterpret_cast<float *>(&v4);
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const bool valid = t0 + 16 * b + 4 * G + r < j1;
+                const float s = acc[b][r] * a.scale;
+                v[r] = valid ? s : kNegInf;
+                if (valid) m = s > m ? s : m;
+            }
+            *reinterpret_cast<float4 *>(sp + 16 * b) = v4;
         }
     }
-    const float mo = __shfl_xor(m, 32);
+    float mo = __shfl_xor(m, 16);
     m = mo > m ? mo : m;
-    if (grp == 0) red[wave][col] = m;
+    mo = __shfl_xor(m, 32);
+    m = mo > m ? mo : m;
+    if (G == 0) red[wave][i] = m;
     __syncthreads();
-    if (threadIdx.x < 32 && static_cast<int>(threadIdx.x) < a.g) {
+    if (threadIdx.x < 16 && static_cast<int>(threadIdx.x) < a.g) {
         float r = red[0][threadIdx.x];
 #pragma unroll
         for (int w = 1; w < 4; w++) r = red[w][threadIdx.x] > r ? red[w][threadIdx.x] : r;
@@ -289,34 +380,37 @@ __global__ __launch_bounds__(256) void decode_qk(DecodeArgs a)
 //  1. wave w loads V tile w (whole rows) into registers;
 //  2. the exact maximum per query head is reduced from the pass-1 maxima;
 //  3. the g x 256 exponentials are computed once, split into hi + lo bf16 and
-//     stored in LDS (rows padded by 16 bytes), with per-head sums;
-//  4. the V tiles go to LDS (swizzled);
-//  5. wave w computes O for the dimension slice w % (D/32) over its share of
-//     the tiles (all 8 at D = 256): V^T from transpose reads, P^T from LDS.
-// Static LDS at D = 256, g = 16: 131 072 + 16 896 + ~2 400 bytes.
+//     stored in LDS as P columns: with g <= 8, columns 0..7 hold hi and 8..15
+//     lo, so one v_mfma_f32_16x16x32_bf16 covers both halves; with g > 8 the
+//     hi and lo halves are two 16-column blocks;
+//  4. the V tiles go to LDS (swizzled for the 16-row transpose reads);
+//  5. wave w computes O^T = V^T . P^T for its dimension blocks over its
+//     share of the tiles; O = O(hi columns) + O(lo columns).
+// Static LDS at D = 256: 131 072 + 16 896 + ~2 600 bytes.
 // ---------------------------------------------------------------------------
 constexpr int kPvWaves = 8;
 
 template <int D>
 __global__ __launch_bounds__(512, 1) void decode_pv(DecodeArgs a)
 {
-    constexpr int KEYS = kPvWaves * kKeyTile;          // 256
-    constexpr int PS = KEYS + 8;                       // P row stride, bf16
-    constexpr int SLICES = D / 32;                      // dimension slices
-    constexpr int PARTS = kPvWaves / SLICES;            // waves per slice
-    constexpr int TPP = kPvWaves / PARTS;               // tiles per wave
+    constexpr int KEYS = kPvWaves * kKeyTile;                   // 256
+    constexpr int PS = KEYS + 8;                                // P column stride, bf16
+    constexpr int DB = D / 16;                                  // 16-dimension blocks
+    constexpr int DBW = DB >= kPvWaves ? DB / kPvWaves : 1;     // blocks per wave
+    constexpr int PARTS = DB >= kPvWaves ? 1 : kPvWaves / DB;   // waves per block
+    constexpr int WPP = kPvWaves / PARTS;                       // waves per part
+    constexpr int TPP = kPvWaves / PARTS;                       // tiles per wave
     __shared__ __attribute__((aligned(16))) uint16_t vt[kPvWaves][kKeyTile * D];
-    __shared__ __attribute__((aligned(16))) uint16_t phi[kDecodeMaxGroup * PS];
-    __shared__ __attribute__((aligned(16))) uint16_t plo[kDecodeMaxGroup * PS];
-    __shared__ float mred[512];
+    __shared__ __attribute__((aligned(16))) uint16_t pc[2 * kDecodeMaxGroup * PS];
     __shared__ float smax[kDecodeMaxGroup];
     __shared__ float lpart[kPvWaves][kDecodeMaxGroup];
-    __shared__ __attribute__((aligned(16))) float ored[PARTS > 1 ? (PARTS - 1) * SLICES * 16 * 64 : 1];
+    __shared__ __attribute__((aligned(16))) float ored[PARTS > 1 ? (PARTS - 1) * WPP * 2 * DBW * 4 * 64 : 1];
     const int kvh = blockIdx.y, wg = blockIdx.x, tid = threadIdx.x;
-    const int wave = tid >> 6, l = tid & 63, col = l & 31, grp = l >> 5;
+    const int wave = tid >> 6, l = tid & 63, j = l & 15, G = l >> 4;
     const uint64_t j0 = static_cast<uint64_t>(wg) * KEYS;
     const uint64_t j1 = j0 + KEYS < a.n ? j0 + KEYS : a.n;
     const uint16_t *vbase = a.v + static_cast<uint64_t>(kvh) * a.kv_stride;
+    const int nh = a.g <= 8 ? 8 : 16;                           // lo columns start here
     // The small loads go first: the vector-memory counter completes in order,
     // so anything issued after the V tile would wait for all of it.
     const int key_e = tid % KEYS;
@@ -329,103 +423,115 @@ __global__ __launch_bounds__(512, 1) void decode_pv(DecodeArgs a)
         const int hc = h < a.g ? h : 0;
         sv[i] = a.scores[static_cast<uint64_t>(kvh * a.g + hc) * a.npad + (kv_e ? gk_e : 0)];
     }
-    const int tph = 512 / a.g;
-    const int jh = tid / tph, u = tid % tph;
-    float m = kNegInf;
-    {
-        const float *src = a.wgmax + (static_cast<uint64_t>(kvh) * a.g + (jh < a.g ? jh : 0)) * a.nwg_qk;
-        constexpr int BATCH = 8;
-        for (int w0 = u; w0 < a.nwg_qk; w0 += BATCH * tph) {
-            float x[BATCH];
+    // Pass-1 maxima: T lanes per head (a whole wave for g <= 8, half a wave
+    // for g <= 16); lane u reads entries u, u + T, .. of head t / T. The first
+    // batch is loaded before the V tile, later batches (more than 8 T
+    // workgroups in pass 1) after it.
+    const int T = a.g <= 8 ? 64 : 32;
+    const int jh = tid / T, u = tid % T;
+    const float *msrc = a.wgmax + (static_cast<uint64_t>(kvh) * a.g + (jh < a.g ? jh : 0)) * a.nwg_qk;
+    constexpr int BATCH = 8;
+    float mx[BATCH];
 #pragma unroll
-            for (int b = 0; b < BATCH; b++) {
-                const int w = w0 + b * tph;
-                x[b] = src[w < a.nwg_qk ? w : 0];
-            }
-#pragma unroll
-            for (int b = 0; b < BATCH; b++) m = (w0 + b * tph < a.nwg_qk && x[b] > m) ? x[b] : m;
-        }
-        if (jh >= a.g) m = kNegInf;
+    for (int b = 0; b < BATCH; b++) {
+        const int w = u + b * T;
+        mx[b] = msrc[w < a.nwg_qk ? w : 0];
     }
     u32x4 vr[Tile<D, 64>::kPer];
     tile_gload<D, 64>(vbase, j0 + kKeyTile * wave, j1, l, vr);
-
-    // 2. exact maximum per query head, from the pass-1 workgroup maxima
-    {
-        mred[tid] = m;
-        __syncthreads();
-        if (tid < a.g) {
-            float r = kNegInf;
-            for (int i = 0; i < tph; i++) {
-                const float x = mred[tid * tph + i];
-                r = x > r ? x : r;
-            }
-            smax[tid] = r;
+    __builtin_amdgcn_sched_barrier(0);                          // all loads issued first
+    float m = kNegInf;
+#pragma unroll
+    for (int b = 0; b < BATCH; b++) m = (u + b * T < a.nwg_qk && mx[b] > m) ? mx[b] : m;
+    for (int w0 = u + BATCH * T; w0 < a.nwg_qk; w0 += BATCH * T) {
+#pragma unroll
+        for (int b = 0; b < BATCH; b++) {
+            const int w = w0 + b * T;
+            mx[b] = msrc[w < a.nwg_qk ? w : 0];
         }
-        __syncthreads();
+#pragma unroll
+        for (int b = 0; b < BATCH; b++) m = (w0 + b * T < a.nwg_qk && mx[b] > m) ? mx[b] : m;
     }
+
+    // 2. exact maximum per query head: a DPP reduction over the head's lanes
+    m = wave_max_hi(m, T == 64);
+    if (u == T - 1 && jh < a.g) smax[jh] = m;
+    __syncthreads();
+
     // 3. dense exponentials: thread t owns key j0 + t % 256 for heads t/256,
     //    t/256 + 2, ...; a wave covers 64 consecutive keys of one head set
     {
-        const int key = key_e;
-        const bool kv = kv_e;
 #pragma unroll
         for (int i = 0; i < kDecodeMaxGroup / 2; i++) {
             const int h = tid / KEYS + 2 * i;
             if (h >= a.g) break;
-            const float e = kv ? exp_poly(sv[i] - smax[h]) : 0.0f;
+            const float e = kv_e ? exp_poly(sv[i] - smax[h]) : 0.0f;
             const uint32_t hb = bf16_rne(e);
-            phi[h * PS + key] = static_cast<uint16_t>(hb);
-            plo[h * PS + key] = static_cast<uint16_t>(bf16_rne(e - __uint_as_float(hb << 16)));
-            float sum = e;
-#pragma unroll
-            for (int off = 32; off >= 1; off >>= 1) sum += __shfl_xor(sum, off);
-            if (l == 0) lpart[wave][h] = sum;
+            pc[h * PS + key_e] = static_cast<uint16_t>(hb);
+            pc[(nh + h) * PS + key_e] = static_cast<uint16_t>(bf16_rne(e - __uint_as_float(hb << 16)));
+            const float sum = wave_sum_hi(e);
+            if (l == 63) lpart[wave][h] = sum;
         }
     }
     // 4. V tile to LDS
-    tile_lstore<D, 64, VSW>(vt[wave], l, vr);
+    tile_mask<D, 64>(j0 + kKeyTile * wave, j1, l, vr);
+    tile_lstore_v16<D, 64>(vt[wave], l, vr);
     __syncthreads();
 
-    // 5. P.V for one dimension slice
-    const int slice = wave % SLICES, part = wave / SLICES;
-    const bool colv = col < a.g;
-    f32x16 o = {};
+    // 5. P.V for this wave's dimension blocks. Columns that hold no head read
+    //    whatever the LDS holds; their outputs are never used.
+    const int dgi = wave % WPP, part = wave / WPP;
+    const int ncb = a.g <= 8 ? 1 : 2;
+    f32x4 o[2][DBW] = {};
 #pragma unroll
     for (int tt = 0; tt < TPP; tt++) {
         const int t = part * TPP + tt;
+        const u32x4 b0 = load16(pc + j * PS + kKeyTile * t + 8 * G);
+        u32x4 b1 = b0;
+        if (ncb == 2) b1 = load16(pc + (16 + j) * PS + kKeyTile * t + 8 * G);
 #pragma unroll
-        for (int h = 0; h < 2; h++) {
-            const int k0 = kKeyTile * t + 16 * h + 8 * grp;
-            const u32x4 ph = load16(phi + (colv ? col : 0) * PS + k0);
-            const u32x4 pl = load16(plo + (colv ? col : 0) * PS + k0);
-            const u32x4 zero = {0, 0, 0, 0};
-            const u32x4 av = vt_operand<D>(vt[t], 16 * h, 32 * slice, l);
-            o = mfma(av, colv ? ph : zero, o);
-            o = mfma(av, colv ? pl : zero, o);
+        for (int db = 0; db < DBW; db++) {
+            const u32x4 av = vt16_operand<D>(vt[t], 16 * (dgi * DBW + db), l);
+            o[0][db] = mfma16(av, b0, o[0][db]);
+            if (ncb == 2) o[1][db] = mfma16(av, b1, o[1][db]);
         }
     }
     if (PARTS > 1) {
         if (part > 0) {
-            float *dst = ored + ((part - 1) * SLICES + slice) * 1024;
+            float *dst = ored + ((part - 1) * WPP + dgi) * (2 * DBW * 4 * 64);
 #pragma unroll
-            for (int r = 0; r < 16; r++) dst[r * 64 + l] = o[r];
+            for (int c = 0; c < 2; c++)
+#pragma unroll
+                for (int db = 0; db < DBW; db++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++) dst[((c * DBW + db) * 4 + r) * 64 + l] = o[c][db][r];
         }
         __syncthreads();
         if (part == 0)
             for (int p = 1; p < PARTS; p++) {
-                const float *src = ored + ((p - 1) * SLICES + slice) * 1024;
+                const float *src = ored + ((p - 1) * WPP + dgi) * (2 * DBW * 4 * 64);
 #pragma unroll
-                for (int r = 0; r < 16; r++) o[r] += src[r * 64 + l];
+                for (int c = 0; c < 2; c++)
+#pragma unroll
+                    for (int db = 0; db < DBW; db++)
+#pragma unroll
+                        for (int r = 0; r < 4; r++) o[c][db][r] += src[((c * DBW + db) * 4 + r) * 64 + l];
             }
     }
+    // O(head) = O(hi column) + O(lo column): lane j + 8 holds the lo column
+    // of head j when g <= 8, the second block when g > 8.
     const uint64_t pbase = (static_cast<uint64_t>(kvh) * a.nwg_pv + wg) * a.g;
-    if (part == 0 && colv) {
-        float *dst = a.part_o + (pbase + col) * D + 32 * slice + 4 * grp;
 #pragma unroll
-        for (int c = 0; c < 4; c++) {
-            float4 v4 = {o[4 * c], o[4 * c + 1], o[4 * c + 2], o[4 * c + 3]};
-            *reinterpret_cast<float4 *>(dst + 8 * c) = v4;
+    for (int db = 0; db < DBW; db++) {
+        f32x4 s;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const float lo8 = __shfl_xor(o[0][db][r], 8);
+            s[r] = ncb == 1 ? o[0][db][r] + lo8 : o[0][db][r] + o[1][db][r];
+        }
+        if (part == 0 && j < (ncb == 1 ? 8 : 16) && j < a.g) {
+            float *dst = a.part_o + (pbase + j) * D + 16 * (dgi * DBW + db) + 4 * G;
+            *reinterpret_cast<float4 *>(dst) = float4{s[0], s[1], s[2], s[3]};
         }
     }
     if (tid < a.g) {
@@ -569,6 +675,7 @@ __global__ __launch_bounds__(256, 1) void prefill_attn(PrefillArgs a)
 
     // pass 2: exponentials at the exact maximum, P.V with P = hi + lo
     tile_lstore_padded<D, 256>(kb[0], SK, tid, kr);
+    tile_mask<D, 256>(0, a.n, tid, vr);
     tile_lstore_padded<D, 256>(vb[0], SV, tid, vr);
     __syncthreads();
     f32x16 o[D / 32];
@@ -606,6 +713,7 @@ __global__ __launch_bounds__(256, 1) void prefill_attn(PrefillArgs a)
         }
         if (t + 1 < ntiles) {
             tile_lstore_padded<D, 256>(kb[b ^ 1], SK, tid, kr);
+            tile_mask<D, 256>(t0 + kKeyTile, a.n, tid, vr);
             tile_lstore_padded<D, 256>(vb[b ^ 1], SV, tid, vr);
         }
         __syncthreads();
