@@ -192,22 +192,28 @@ template <int D, int THREADS>
 __device__ __forceinline__ void tile_gload(const uint16_t *base, uint64_t t0, uint64_t lim, int tid,
                                            u32x4 (&r)[Tile<D, THREADS>::kPer])
 {
+    // t0 and lim are uniform: the tile base stays in scalar registers and each
+    // lane adds a 32-bit offset. A tile starting at or past lim reads row 0.
+    const bool any = t0 < lim;
+    const uint16_t *tb = base + (any ? t0 : 0) * D;
+    const uint32_t nvalid = any ? static_cast<uint32_t>(lim - t0 < kKeyTile ? lim - t0 : kKeyTile) : 0u;
 #pragma unroll
     for (int i = 0; i < Tile<D, THREADS>::kPer; i++) {
         const int c = tid + THREADS * i, key = c / (D / 8), dc = c % (D / 8);
-        const uint64_t gk = t0 + key;
-        const bool ok = c < Tile<D, THREADS>::kChunks && gk < lim;
-        r[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(base + (ok ? gk * D + 8 * dc : 0)));
+        const bool ok = c < Tile<D, THREADS>::kChunks && static_cast<uint32_t>(key) < nvalid;
+        const uint32_t off = ok ? static_cast<uint32_t>(key * D + 8 * dc) : 0u;
+        r[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(tb + off));
     }
 }
 
 template <int D, int THREADS>
 __device__ __forceinline__ void tile_mask(uint64_t t0, uint64_t lim, int tid, u32x4 (&r)[Tile<D, THREADS>::kPer])
 {
+    const uint32_t nvalid = t0 < lim ? static_cast<uint32_t>(lim - t0 < kKeyTile ? lim - t0 : kKeyTile) : 0u;
 #pragma unroll
     for (int i = 0; i < Tile<D, THREADS>::kPer; i++) {
         const int c = tid + THREADS * i;
-        const bool ok = c < Tile<D, THREADS>::kChunks && t0 + c / (D / 8) < lim;
+        const bool ok = c < Tile<D, THREADS>::kChunks && static_cast<uint32_t>(c / (D / 8)) < nvalid;
         r[i] = ok ? r[i] : u32x4{0, 0, 0, 0};
     }
 }
@@ -594,16 +600,66 @@ __global__ __launch_bounds__(512) void decode_combine(DecodeArgs a)
 // ---------------------------------------------------------------------------
 // Prefill: the causal attention of a chunk, two passes over the keys in one
 // workgroup: the exact row maxima, then exponentials and P.V.
-// grid (row groups, heads/HPW), 256 threads. Wave w serves query head
-// blockIdx.y*HPW + w%HPW and rows [r0 + 32*(w/HPW), +32), r0 the group's
-// first row; the HPW heads of a group share one KV head, so all four waves
-// read the same K and V tiles from LDS. Tiles are double-buffered: the global
-// loads of tile t+1 are in flight while tile t is computed.
+// grid (row groups, heads / HPW), 512 threads = 8 waves, two per SIMD. Wave w
+// serves query head blockIdx.y * HPW + w % HPW and rows r0 + 32 (w / HPW) ..
+// +32, r0 the group's first row; the HPW heads of a workgroup share one KV
+// head (HPW = 8 when g is a multiple of 8), so all waves read the same K and V
+// tiles from LDS. Tiles are double-buffered: the global loads of tile t+1 are
+// in flight while tile t is computed. Tiles below the diagonal of all of a
+// wave's rows skip the causal mask.
+// POW2 (the scale is a positive power of two): fl(fl(dot * scale) - M) equals
+// fl(dot - Mraw) * scale exactly, Mraw being the maximum of the unscaled
+// dot products, and the scale folds exactly into the exponential's clamp
+// (-87.33654 / scale) and multiplier (log2(e) * scale). Otherwise every score
+// is scaled first, as in the reference.
 // ---------------------------------------------------------------------------
-template <int D, int HPW>
-__global__ __launch_bounds__(256, 1) void prefill_attn(PrefillArgs a)
+struct ExpArgs {
+    float m;        // POW2: Mraw; otherwise the scaled maximum M
+    float scale;    // otherwise: the scale
+    float clamp;    // POW2: -87.33654 / scale; otherwise -87.33654
+    float mul;      // POW2: 1.442695 * scale; otherwise 1.442695
+};
+
+template <bool POW2>
+__device__ __forceinline__ float exp_score(float acc, const ExpArgs &x)
 {
-    constexpr int RB = 4 / HPW;
+    const float d = POW2 ? acc - x.m : acc * x.scale - x.m;
+    const float t1 = __builtin_fmaxf(d, x.clamp) * x.mul;
+    const float t2 = __builtin_rintf(t1);
+    const float f = t1 - t2;
+    float p = __builtin_fmaf(f, 0.00967248f, 0.05550411f);
+    p = __builtin_fmaf(f, p, 0.2402265f);
+    p = __builtin_fmaf(f, p, 0.6931472f);
+    p = __builtin_fmaf(f, p, 1.0f);
+    return __builtin_ldexpf(p, static_cast<int>(t2));
+}
+
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+// Round two f32 to bf16, nearest even, packed low/high (v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint32_t pk_bf16(float a, float b)
+{
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{a, b}), bf16x2));
+}
+
+// Eight exponentials as hi and lo bf16 halves, packed in k order.
+__device__ __forceinline__ void split_pack_hw(const float *e, u32x4 &hi, u32x4 &lo)
+{
+#pragma unroll
+    for (int s = 0; s < 4; s++) {
+        const uint32_t h = pk_bf16(e[2 * s], e[2 * s + 1]);
+        const float r0 = e[2 * s] - __uint_as_float(h << 16);
+        const float r1 = e[2 * s + 1] - __uint_as_float(h & 0xFFFF0000u);
+        hi[s] = h;
+        lo[s] = pk_bf16(r0, r1);
+    }
+}
+
+template <int D, int HPW, bool POW2>
+__global__ __launch_bounds__(512, 1) void prefill_attn(PrefillArgs a)
+{
+    constexpr int NW = 8, RB = NW / HPW;
     constexpr int SK = Pad<D>::K, SV = Pad<D>::V;
     __shared__ __attribute__((aligned(16))) uint16_t kb[2][kKeyTile * SK];
     __shared__ __attribute__((aligned(16))) uint16_t vb[2][kKeyTile * SV];
@@ -616,17 +672,17 @@ __global__ __launch_bounds__(256, 1) void prefill_attn(PrefillArgs a)
     const uint64_t w_r0 = wg_r0 + 32 * (wave / HPW);
     const uint64_t row = w_r0 + col;
     const bool rowv = row < a.rows;
+    const bool wact = w_r0 < a.rows;
     const uint64_t wg_rend = wg_r0 + 32 * RB < a.rows ? wg_r0 + 32 * RB : a.rows;
-    const uint64_t wg_kend = a.past + wg_rend;
-    const uint64_t w_kend = w_r0 < a.rows ? a.past + (w_r0 + 32 < a.rows ? w_r0 + 32 : a.rows) : 0;
-    const int ntiles = static_cast<int>((wg_kend + kKeyTile - 1) / kKeyTile);
+    const int ntiles = static_cast<int>((a.past + wg_rend + kKeyTile - 1) / kKeyTile);
+    const uint64_t w_kend = wact ? a.past + (w_r0 + 32 < a.rows ? w_r0 + 32 : a.rows) : 0;
+    const int wtiles = static_cast<int>((w_kend + kKeyTile - 1) / kKeyTile);  // tiles the wave computes
+    const int nfull = wact ? static_cast<int>((a.past + w_r0 + 1) / kKeyTile) : 0;  // no mask needed
     const uint64_t lim = a.past + row;                         // last visible key of this row
 
     const uint16_t *kg = a.k + static_cast<uint64_t>(kvh) * a.kv_stride;
     const uint16_t *vg = a.v + static_cast<uint64_t>(kvh) * a.kv_stride;
-    u32x4 kr[Tile<D, 256>::kPer], vr[Tile<D, 256>::kPer];
-    tile_gload<D, 256>(kg, 0, a.n, tid, kr);
-
+    u32x4 kr[Tile<D, 512>::kPer], vr[Tile<D, 512>::kPer];
     u32x4 qb[D / 16];
     const uint16_t *qp = a.q + (rowv ? row : 0) * a.q_row + static_cast<uint64_t>(head) * a.q_head;
 #pragma unroll
@@ -634,49 +690,59 @@ __global__ __launch_bounds__(256, 1) void prefill_attn(PrefillArgs a)
         const u32x4 v = load16(qp + 16 * s + 8 * grp);
         qb[s] = rowv ? v : u32x4{0, 0, 0, 0};
     }
+    tile_gload<D, 512>(kg, 0, a.n, tid, kr);
     const int arow = swap23(col) * SK + 8 * grp;
+    // One accumulation chain: a second one would not fit the 256 registers
+    // of two waves per SIMD; the other wave on the SIMD fills the gaps.
     auto qk = [&](const uint16_t *kt) {
-        f32x16 acc0 = {}, acc1 = {};
+        f32x16 acc = {};
 #pragma unroll
-        for (int s = 0; s < D / 16; s += 2) {
-            acc0 = mfma(load16(kt + arow + 16 * s), qb[s], acc0);
-            acc1 = mfma(load16(kt + arow + 16 * (s + 1)), qb[s + 1], acc1);
-        }
-        return acc0 + acc1;
+        for (int s = 0; s < D / 16; s++) acc = mfma(load16(kt + arow + 16 * s), qb[s], acc);
+        return acc;
     };
 
-    // pass 1: exact row maxima
-    tile_lstore_padded<D, 256>(kb[0], SK, tid, kr);
+    // pass 1: exact row maxima (of the unscaled dot products when POW2).
+    // Out-of-range keys of the last tile load row 0 and are never visible.
+    tile_lstore_padded<D, 512>(kb[0], SK, tid, kr);
     __syncthreads();
     float m = kNegInf;
     for (int t = 0; t < ntiles; t++) {
         const uint64_t t0 = static_cast<uint64_t>(t) * kKeyTile;
-        if (t + 1 < ntiles) tile_gload<D, 256>(kg, t0 + kKeyTile, a.n, tid, kr);
+        if (t + 1 < ntiles) tile_gload<D, 512>(kg, t0 + kKeyTile, a.n, tid, kr);
         else {
-            tile_gload<D, 256>(kg, 0, a.n, tid, kr);          // pass 2's first tile
-            tile_gload<D, 256>(vg, 0, a.n, tid, vr);
+            tile_gload<D, 512>(kg, 0, a.n, tid, kr);          // pass 2's first tile
+            tile_gload<D, 512>(vg, 0, a.n, tid, vr);
         }
-        if (t0 < w_kend) {
+        __builtin_amdgcn_sched_barrier(0);
+        if (t < wtiles) {
             const f32x16 acc = qk(kb[t & 1]);
+            if (t < nfull) {
 #pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const uint64_t key = t0 + key_of(r, grp);
-                const float s = acc[r] * a.scale;
-                if (rowv && key <= lim) m = s > m ? s : m;
+                for (int r = 0; r < 16; r++) m = __builtin_fmaxf(m, POW2 ? acc[r] : acc[r] * a.scale);
+            } else {
+                // keys t0 + k with k <= vis are visible to this row
+                const int vis = static_cast<int>(static_cast<int64_t>(lim) - static_cast<int64_t>(t0));
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const float s = POW2 ? acc[r] : acc[r] * a.scale;
+                    if (key_of(r, grp) <= vis) m = __builtin_fmaxf(m, s);
+                }
             }
         }
-        if (t + 1 < ntiles) tile_lstore_padded<D, 256>(kb[(t + 1) & 1], SK, tid, kr);
+        if (t + 1 < ntiles) tile_lstore_padded<D, 512>(kb[(t + 1) & 1], SK, tid, kr);
         __syncthreads();
     }
-    {
-        const float mo = __shfl_xor(m, 32);
-        m = mo > m ? mo : m;
-    }
+    m = __builtin_fmaxf(m, __shfl_xor(m, 32));
+    ExpArgs ex;
+    ex.m = m;
+    ex.scale = a.scale;
+    ex.clamp = POW2 ? -87.33654f / a.scale : -87.33654f;
+    ex.mul = POW2 ? 1.442695f * a.scale : 1.442695f;
 
     // pass 2: exponentials at the exact maximum, P.V with P = hi + lo
-    tile_lstore_padded<D, 256>(kb[0], SK, tid, kr);
-    tile_mask<D, 256>(0, a.n, tid, vr);
-    tile_lstore_padded<D, 256>(vb[0], SV, tid, vr);
+    tile_lstore_padded<D, 512>(kb[0], SK, tid, kr);
+    tile_mask<D, 512>(0, a.n, tid, vr);
+    tile_lstore_padded<D, 512>(vb[0], SV, tid, vr);
     __syncthreads();
     f32x16 o[D / 32];
 #pragma unroll
@@ -685,36 +751,46 @@ __global__ __launch_bounds__(256, 1) void prefill_attn(PrefillArgs a)
     for (int t = 0; t < ntiles; t++) {
         const uint64_t t0 = static_cast<uint64_t>(t) * kKeyTile;
         const int b = t & 1;
-        if (t + 1 < ntiles) {
-            tile_gload<D, 256>(kg, t0 + kKeyTile, a.n, tid, kr);
-            tile_gload<D, 256>(vg, t0 + kKeyTile, a.n, tid, vr);
-        }
-        if (t0 < w_kend) {
+        // The next K tile is loaded now, the next V tile after the softmax:
+        // their staging registers are then never live together with both the
+        // scores and the P operands.
+        if (t + 1 < ntiles) tile_gload<D, 512>(kg, t0 + kKeyTile, a.n, tid, kr);
+        __builtin_amdgcn_sched_barrier(0);
+        if (t < wtiles) {
             const f32x16 acc = qk(kb[b]);
-            float ev[16];
+            const bool full = t < nfull;
+            const int vis = full ? 64 : static_cast<int>(static_cast<int64_t>(lim) - static_cast<int64_t>(t0));
+            // Each half of the 32 keys is exponentiated, split and multiplied
+            // in turn, so that only one half's P operands are live.
 #pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const uint64_t key = t0 + key_of(r, grp);
-                const float s = acc[r] * a.scale;
-                ev[r] = (rowv && key <= lim) ? exp_poly(s - m) : 0.0f;
-                lsum += ev[r];
-            }
-            u32x4 hi[2], lo[2];
-            split_pack(ev, hi[0], lo[0]);
-            split_pack(ev + 8, hi[1], lo[1]);
+            for (int h = 0; h < 2; h++) {
+                float ev[8];
 #pragma unroll
-            for (int h = 0; h < 2; h++)
+                for (int r = 0; r < 8; r++) {
+                    const float e = exp_score<POW2>(acc[8 * h + r], ex);
+                    ev[r] = full || key_of(8 * h + r, grp) <= vis ? e : 0.0f;
+                    lsum += ev[r];
+                }
+                u32x4 hi, lo;
+                split_pack_hw(ev, hi, lo);
+                if (h == 0) {
+                    if (t + 1 < ntiles) tile_gload<D, 512>(vg, t0 + kKeyTile, a.n, tid, vr);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
 #pragma unroll
                 for (int dt = 0; dt < D / 32; dt++) {
                     const u32x4 av = vt_operand_padded<D>(vb[b], 16 * h, 32 * dt, l);
-                    o[dt] = mfma(av, hi[h], o[dt]);
-                    o[dt] = mfma(av, lo[h], o[dt]);
+                    o[dt] = mfma(av, hi, o[dt]);
+                    o[dt] = mfma(av, lo, o[dt]);
                 }
+            }
+        } else if (t + 1 < ntiles) {
+            tile_gload<D, 512>(vg, t0 + kKeyTile, a.n, tid, vr);
         }
         if (t + 1 < ntiles) {
-            tile_lstore_padded<D, 256>(kb[b ^ 1], SK, tid, kr);
-            tile_mask<D, 256>(t0 + kKeyTile, a.n, tid, vr);
-            tile_lstore_padded<D, 256>(vb[b ^ 1], SV, tid, vr);
+            tile_lstore_padded<D, 512>(kb[b ^ 1], SK, tid, kr);
+            tile_mask<D, 512>(t0 + kKeyTile, a.n, tid, vr);
+            tile_lstore_padded<D, 512>(vb[b ^ 1], SV, tid, vr);
         }
         __syncthreads();
     }
@@ -738,6 +814,15 @@ __global__ __launch_bounds__(256, 1) void prefill_attn(PrefillArgs a)
 // ---------------------------------------------------------------------------
 bool head_dim_supported(int d) { return d == 64 || d == 128 || d == 256; }
 
+// A positive power of two in [2^-20, 2^20]: scaling by it is exact for the
+// scores and for the folded exponential constants.
+static bool scale_is_pow2(float s)
+{
+    const uint32_t b = __builtin_bit_cast(uint32_t, s);
+    const uint32_t e = (b >> 23) & 0xFF;
+    return (b & 0x807FFFFFu) == 0 && e >= 127 - 20 && e <= 127 + 20;
+}
+
 template <int D>
 static hipError_t decode_d(const DecodeArgs &a, int kv_heads, hipStream_t s)
 {
@@ -760,15 +845,17 @@ hipError_t launch_decode(const DecodeArgs &a, int head_dim, int kv_heads, hipStr
 template <int D, int HPW>
 static void prefill_dh(const PrefillArgs &a, int heads, hipStream_t s)
 {
-    const int rows_per_wg = 32 * (4 / HPW);
+    const int rows_per_wg = 32 * (8 / HPW);
     const dim3 grid(static_cast<unsigned>((a.rows + rows_per_wg - 1) / rows_per_wg), heads / HPW);
-    hipLaunchKernelGGL((prefill_attn<D, HPW>), grid, dim3(256), 0, s, a);
+    if (scale_is_pow2(a.scale)) hipLaunchKernelGGL((prefill_attn<D, HPW, true>), grid, dim3(512), 0, s, a);
+    else hipLaunchKernelGGL((prefill_attn<D, HPW, false>), grid, dim3(512), 0, s, a);
 }
 
 template <int D>
 static void prefill_d(const PrefillArgs &a, int heads, hipStream_t s)
 {
-    if (a.gqa % 4 == 0) prefill_dh<D, 4>(a, heads, s);
+    if (a.gqa % 8 == 0) prefill_dh<D, 8>(a, heads, s);
+    else if (a.gqa % 4 == 0) prefill_dh<D, 4>(a, heads, s);
     else if (a.gqa % 2 == 0) prefill_dh<D, 2>(a, heads, s);
     else prefill_dh<D, 1>(a, heads, s);
 }
