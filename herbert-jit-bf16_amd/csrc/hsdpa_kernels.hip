@@ -34,6 +34,8 @@
 
 #include "hsdpa_kernels.h"
 
+#include <type_traits>
+
 namespace hsdpa {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -675,8 +677,6 @@ __global__ __launch_bounds__(512, 1) void prefill_attn(PrefillArgs a)
     const bool wact = w_r0 < a.rows;
     const uint64_t wg_rend = wg_r0 + 32 * RB < a.rows ? wg_r0 + 32 * RB : a.rows;
     const int ntiles = static_cast<int>((a.past + wg_rend + kKeyTile - 1) / kKeyTile);
-    const uint64_t w_kend = wact ? a.past + (w_r0 + 32 < a.rows ? w_r0 + 32 : a.rows) : 0;
-    const int wtiles = static_cast<int>((w_kend + kKeyTile - 1) / kKeyTile);  // tiles the wave computes
     const int nfull = wact ? static_cast<int>((a.past + w_r0 + 1) / kKeyTile) : 0;  // no mask needed
     const uint64_t lim = a.past + row;                         // last visible key of this row
 
@@ -701,35 +701,36 @@ __global__ __launch_bounds__(512, 1) void prefill_attn(PrefillArgs a)
         return acc;
     };
 
+    // Every wave computes every tile of the workgroup's key range: tiles past
+    // a wave's last visible key take the masked path and contribute nothing.
+    // With no wave-dependent branches around them, the loads of the next
+    // tiles stay in flight across the compute.
+
     // pass 1: exact row maxima (of the unscaled dot products when POW2).
-    // Out-of-range keys of the last tile load row 0 and are never visible.
+    // Out-of-range keys of the last tile read row 0 and are never visible.
     tile_lstore_padded<D, 512>(kb[0], SK, tid, kr);
     __syncthreads();
     float m = kNegInf;
     for (int t = 0; t < ntiles; t++) {
         const uint64_t t0 = static_cast<uint64_t>(t) * kKeyTile;
-        if (t + 1 < ntiles) tile_gload<D, 512>(kg, t0 + kKeyTile, a.n, tid, kr);
-        else {
-            tile_gload<D, 512>(kg, 0, a.n, tid, kr);          // pass 2's first tile
-            tile_gload<D, 512>(vg, 0, a.n, tid, vr);
-        }
+        const bool last = t + 1 == ntiles;
+        tile_gload<D, 512>(kg, last ? 0 : t0 + kKeyTile, a.n, tid, kr);   // after the last: pass 2's first tile
+        if (last) tile_gload<D, 512>(vg, 0, a.n, tid, vr);
         __builtin_amdgcn_sched_barrier(0);
-        if (t < wtiles) {
-            const f32x16 acc = qk(kb[t & 1]);
-            if (t < nfull) {
+        const f32x16 acc = qk(kb[t & 1]);
+        if (t < nfull) {
 #pragma unroll
-                for (int r = 0; r < 16; r++) m = __builtin_fmaxf(m, POW2 ? acc[r] : acc[r] * a.scale);
-            } else {
-                // keys t0 + k with k <= vis are visible to this row
-                const int vis = static_cast<int>(static_cast<int64_t>(lim) - static_cast<int64_t>(t0));
+            for (int r = 0; r < 16; r++) m = __builtin_fmaxf(m, POW2 ? acc[r] : acc[r] * a.scale);
+        } else {
+            // keys t0 + k with k <= vis are visible to this row
+            const int vis = static_cast<int>(static_cast<int64_t>(lim) - static_cast<int64_t>(t0));
 #pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    const float s = POW2 ? acc[r] : acc[r] * a.scale;
-                    if (key_of(r, grp) <= vis) m = __builtin_fmaxf(m, s);
-                }
+            for (int r = 0; r < 16; r++) {
+                const float s = POW2 ? acc[r] : acc[r] * a.scale;
+                if (key_of(r, grp) <= vis) m = __builtin_fmaxf(m, s);
             }
         }
-        if (t + 1 < ntiles) tile_lstore_padded<D, 512>(kb[(t + 1) & 1], SK, tid, kr);
+        if (!last) tile_lstore_padded<D, 512>(kb[(t + 1) & 1], SK, tid, kr);
         __syncthreads();
     }
     m = __builtin_fmaxf(m, __shfl_xor(m, 32));
@@ -739,7 +740,9 @@ __global__ __launch_bounds__(512, 1) void prefill_attn(PrefillArgs a)
     ex.clamp = POW2 ? -87.33654f / a.scale : -87.33654f;
     ex.mul = POW2 ? 1.442695f * a.scale : 1.442695f;
 
-    // pass 2: exponentials at the exact maximum, P.V with P = hi + lo
+    // pass 2: exponentials at the exact maximum, P.V with P = hi + lo. The
+    // next K tile is loaded first, the next V tile after the first half's
+    // softmax, so that their staging registers are not live at the peak.
     tile_lstore_padded<D, 512>(kb[0], SK, tid, kr);
     tile_mask<D, 512>(0, a.n, tid, vr);
     tile_lstore_padded<D, 512>(vb[0], SV, tid, vr);
@@ -751,42 +754,42 @@ __global__ __launch_bounds__(512, 1) void prefill_attn(PrefillArgs a)
     for (int t = 0; t < ntiles; t++) {
         const uint64_t t0 = static_cast<uint64_t>(t) * kKeyTile;
         const int b = t & 1;
-        // The next K tile is loaded now, the next V tile after the softmax:
-        // their staging registers are then never live together with both the
-        // scores and the P operands.
-        if (t + 1 < ntiles) tile_gload<D, 512>(kg, t0 + kKeyTile, a.n, tid, kr);
+        tile_gload<D, 512>(kg, t0 + kKeyTile, a.n, tid, kr);  // past the end: row 0, unused
         __builtin_amdgcn_sched_barrier(0);
-        if (t < wtiles) {
-            const f32x16 acc = qk(kb[b]);
-            const bool full = t < nfull;
-            const int vis = full ? 64 : static_cast<int>(static_cast<int64_t>(lim) - static_cast<int64_t>(t0));
-            // Each half of the 32 keys is exponentiated, split and multiplied
-            // in turn, so that only one half's P operands are live.
+        const f32x16 acc = qk(kb[b]);
+        const bool full = t < nfull;
+        const int vis = static_cast<int>(static_cast<int64_t>(lim) - static_cast<int64_t>(t0));
+        // exponentials of one half of the tile's keys as hi and lo operands
+        auto half = [&](int h, auto masked, u32x4 &hi, u32x4 &lo) {
+            constexpr bool MASKED = decltype(masked)::value;
+            float ev[8];
 #pragma unroll
-            for (int h = 0; h < 2; h++) {
-                float ev[8];
-#pragma unroll
-                for (int r = 0; r < 8; r++) {
-                    const float e = exp_score<POW2>(acc[8 * h + r], ex);
-                    ev[r] = full || key_of(8 * h + r, grp) <= vis ? e : 0.0f;
-                    lsum += ev[r];
-                }
-                u32x4 hi, lo;
-                split_pack_hw(ev, hi, lo);
-                if (h == 0) {
-                    if (t + 1 < ntiles) tile_gload<D, 512>(vg, t0 + kKeyTile, a.n, tid, vr);
-                    __builtin_amdgcn_sched_barrier(0);
-                }
-#pragma unroll
-                for (int dt = 0; dt < D / 32; dt++) {
-                    const u32x4 av = vt_operand_padded<D>(vb[b], 16 * h, 32 * dt, l);
-                    o[dt] = mfma(av, hi, o[dt]);
-                    o[dt] = mfma(av, lo, o[dt]);
-                }
+            for (int r = 0; r < 8; r++) {
+                const float e = exp_score<POW2>(acc[8 * h + r], ex);
+                ev[r] = !MASKED || key_of(8 * h + r, grp) <= vis ? e : 0.0f;
+                lsum += ev[r];
             }
-        } else if (t + 1 < ntiles) {
-            tile_gload<D, 512>(vg, t0 + kKeyTile, a.n, tid, vr);
-        }
+            split_pack_hw(ev, hi, lo);
+        };
+        auto pv = [&](int h, const u32x4 &hi, const u32x4 &lo) {
+            __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+            for (int dt = 0; dt < D / 32; dt++) {
+                const u32x4 av = vt_operand_padded<D>(vb[b], 16 * h, 32 * dt, l);
+                o[dt] = mfma(av, hi, o[dt]);
+                o[dt] = mfma(av, lo, o[dt]);
+            }
+            __builtin_amdgcn_s_setprio(0);
+        };
+        u32x4 hi, lo;
+        if (full) half(0, std::false_type{}, hi, lo);
+        else half(0, std::true_type{}, hi, lo);
+        tile_gload<D, 512>(vg, t0 + kKeyTile, a.n, tid, vr);
+        __builtin_amdgcn_sched_barrier(0);
+        pv(0, hi, lo);
+        if (full) half(1, std::false_type{}, hi, lo);
+        else half(1, std::true_type{}, hi, lo);
+        pv(1, hi, lo);
         if (t + 1 < ntiles) {
             tile_lstore_padded<D, 512>(kb[b ^ 1], SK, tid, kr);
             tile_mask<D, 512>(t0 + kKeyTile, a.n, tid, vr);
