@@ -31,6 +31,17 @@ sys.path.insert(0, os.path.join(ROOT, "herbert-jit-bf16_amd"))
 HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, GB/s
 MFMA_BF16_PEAK_TFS = 2500.0  # MI355X dense bf16 MFMA, TFLOP/s
 
+# Memory traffic per call, from rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE runs
+# of this script (KiB per dispatch, summed over the kernels of one call).
+# FETCH_SIZE is scaled by 2 and WRITE_SIZE by 1: a 256 MiB device copy reads
+# 131 086 KiB and writes 262 144 KiB on these counters. FETCH_SIZE counts
+# every L2 fill from the memory fabric, so Infinity Cache hits are included.
+# Summary and commands: profiles/pmc_traffic_decode32k_prefill4096.md
+TRAFFIC_BYTES = {
+    "decode_32k": (2 * (16452.3 + 17547.9 + 1087.9) + (2176.4 + 2056.0 + 8.0)) * 1024,
+    "prefill_4096_after_8192": (2 * 1267085.2 + 35840.0) * 1024,
+}
+
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
@@ -189,7 +200,7 @@ def main():
                                "32768 cached keys, bf16 q/K/V/out, f32 accumulation, scale 1/16",
                    "algorithmic_bytes": dec_bytes, "kv_caches_rotated": 16, "timing": "HIP graph of the timed steps"},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": round(TRAFFIC_BYTES["decode_32k"]),
                      "kernel": "decode step (decode_qk + decode_pv + decode_combine)"},
     }
 
@@ -213,7 +224,8 @@ def main():
                                    "16 query heads on 2 KV heads, head_dim 256, scale 1/16",
                        "algorithmic_flops": flops},
             "roofline": {"bound": "mfma", "achieved": round(tfs, 2), "peak": MFMA_BF16_PEAK_TFS, "unit": "TFLOP/s",
-                         "frac": round(tfs / MFMA_BF16_PEAK_TFS, 4), "traffic": None,
+                         "frac": round(tfs / MFMA_BF16_PEAK_TFS, 4),
+                         "traffic": round(TRAFFIC_BYTES["prefill_4096_after_8192"]),
                          "kernel": "prefill_attn"},
         }
         del ks, vs, q, out
