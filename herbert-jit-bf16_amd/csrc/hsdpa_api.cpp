@@ -69,9 +69,57 @@ hsdpa_status check_device()
     return g_dev_state[dev] == 1 ? HSDPA_OK : HSDPA_ERR_NO_DEVICE;
 }
 
+// KvSpec::validate (src/jit/execution/abi.rs:74-103) and the x86 refusal of
+// the R16 copies (src/jit/target/x86/execution/kv.rs:17-21).
+hsdpa_status check_kv_spec(const hsdpa_kv_spec &s)
+{
+    if (s.heads == 0 || s.head_dim == 0 || s.max_batch == 0) return HSDPA_ERR_EMPTY;
+    if (s.capacity < s.max_batch) return HSDPA_ERR_CAPACITY;
+    const uint64_t i32 = static_cast<uint64_t>(INT32_MAX);
+    if (s.stride > i32 / 2) return HSDPA_ERR_STRIDE;
+    if (s.capacity > s.stride / s.head_dim || s.capacity * s.head_dim > s.stride) return HSDPA_ERR_STRIDE;
+    if (s.heads > i32 || s.heads * s.head_dim > i32 / 2) return HSDPA_ERR_STRIDE;
+    if (s.r16 != 0) return HSDPA_ERR_LAYOUT;
+    return HSDPA_OK;
+}
+
 }  // namespace
 
 extern "C" {
+
+hsdpa_status hsdpa_kv_check(const hsdpa_kv_spec *spec)
+{
+    if (!spec) return HSDPA_ERR_NULL;
+    return check_kv_spec(*spec);
+}
+
+hsdpa_status hsdpa_kv_append(const hsdpa_kv_spec *spec, const hsdpa_kv_call *call, void *stream)
+{
+    if (!spec || !call) return HSDPA_ERR_NULL;
+    const hsdpa_status st = check_kv_spec(*spec);
+    if (st != HSDPA_OK) return st;
+    if (call->rows == 0) return HSDPA_OK;                        // kv.rs:33-34
+    if (call->rows > spec->max_batch) return HSDPA_ERR_BATCH;
+    if (call->past > spec->capacity || call->rows > spec->capacity - call->past) return HSDPA_ERR_CAPACITY;
+    if (!call->keys || !call->values || !call->input_keys || !call->input_values) return HSDPA_ERR_NULL;
+    const hsdpa_status dv = check_device();
+    if (dv != HSDPA_OK) return dv;
+    hsdpa::KvAppendArgs a;
+    a.keys = call->keys;
+    a.values = call->values;
+    a.in_keys = call->input_keys;
+    a.in_values = call->input_values;
+    a.rows = call->rows;
+    a.past = call->past;
+    a.heads = spec->heads;
+    a.head_dim = spec->head_dim;
+    a.stride = spec->stride;
+    const bool vec = spec->head_dim % 8 == 0 && spec->stride % 8 == 0 && aligned16(call->keys) &&
+                     aligned16(call->values) && aligned16(call->input_keys) && aligned16(call->input_values);
+    if (hsdpa::launch_kv_append(a, vec, static_cast<hipStream_t>(stream)) != hipSuccess) return HSDPA_ERR_HIP;
+    return HSDPA_OK;
+}
+
 
 hsdpa_status hsdpa_plan_create(const hsdpa_spec *spec, hsdpa_plan **out)
 {
@@ -184,6 +232,8 @@ const char *hsdpa_status_string(hsdpa_status status)
     case HSDPA_ERR_NULL: return "null pointer";
     case HSDPA_ERR_HIP: return "HIP launch or runtime error";
     case HSDPA_ERR_NO_DEVICE: return "no gfx950 device is current";
+    case HSDPA_ERR_BATCH: return "more rows than the reserve's max_batch";
+    case HSDPA_ERR_LAYOUT: return "the R16 copies of the KV cache are an AArch64 layout";
     }
     return "unknown status";
 }

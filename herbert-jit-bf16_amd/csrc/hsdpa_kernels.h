@@ -45,7 +45,15 @@ constexpr int kDecodeKeysQK = 128;    // keys per decode pass-1 workgroup (4 wav
 constexpr int kDecodeKeysPV = 256;    // keys per decode pass-2 workgroup (8 waves x 1 tile)
 constexpr int kDecodeMaxGroup = 16;   // query heads per KV head the decode kernels take
 
+// KV append: token-major block rows into the head-major cache.
+struct KvAppendArgs {
+    uint16_t *keys, *values;
+    const uint16_t *in_keys, *in_values;
+    uint64_t rows, past, heads, head_dim, stride;
+};
+
 bool head_dim_supported(int d);
+hipError_t launch_kv_append(const KvAppendArgs &a, bool vec, hipStream_t s);
 hipError_t launch_decode(const DecodeArgs &a, int head_dim, int kv_heads, hipStream_t s);
 hipError_t launch_prefill(const PrefillArgs &a, int head_dim, int heads, hipStream_t s);
 

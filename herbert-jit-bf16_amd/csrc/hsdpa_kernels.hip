@@ -813,6 +813,38 @@ __global__ __launch_bounds__(512, 1) void prefill_attn(PrefillArgs a)
 }
 
 // ---------------------------------------------------------------------------
+// KV append (src/jit/target/x86/execution/kv.rs:15-69): row r of KV head h of
+// the token-major block, (r*heads + h)*head_dim, to position past + r of head
+// h, h*stride + (past + r)*head_dim. The source is one contiguous run, so
+// element e of it maps to (r, h, d) = (e / (heads*hd), e / hd % heads, e % hd).
+// Vector path: 16 bytes per lane (head_dim and stride multiples of 8, pointers
+// 16-byte aligned); otherwise one bf16 per lane. Grid-stride over the block.
+// ---------------------------------------------------------------------------
+template <bool VEC>
+__global__ __launch_bounds__(256) void kv_append(KvAppendArgs a)
+{
+    constexpr uint64_t W = VEC ? 8 : 1;                          // elements per lane
+    const uint64_t per_row = a.heads * a.head_dim;
+    const uint64_t total = a.rows * per_row / W;
+    for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
+         i += static_cast<uint64_t>(gridDim.x) * blockDim.x) {
+        const uint64_t e = i * W;
+        const uint64_t r = e / per_row, rem = e - r * per_row;
+        const uint64_t h = rem / a.head_dim, d = rem - h * a.head_dim;
+        const uint64_t dst = h * a.stride + (a.past + r) * a.head_dim + d;
+        if (VEC) {
+            const u32x4 kv = *reinterpret_cast<const u32x4 *>(a.in_keys + e);
+            const u32x4 vv = *reinterpret_cast<const u32x4 *>(a.in_values + e);
+            *reinterpret_cast<u32x4 *>(a.keys + dst) = kv;
+            *reinterpret_cast<u32x4 *>(a.values + dst) = vv;
+        } else {
+            a.keys[dst] = a.in_keys[e];
+            a.values[dst] = a.in_values[e];
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // launchers
 // ---------------------------------------------------------------------------
 bool head_dim_supported(int d) { return d == 64 || d == 128 || d == 256; }
@@ -861,6 +893,16 @@ static void prefill_d(const PrefillArgs &a, int heads, hipStream_t s)
     else if (a.gqa % 4 == 0) prefill_dh<D, 4>(a, heads, s);
     else if (a.gqa % 2 == 0) prefill_dh<D, 2>(a, heads, s);
     else prefill_dh<D, 1>(a, heads, s);
+}
+
+hipError_t launch_kv_append(const KvAppendArgs &a, bool vec, hipStream_t s)
+{
+    const uint64_t total = a.rows * a.heads * a.head_dim / (vec ? 8 : 1);
+    const uint64_t wgs = (total + 255) / 256;
+    const dim3 grid(static_cast<unsigned>(wgs < 16384 ? wgs : 16384));
+    if (vec) hipLaunchKernelGGL(kv_append<true>, grid, dim3(256), 0, s, a);
+    else hipLaunchKernelGGL(kv_append<false>, grid, dim3(256), 0, s, a);
+    return hipGetLastError();
 }
 
 hipError_t launch_prefill(const PrefillArgs &a, int head_dim, int heads, hipStream_t s)

@@ -8,4 +8,5 @@ workloads (workloads.py) used by the tests and the benchmark.
 from . import workloads  # noqa: F401
 from .binding import (  # noqa: F401
     HsdpaError, Plan, Spec, Call, STATUS, library, library_path, attention_torch,
+    KvSpec, KvCall, kv_spec, kv_append_raw, kv_append_torch,
 )

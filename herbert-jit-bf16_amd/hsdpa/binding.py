@@ -19,10 +19,10 @@ STATUS = {
     0: "HSDPA_OK", 1: "HSDPA_ERR_EMPTY", 2: "HSDPA_ERR_HEAD_DIM", 3: "HSDPA_ERR_GQA",
     4: "HSDPA_ERR_STRIDE", 5: "HSDPA_ERR_SINK_UNSUPPORTED", 6: "HSDPA_ERR_CAPACITY",
     7: "HSDPA_ERR_WORKSPACE", 8: "HSDPA_ERR_ALIGNMENT", 9: "HSDPA_ERR_NULL", 10: "HSDPA_ERR_HIP",
-    11: "HSDPA_ERR_NO_DEVICE",
+    11: "HSDPA_ERR_NO_DEVICE", 12: "HSDPA_ERR_BATCH", 13: "HSDPA_ERR_LAYOUT",
 }
 EXPORTS = ["hsdpa_plan_create", "hsdpa_plan_destroy", "hsdpa_workspace_bytes", "hsdpa_attention",
-           "hsdpa_status_string", "hsdpa_version"]
+           "hsdpa_status_string", "hsdpa_version", "hsdpa_kv_check", "hsdpa_kv_append"]
 
 
 class HsdpaError(RuntimeError):
@@ -44,6 +44,19 @@ class Call(ctypes.Structure):
                 ("output", ctypes.c_void_p), ("rows", ctypes.c_uint64), ("past", ctypes.c_uint64),
                 ("scale", ctypes.c_float), ("sink", ctypes.c_float), ("workspace", ctypes.c_void_p),
                 ("workspace_bytes", ctypes.c_uint64)]
+
+
+class KvSpec(ctypes.Structure):
+    """KvSpec (src/jit/execution/abi.rs:57-73)."""
+    _fields_ = [("heads", ctypes.c_uint64), ("head_dim", ctypes.c_uint64), ("stride", ctypes.c_uint64),
+                ("capacity", ctypes.c_uint64), ("max_batch", ctypes.c_uint64), ("r16", ctypes.c_uint32),
+                ("reserved", ctypes.c_uint32)]
+
+
+class KvCall(ctypes.Structure):
+    """KvCall (src/jit/execution/abi.rs:105-130), rows and past by value."""
+    _fields_ = [("keys", ctypes.c_void_p), ("values", ctypes.c_void_p), ("input_keys", ctypes.c_void_p),
+                ("input_values", ctypes.c_void_p), ("rows", ctypes.c_uint64), ("past", ctypes.c_uint64)]
 
 
 def library_path() -> str:
@@ -69,6 +82,10 @@ def library():
         L.hsdpa_status_string.argtypes = [ctypes.c_int]
         L.hsdpa_status_string.restype = ctypes.c_char_p
         L.hsdpa_version.restype = ctypes.c_uint32
+        L.hsdpa_kv_check.argtypes = [ctypes.POINTER(KvSpec)]
+        L.hsdpa_kv_check.restype = ctypes.c_int
+        L.hsdpa_kv_append.argtypes = [ctypes.POINTER(KvSpec), ctypes.POINTER(KvCall), ctypes.c_void_p]
+        L.hsdpa_kv_append.restype = ctypes.c_int
         _lib = L
     return _lib
 
@@ -129,3 +146,36 @@ def attention_torch(plan: Plan, q, k, v, out, rows: int, past: int, scale: float
     s = torch.cuda.current_stream() if stream is None else stream
     plan.attention_raw(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), rows, past, scale,
                        workspace.data_ptr(), workspace.numel() * workspace.element_size(), s.cuda_stream)
+
+
+def kv_spec(heads: int, head_dim: int, capacity: int, max_batch: int, stride: int | None = None,
+            r16: bool = False) -> KvSpec:
+    """A KV reserve geometry, validated like KvSpec::validate (raises HsdpaError)."""
+    spec = KvSpec(heads, head_dim, capacity * head_dim if stride is None else stride, capacity, max_batch,
+                  int(r16), 0)
+    rc = library().hsdpa_kv_check(ctypes.byref(spec))
+    if rc != 0:
+        raise HsdpaError(rc, "hsdpa_kv_check")
+    return spec
+
+
+def kv_append_raw(spec: KvSpec, keys: int, values: int, input_keys: int, input_values: int, rows: int,
+                  past: int, stream: int = 0) -> None:
+    call = KvCall(keys, values, input_keys, input_values, rows, past)
+    rc = library().hsdpa_kv_append(ctypes.byref(spec), ctypes.byref(call), ctypes.c_void_p(stream))
+    if rc != 0:
+        raise HsdpaError(rc, "hsdpa_kv_append")
+
+
+def kv_append_torch(spec: KvSpec, keys, values, input_keys, input_values, rows: int, past: int,
+                    stream=None) -> None:
+    """The kv-append node on torch device tensors holding bf16 bits. Views at
+    any element offset are accepted (unaligned ones take the scalar path)."""
+    import torch
+
+    for t in (keys, values, input_keys, input_values):
+        if not t.is_cuda:
+            raise ValueError("tensors must be device tensors")
+    s = torch.cuda.current_stream() if stream is None else stream
+    kv_append_raw(spec, keys.data_ptr(), values.data_ptr(), input_keys.data_ptr(), input_values.data_ptr(),
+                  rows, past, s.cuda_stream)

@@ -22,6 +22,14 @@
  *                           entry loop (src/jit/target/x86/execution/entry.rs:437-483)
  *   hsdpa_status            Decline (src/jit/ir.rs:177-230) and
  *                           ExecutionError (attention.rs:86-98)
+ *   hsdpa_kv_spec           KvSpec, src/jit/execution/abi.rs:57-73
+ *   hsdpa_kv_call           KvCall, src/jit/execution/abi.rs:105-130
+ *   hsdpa_kv_check          KvSpec::validate, abi.rs:74-103, and the x86
+ *                           refusal of the R16 copies
+ *                           (src/jit/target/x86/execution/kv.rs:17-21)
+ *   hsdpa_kv_append         the kv-append node (src/jit/schedule/lowering.rs:578-592):
+ *                           every task of append
+ *                           (src/jit/target/x86/execution/kv.rs:15-69)
  *
  * All strides are in bf16 elements, like the reference. All pointers are
  * device pointers (HBM) except the spec/call/plan structs themselves, which
@@ -55,7 +63,9 @@ typedef enum hsdpa_status {
     HSDPA_ERR_ALIGNMENT = 8,        /* a pointer or stride not 16-byte aligned */
     HSDPA_ERR_NULL = 9,             /* a required pointer is null */
     HSDPA_ERR_HIP = 10,             /* a HIP launch or runtime call failed */
-    HSDPA_ERR_NO_DEVICE = 11        /* no gfx950 device current */
+    HSDPA_ERR_NO_DEVICE = 11,       /* no gfx950 device current */
+    HSDPA_ERR_BATCH = 12,           /* kv append: rows > max_batch (the frame's bound) */
+    HSDPA_ERR_LAYOUT = 13           /* kv append: the R16 copies, an AArch64 layout (kv.rs:19-21) */
 } hsdpa_status;
 
 /* Per-layer geometry, fixed at mount (AttentionSpec + cache reserve). */
@@ -104,6 +114,38 @@ uint64_t hsdpa_workspace_bytes(const hsdpa_plan *plan);
  * NULL is the default stream). Validation happens on the host before any
  * launch; nothing is allocated. */
 hsdpa_status hsdpa_attention(const hsdpa_plan *plan, const hsdpa_call *call, void *stream);
+
+/* ---- KV append: the node before the attention ------------------------------
+ * The keys and values of the current block, token-major (row r, KV head h at
+ * input + (r*heads + h)*head_dim), copied into the head-major cache at
+ * position past + r of head h (cache + h*stride + (past + r)*head_dim). */
+typedef struct hsdpa_kv_spec {
+    uint64_t heads;        /* KV heads */
+    uint64_t head_dim;     /* elements per head */
+    uint64_t stride;       /* elements reserved per KV head (>= capacity*head_dim) */
+    uint64_t capacity;     /* positions reserved per KV head */
+    uint64_t max_batch;    /* maximum rows in one block */
+    uint32_t r16;          /* KvSpec::r16: must be 0 */
+    uint32_t reserved;     /* 0 */
+} hsdpa_kv_spec;
+
+typedef struct hsdpa_kv_call {
+    uint16_t *keys;               /* head-major cache */
+    uint16_t *values;             /* head-major cache, same layout */
+    const uint16_t *input_keys;   /* the block's token-major keys */
+    const uint16_t *input_values; /* the block's token-major values */
+    uint64_t rows;                /* rows of the block; 0 = nothing */
+    uint64_t past;                /* absolute position of the block's first row */
+} hsdpa_kv_call;
+
+/* Mount-time validation of the reserve geometry (KvSpec::validate). */
+hsdpa_status hsdpa_kv_check(const hsdpa_kv_spec *spec);
+
+/* The append, enqueued on `stream`. Checks the geometry and the call
+ * (rows <= max_batch, past + rows <= capacity, non-null pointers) on the host
+ * before any launch. Any alignment is accepted; 16-byte aligned pointers with
+ * head_dim and stride multiples of 8 take the vector path. */
+hsdpa_status hsdpa_kv_append(const hsdpa_kv_spec *spec, const hsdpa_kv_call *call, void *stream);
 
 /* Static, human-readable name of a status. */
 const char *hsdpa_status_string(hsdpa_status status);
