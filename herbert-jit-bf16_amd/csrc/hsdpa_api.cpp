@@ -87,6 +87,71 @@ hsdpa_status check_kv_spec(const hsdpa_kv_spec &s)
 
 extern "C" {
 
+// norm_rope's checks (transforms.rs:38-40), the element kernels' shapes (a
+// multiple of 32 elements, emit_elem.rs spec.check) and the binding's strides.
+static hsdpa_status check_norm_rope(const hsdpa_norm_rope_spec &s)
+{
+    if (s.heads == 0 || s.head_dim == 0) return HSDPA_ERR_EMPTY;
+    if (s.head_dim % 32 != 0 || s.head_dim > 512) return HSDPA_ERR_HEAD_DIM;
+    if (s.rotary_dims % 32 != 0 || s.rotary_dims > s.head_dim) return HSDPA_ERR_HEAD_DIM;
+    const uint64_t i32 = static_cast<uint64_t>(INT32_MAX);
+    if (s.heads > i32 || s.head_stride > i32 / 2 || s.row_stride > i32 / 2) return HSDPA_ERR_STRIDE;
+    if (s.head_stride < s.head_dim || s.heads * s.head_stride > s.row_stride) return HSDPA_ERR_STRIDE;
+    if (s.rotary_dims && s.table_row < s.rotary_dims / 2) return HSDPA_ERR_STRIDE;
+    return HSDPA_OK;
+}
+
+hsdpa_status hsdpa_head_norm_rope(const hsdpa_norm_rope_spec *spec, const hsdpa_norm_rope_call *call, void *stream)
+{
+    if (!spec || !call) return HSDPA_ERR_NULL;
+    const hsdpa_status st = check_norm_rope(*spec);
+    if (st != HSDPA_OK) return st;
+    if (call->rows == 0) return HSDPA_OK;
+    if (call->rows > (1u << 31) - 1) return HSDPA_ERR_CAPACITY;
+    if (spec->rotary_dims && (call->past > spec->positions || call->rows > spec->positions - call->past))
+        return HSDPA_ERR_CAPACITY;
+    if (!call->data || !call->weight || (spec->rotary_dims && (!call->cos || !call->sin))) return HSDPA_ERR_NULL;
+    const hsdpa_status dv = check_device();
+    if (dv != HSDPA_OK) return dv;
+    hsdpa::NormRopeArgs a;
+    a.data = call->data;
+    a.w = call->weight;
+    a.cos = call->cos;
+    a.sin = call->sin;
+    a.rows = call->rows;
+    a.past = call->past;
+    a.row_stride = spec->row_stride;
+    a.head_stride = spec->head_stride;
+    a.table_row = spec->table_row;
+    a.heads = static_cast<int>(spec->heads);
+    a.dim = static_cast<int>(spec->head_dim);
+    a.rotary = static_cast<int>(spec->rotary_dims);
+    a.plus_one = spec->plus_one ? 1 : 0;
+    a.eps = call->eps;
+    if (hsdpa::launch_norm_rope(a, static_cast<hipStream_t>(stream)) != hipSuccess) return HSDPA_ERR_HIP;
+    return HSDPA_OK;
+}
+
+hsdpa_status hsdpa_output_gate(const hsdpa_gate_spec *spec, const hsdpa_gate_call *call, void *stream)
+{
+    if (!spec || !call) return HSDPA_ERR_NULL;
+    if (spec->width == 0) return HSDPA_ERR_EMPTY;
+    if (spec->attn_row < spec->width || spec->gate_row < spec->width) return HSDPA_ERR_STRIDE;
+    if (call->rows == 0) return HSDPA_OK;
+    if (!call->attn || !call->gate) return HSDPA_ERR_NULL;
+    const hsdpa_status dv = check_device();
+    if (dv != HSDPA_OK) return dv;
+    hsdpa::GateArgs a;
+    a.attn = call->attn;
+    a.gate = call->gate;
+    a.rows = call->rows;
+    a.width = spec->width;
+    a.attn_row = spec->attn_row;
+    a.gate_row = spec->gate_row;
+    if (hsdpa::launch_gate(a, static_cast<hipStream_t>(stream)) != hipSuccess) return HSDPA_ERR_HIP;
+    return HSDPA_OK;
+}
+
 hsdpa_status hsdpa_kv_check(const hsdpa_kv_spec *spec)
 {
     if (!spec) return HSDPA_ERR_NULL;

@@ -52,7 +52,25 @@ struct KvAppendArgs {
     uint64_t rows, past, heads, head_dim, stride;
 };
 
+// Head RMS norm + RoPE, one wave per (row, head).
+struct NormRopeArgs {
+    uint16_t *data;
+    const uint16_t *w, *cos, *sin;
+    uint64_t rows, past, row_stride, head_stride, table_row;
+    int heads, dim, rotary, plus_one;
+    float eps;
+};
+
+// Output gate: attn <- attn / (1 + exp(min(-gate, 88))).
+struct GateArgs {
+    uint16_t *attn;
+    const uint16_t *gate;
+    uint64_t rows, width, attn_row, gate_row;
+};
+
 bool head_dim_supported(int d);
+hipError_t launch_norm_rope(const NormRopeArgs &a, hipStream_t s);
+hipError_t launch_gate(const GateArgs &a, hipStream_t s);
 hipError_t launch_kv_append(const KvAppendArgs &a, bool vec, hipStream_t s);
 hipError_t launch_decode(const DecodeArgs &a, int head_dim, int kv_heads, hipStream_t s);
 hipError_t launch_prefill(const PrefillArgs &a, int head_dim, int heads, hipStream_t s);

@@ -845,6 +845,112 @@ __global__ __launch_bounds__(256) void kv_append(KvAppendArgs a)
 }
 
 // ---------------------------------------------------------------------------
+// Head RMS norm + RoPE (the head-norm-rope node, transforms.rs:32-81), one wave
+// per (row, head), restating the AVX-512 element kernels bit for bit:
+//  * sum of squares (emit_elem.rs:251-271): vdpbf16ps(x, x) per block of 32
+//    into chain c % min(4, blocks), 16 f32 lanes per chain; chain c lives in
+//    lanes 16c .. 16c+15, lane L of a chain takes elements 2L+1 then 2L of each
+//    block (bf16 inputs denormals-as-zero, each product exact, one rounding per
+//    add, results flushed to zero); chains added in order, then the hsum tree;
+//  * scalar: * fl(1/dim), + eps, correctly rounded sqrt, 1 / that;
+//  * y = bf16((x * inv) * w'), w' = w or w + 1 (emit_elem.rs:302-334);
+//  * rotate_half RoPE on the normalised bf16 values (emit_elem.rs:479-520):
+//    a' = fma(-b, s, a c), b' = fma(b, c, a s).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float bf16_daz(uint16_t b)
+{
+    return __uint_as_float((b & 0x7F80u) ? static_cast<uint32_t>(b) << 16 : static_cast<uint32_t>(b & 0x8000u) << 16);
+}
+
+__device__ __forceinline__ float ftz(float x)
+{
+    const uint32_t b = __float_as_uint(x);
+    return (b & 0x7F800000u) ? x : __uint_as_float(b & 0x80000000u);
+}
+
+__device__ __forceinline__ float bf16f(uint16_t b) { return __uint_as_float(static_cast<uint32_t>(b) << 16); }
+
+__global__ __launch_bounds__(64) void head_norm_rope(NormRopeArgs a)
+{
+    __shared__ uint16_t ybuf[512];
+    const int l = threadIdx.x, c = l >> 4, L = l & 15;
+    const uint64_t row = blockIdx.x;
+    uint16_t *x = a.data + row * a.row_stride + static_cast<uint64_t>(blockIdx.y) * a.head_stride;
+    const int nb = a.dim / 32, nacc = nb < 4 ? nb : 4;
+    float acc = 0.0f;
+    if (c < nacc)
+        for (int b = c; b < nb; b += nacc) {
+            const float x1 = bf16_daz(x[32 * b + 2 * L + 1]), x0 = bf16_daz(x[32 * b + 2 * L]);
+            acc = ftz(__builtin_fmaf(x1, x1, acc));
+            acc = ftz(__builtin_fmaf(x0, x0, acc));
+        }
+    // chains 1..3 added in order into chain 0
+    const float c1 = __shfl(acc, L + 16), c2 = __shfl(acc, L + 32), c3 = __shfl(acc, L + 48);
+    float s = acc;
+    if (nacc > 1) s = s + c1;
+    if (nacc > 2) s = s + c2;
+    if (nacc > 3) s = s + c3;
+    // the hsum tree over the 16 lanes of chain 0, in every lane
+    float lv[16];
+#pragma unroll
+    for (int i = 0; i < 16; i++) lv[i] = __shfl(s, i);
+    float h8[8], h4[4];
+#pragma unroll
+    for (int i = 0; i < 8; i++) h8[i] = lv[i] + lv[i + 8];
+#pragma unroll
+    for (int i = 0; i < 4; i++) h4[i] = h8[i] + h8[i + 4];
+    const float u0 = h4[0] + h4[1], u1 = h4[2] + h4[3];
+    float ms = u0 + u1;
+    ms = ms * (1.0f / static_cast<float>(a.dim));
+    ms = ms + a.eps;
+    const float inv = 1.0f / __builtin_sqrtf(ms);
+    for (int i = l; i < a.dim; i += 64) {
+        float ww = bf16f(a.w[i]);
+        if (a.plus_one) ww = ww + 1.0f;
+        float v = bf16f(x[i]) * inv;
+        v = v * ww;
+        ybuf[i] = static_cast<uint16_t>(cvt_out(v));
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const int half = a.rotary / 2;
+    const uint16_t *cs = a.cos + (a.past + row) * a.table_row;
+    const uint16_t *sn = a.sin + (a.past + row) * a.table_row;
+    for (int i = l; i < a.dim; i += 64) {
+        uint16_t out = ybuf[i];
+        if (i < a.rotary) {
+            const int j = i < half ? i : i - half;
+            const float av = bf16f(ybuf[j]), bv = bf16f(ybuf[j + half]);
+            const float cv = bf16f(cs[j]), sv = bf16f(sn[j]);
+            const float r = i < half ? __builtin_fmaf(-bv, sv, av * cv) : __builtin_fmaf(bv, cv, av * sv);
+            out = static_cast<uint16_t>(cvt_out(r));
+        }
+        x[i] = out;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Output gate (ElemOp::SigmoidMul, emit_elem.rs:350-440): e = 0 - g;
+// e = e < 88 ? e : 88 (vminps: the bound when e is NaN); the softmax's
+// exponential; y = bf16(a / (e + 1)). Grid-stride over rows x width.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void output_gate(GateArgs a)
+{
+    const uint64_t total = a.rows * a.width;
+    for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
+         i += static_cast<uint64_t>(gridDim.x) * blockDim.x) {
+        const uint64_t r = i / a.width, c = i - r * a.width;
+        uint16_t *ap = a.attn + r * a.attn_row + c;
+        float e = 0.0f - bf16f(a.gate[r * a.gate_row + c]);
+        e = e < 88.0f ? e : 88.0f;
+        e = exp_poly(e);
+        e = e + 1.0f;
+        *ap = static_cast<uint16_t>(cvt_out(bf16f(*ap) / e));
+    }
+}
+
+// ---------------------------------------------------------------------------
 // launchers
 // ---------------------------------------------------------------------------
 bool head_dim_supported(int d) { return d == 64 || d == 128 || d == 256; }
@@ -902,6 +1008,20 @@ hipError_t launch_kv_append(const KvAppendArgs &a, bool vec, hipStream_t s)
     const dim3 grid(static_cast<unsigned>(wgs < 16384 ? wgs : 16384));
     if (vec) hipLaunchKernelGGL(kv_append<true>, grid, dim3(256), 0, s, a);
     else hipLaunchKernelGGL(kv_append<false>, grid, dim3(256), 0, s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_norm_rope(const NormRopeArgs &a, hipStream_t s)
+{
+    hipLaunchKernelGGL(head_norm_rope, dim3(static_cast<unsigned>(a.rows), static_cast<unsigned>(a.heads)), dim3(64), 0,
+                       s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_gate(const GateArgs &a, hipStream_t s)
+{
+    const uint64_t wgs = (a.rows * a.width + 255) / 256;
+    hipLaunchKernelGGL(output_gate, dim3(static_cast<unsigned>(wgs < 16384 ? wgs : 16384)), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 

@@ -9,4 +9,5 @@ from . import workloads  # noqa: F401
 from .binding import (  # noqa: F401
     HsdpaError, Plan, Spec, Call, STATUS, library, library_path, attention_torch,
     KvSpec, KvCall, kv_spec, kv_append_raw, kv_append_torch,
+    NormRopeSpec, NormRopeCall, GateSpec, GateCall, head_norm_rope_torch, output_gate_torch,
 )

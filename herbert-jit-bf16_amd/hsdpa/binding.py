@@ -22,7 +22,8 @@ STATUS = {
     11: "HSDPA_ERR_NO_DEVICE", 12: "HSDPA_ERR_BATCH", 13: "HSDPA_ERR_LAYOUT",
 }
 EXPORTS = ["hsdpa_plan_create", "hsdpa_plan_destroy", "hsdpa_workspace_bytes", "hsdpa_attention",
-           "hsdpa_status_string", "hsdpa_version", "hsdpa_kv_check", "hsdpa_kv_append"]
+           "hsdpa_status_string", "hsdpa_version", "hsdpa_kv_check", "hsdpa_kv_append",
+           "hsdpa_head_norm_rope", "hsdpa_output_gate"]
 
 
 class HsdpaError(RuntimeError):
@@ -59,6 +60,26 @@ class KvCall(ctypes.Structure):
                 ("input_values", ctypes.c_void_p), ("rows", ctypes.c_uint64), ("past", ctypes.c_uint64)]
 
 
+class NormRopeSpec(ctypes.Structure):
+    _fields_ = [("heads", ctypes.c_uint64), ("head_dim", ctypes.c_uint64), ("head_stride", ctypes.c_uint64),
+                ("row_stride", ctypes.c_uint64), ("rotary_dims", ctypes.c_uint64), ("table_row", ctypes.c_uint64),
+                ("positions", ctypes.c_uint64), ("plus_one", ctypes.c_uint32), ("reserved", ctypes.c_uint32)]
+
+
+class NormRopeCall(ctypes.Structure):
+    _fields_ = [("data", ctypes.c_void_p), ("weight", ctypes.c_void_p), ("cos", ctypes.c_void_p),
+                ("sin", ctypes.c_void_p), ("rows", ctypes.c_uint64), ("past", ctypes.c_uint64),
+                ("eps", ctypes.c_float), ("reserved", ctypes.c_float)]
+
+
+class GateSpec(ctypes.Structure):
+    _fields_ = [("width", ctypes.c_uint64), ("attn_row", ctypes.c_uint64), ("gate_row", ctypes.c_uint64)]
+
+
+class GateCall(ctypes.Structure):
+    _fields_ = [("attn", ctypes.c_void_p), ("gate", ctypes.c_void_p), ("rows", ctypes.c_uint64)]
+
+
 def library_path() -> str:
     return os.path.join(_HERE, _LIB_NAME)
 
@@ -86,6 +107,11 @@ def library():
         L.hsdpa_kv_check.restype = ctypes.c_int
         L.hsdpa_kv_append.argtypes = [ctypes.POINTER(KvSpec), ctypes.POINTER(KvCall), ctypes.c_void_p]
         L.hsdpa_kv_append.restype = ctypes.c_int
+        L.hsdpa_head_norm_rope.argtypes = [ctypes.POINTER(NormRopeSpec), ctypes.POINTER(NormRopeCall),
+                                           ctypes.c_void_p]
+        L.hsdpa_head_norm_rope.restype = ctypes.c_int
+        L.hsdpa_output_gate.argtypes = [ctypes.POINTER(GateSpec), ctypes.POINTER(GateCall), ctypes.c_void_p]
+        L.hsdpa_output_gate.restype = ctypes.c_int
         _lib = L
     return _lib
 
@@ -179,3 +205,35 @@ def kv_append_torch(spec: KvSpec, keys, values, input_keys, input_values, rows: 
     s = torch.cuda.current_stream() if stream is None else stream
     kv_append_raw(spec, keys.data_ptr(), values.data_ptr(), input_keys.data_ptr(), input_values.data_ptr(),
                   rows, past, s.cuda_stream)
+
+
+def head_norm_rope_torch(data, weight, cos, sin, heads: int, head_dim: int, head_stride: int, row_stride: int,
+                         rotary_dims: int, rows: int, past: int, eps: float, plus_one: bool = True,
+                         table_row: int | None = None, positions: int | None = None, stream=None) -> None:
+    """The head-norm-rope node on torch device tensors holding bf16 bits; data
+    is updated in place. cos/sin are [positions][table_row] tables."""
+    import torch
+
+    half = rotary_dims // 2
+    tr = half if table_row is None else table_row
+    pos = (cos.numel() // tr if tr else 0) if positions is None else positions
+    spec = NormRopeSpec(heads, head_dim, head_stride, row_stride, rotary_dims, tr, pos, int(plus_one), 0)
+    call = NormRopeCall(data.data_ptr(), weight.data_ptr(), cos.data_ptr() if cos is not None else 0,
+                        sin.data_ptr() if sin is not None else 0, rows, past, eps, 0.0)
+    s = torch.cuda.current_stream() if stream is None else stream
+    rc = library().hsdpa_head_norm_rope(ctypes.byref(spec), ctypes.byref(call), ctypes.c_void_p(s.cuda_stream))
+    if rc != 0:
+        raise HsdpaError(rc, "hsdpa_head_norm_rope")
+
+
+def output_gate_torch(attn, gate, width: int, attn_row: int, gate_row: int, rows: int, stream=None) -> None:
+    """attn <- attn * sigmoid(gate) in place (torch device tensors of bf16 bits;
+    `gate` may be a view starting at q + q_dim)."""
+    import torch
+
+    spec = GateSpec(width, attn_row, gate_row)
+    call = GateCall(attn.data_ptr(), gate.data_ptr(), rows)
+    s = torch.cuda.current_stream() if stream is None else stream
+    rc = library().hsdpa_output_gate(ctypes.byref(spec), ctypes.byref(call), ctypes.c_void_p(s.cuda_stream))
+    if rc != 0:
+        raise HsdpaError(rc, "hsdpa_output_gate")

@@ -30,6 +30,12 @@
  *   hsdpa_kv_append         the kv-append node (src/jit/schedule/lowering.rs:578-592):
  *                           every task of append
  *                           (src/jit/target/x86/execution/kv.rs:15-69)
+ *   hsdpa_head_norm_rope    the head-norm-rope node (lowering.rs:549-577): per row,
+ *                           norm_rope (src/jit/target/x86/execution/transforms.rs:32-81)
+ *                           around ElemOp::RmsNorm[Gemma] and ElemOp::Rope
+ *                           (src/jit/target/x86/emit_elem.rs:239-335, 479-520)
+ *   hsdpa_output_gate       the attention-output-gate node (lowering.rs:642-666):
+ *                           ElemOp::SigmoidMul per row (emit_elem.rs:350-440)
  *
  * All strides are in bf16 elements, like the reference. All pointers are
  * device pointers (HBM) except the spec/call/plan structs themselves, which
@@ -146,6 +152,57 @@ hsdpa_status hsdpa_kv_check(const hsdpa_kv_spec *spec);
  * before any launch. Any alignment is accepted; 16-byte aligned pointers with
  * head_dim and stride multiples of 8 take the vector path. */
 hsdpa_status hsdpa_kv_append(const hsdpa_kv_spec *spec, const hsdpa_kv_call *call, void *stream);
+
+/* ---- Head RMS norm + RoPE: the node before the KV append ------------------
+ * For each row r and head h, x = data + r*row_stride + h*head_stride (head_dim
+ * bf16, in place): x <- rmsnorm(x) * w (Gemma: * (1 + w), added in f32), then
+ * the rotate_half RoPE on its first rotary_dims dimensions with the pairs
+ * (j, j + rotary_dims/2) and the tables' row at position past + r (cos and
+ * sin, table_row bf16 apart, rotary_dims/2 used). The engine calls it once
+ * for q (q_norm) and once for k (k_norm). */
+typedef struct hsdpa_norm_rope_spec {
+    uint64_t heads;        /* heads of the buffer (query or KV heads) */
+    uint64_t head_dim;     /* a multiple of 32, at most 512 */
+    uint64_t head_stride;  /* elements between heads of a row */
+    uint64_t row_stride;   /* elements between rows */
+    uint64_t rotary_dims;  /* rotated dimensions: a multiple of 32, at most head_dim; 0 = none */
+    uint64_t table_row;    /* elements between positions in cos and sin (>= rotary_dims/2) */
+    uint64_t positions;    /* positions the tables hold */
+    uint32_t plus_one;     /* 1: Gemma convention (1 + w), as Qwen3.5; 0: w */
+    uint32_t reserved;     /* 0 */
+} hsdpa_norm_rope_spec;
+
+typedef struct hsdpa_norm_rope_call {
+    uint16_t *data;          /* q or k, token-major, normalised and rotated in place */
+    const uint16_t *weight;  /* head_dim bf16 (q_norm or k_norm) */
+    const uint16_t *cos;     /* [positions][table_row] bf16 */
+    const uint16_t *sin;     /* same layout */
+    uint64_t rows;
+    uint64_t past;           /* position of the first row */
+    float eps;               /* RMSNorm epsilon */
+    float reserved;          /* 0 */
+} hsdpa_norm_rope_call;
+
+hsdpa_status hsdpa_head_norm_rope(const hsdpa_norm_rope_spec *spec, const hsdpa_norm_rope_call *call, void *stream);
+
+/* ---- Output gate: the node after the attention ---------------------------
+ * attn[r][i] <- attn[r][i] * sigmoid(gate[r][i]) for i < width, computed as
+ * attn / (1 + exp(min(-gate, 88))) with the softmax's exponential; on the
+ * gated model the gate follows Q on each row of q (gate = q + q_dim,
+ * gate_row = q_row). */
+typedef struct hsdpa_gate_spec {
+    uint64_t width;        /* elements per row (q_dim) */
+    uint64_t attn_row;     /* elements between rows of attn */
+    uint64_t gate_row;     /* elements between rows of the gate */
+} hsdpa_gate_spec;
+
+typedef struct hsdpa_gate_call {
+    uint16_t *attn;          /* in place */
+    const uint16_t *gate;
+    uint64_t rows;
+} hsdpa_gate_call;
+
+hsdpa_status hsdpa_output_gate(const hsdpa_gate_spec *spec, const hsdpa_gate_call *call, void *stream);
 
 /* Static, human-readable name of a status. */
 const char *hsdpa_status_string(hsdpa_status status);

@@ -49,6 +49,19 @@ def lib():
         L.oracle_dpbf16_lane.restype = ctypes.c_float
         L.oracle_exp_poly.argtypes = [ctypes.c_float]
         L.oracle_exp_poly.restype = ctypes.c_float
+        L.oracle_hsum16.argtypes = [ctypes.c_void_p]
+        L.oracle_hsum16.restype = ctypes.c_float
+        L.oracle_rms_sumsq.argtypes = [u16p, ctypes.c_int]
+        L.oracle_rms_sumsq.restype = ctypes.c_float
+        L.oracle_rmsnorm.argtypes = [u16p, u16p, u16p, ctypes.c_int, ctypes.c_float, ctypes.c_int]
+        L.oracle_rmsnorm.restype = None
+        L.oracle_rope.argtypes = [u16p, u16p, u16p, ctypes.c_int]
+        L.oracle_rope.restype = None
+        L.oracle_head_norm_rope.argtypes = [u16p, u16p, u16p, u16p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                            ctypes.c_int, ctypes.c_float, ctypes.c_int]
+        L.oracle_head_norm_rope.restype = None
+        L.oracle_sigmoid_mul.argtypes = [u16p, u16p, u16p, ctypes.c_int]
+        L.oracle_sigmoid_mul.restype = None
         L.oracle_qk_dot.argtypes = [u16p, u16p, ctypes.c_int]
         L.oracle_qk_dot.restype = ctypes.c_float
         L.oracle_sdpa_head.argtypes = [u16p, u16p, u16p, ctypes.c_void_p, u16p, ctypes.c_uint64,
@@ -126,3 +139,58 @@ def prefill_block(q: np.ndarray, k: np.ndarray, v: np.ndarray, past: int, scale:
     out = np.zeros((rows, d), dtype=np.uint16)
     lib().oracle_sdpa_prefill_block(_ptr(q), _ptr(k), _ptr(v), _ptr(sc), _ptr(out), past, scale, d, rows, d, d)
     return out
+
+
+
+def _p(a):
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+def rmsnorm(x: np.ndarray, w: np.ndarray, eps: float, plus_one: bool = True) -> np.ndarray:
+    """ElemOp::RmsNorm[Gemma] on one vector of bf16 bits (the restatement)."""
+    x = np.ascontiguousarray(x, np.uint16)
+    w = np.ascontiguousarray(w, np.uint16)
+    y = np.empty_like(x)
+    lib().oracle_rmsnorm(_p(x), _p(w), _p(y), x.size, eps, int(plus_one))
+    return y
+
+
+def rms_sumsq(x: np.ndarray) -> float:
+    x = np.ascontiguousarray(x, np.uint16)
+    return float(lib().oracle_rms_sumsq(_p(x), x.size))
+
+
+def rope(x: np.ndarray, cos_row: np.ndarray, sin_row: np.ndarray) -> np.ndarray:
+    """ElemOp::Rope on one vector (returns a rotated copy)."""
+    y = np.ascontiguousarray(x, np.uint16).copy()
+    c = np.ascontiguousarray(cos_row, np.uint16)
+    s = np.ascontiguousarray(sin_row, np.uint16)
+    lib().oracle_rope(_p(y), _p(c), _p(s), y.size)
+    return y
+
+
+def head_norm_rope(data: np.ndarray, w: np.ndarray, cos: np.ndarray, sin: np.ndarray, rows: int, past: int,
+                   heads: int, head_dim: int, head_stride: int, row_stride: int, rotary: int, eps: float,
+                   plus_one: bool = True, table_row: int | None = None) -> np.ndarray:
+    """The head-norm-rope node over `rows` rows of a flat bf16 buffer (copy)."""
+    out = np.ascontiguousarray(data, np.uint16).copy()
+    w = np.ascontiguousarray(w, np.uint16)
+    tr = rotary // 2 if table_row is None else table_row
+    cos = np.ascontiguousarray(cos, np.uint16).reshape(-1)
+    sin = np.ascontiguousarray(sin, np.uint16).reshape(-1)
+    L = lib()
+    for r in range(rows):
+        row = out[r * row_stride:]
+        at = (past + r) * tr
+        L.oracle_head_norm_rope(_p(row), _p(w), _p(cos[at:]) if rotary else None, _p(sin[at:]) if rotary else None,
+                                heads, head_stride, head_dim, rotary, eps, int(plus_one))
+    return out
+
+
+def sigmoid_mul(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    """ElemOp::SigmoidMul: a / (1 + exp(min(-b, 88))) in bf16."""
+    a = np.ascontiguousarray(a, np.uint16)
+    b = np.ascontiguousarray(b, np.uint16)
+    y = np.empty_like(a)
+    lib().oracle_sigmoid_mul(_p(a), _p(b), _p(y), a.size)
+    return y

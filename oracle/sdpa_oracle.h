@@ -134,6 +134,31 @@ long oracle_dpbf16_selfcheck(uint64_t seed, long lanes);
  * -1 without AVX-512 BF16. */
 long oracle_cvt_exp_selfcheck(uint64_t seed, long count);
 
+/* ---- The element kernels around the attention (elem_scalar.c) ------------
+ * Restatements of the AVX-512 element kernels of
+ * src/jit/target/x86/emit_elem.rs that the attention chain uses. */
+
+/* The hsum tree of base.rs:258-267 / emit_elem.rs:175-183 on 16 lanes. */
+float oracle_hsum16(const float *lanes);
+/* The sum of squares of ElemOp::RmsNorm (emit_elem.rs:251-271): vdpbf16ps
+ * chains, chain sums in order, hsum. */
+float oracle_rms_sumsq(const uint16_t *x, int dim);
+/* ElemOp::RmsNorm / RmsNormGemma (emit_elem.rs:239-335) on one vector of
+ * `dim` bf16 (a multiple of 32): y may alias x. */
+void oracle_rmsnorm(const uint16_t *x, const uint16_t *w, uint16_t *y, int dim, float eps, int plus_one);
+/* ElemOp::Rope (emit_elem.rs:479-520), rotate_half, in place on `dim` bf16
+ * with dim/2 cos and sin entries. */
+void oracle_rope(uint16_t *x, const uint16_t *cos_row, const uint16_t *sin_row, int dim);
+/* The head-norm-rope node on one row (transforms.rs:32-81 with the binding of
+ * lowering.rs:549-577): for each of `heads` heads `stride` apart, the norm in
+ * place, then the rope over its first `rotary` dimensions. */
+void oracle_head_norm_rope(uint16_t *row, const uint16_t *w, const uint16_t *cos_row,
+                           const uint16_t *sin_row, int heads, int stride, int dim, int rotary,
+                           float eps, int plus_one);
+/* ElemOp::SigmoidMul (emit_elem.rs:350-440): y = a / (1 + exp(min(0 - b, 88)))
+ * on `n` bf16 (y may alias a). */
+void oracle_sigmoid_mul(const uint16_t *a, const uint16_t *b, uint16_t *y, int n);
+
 #ifdef __cplusplus
 }
 #endif

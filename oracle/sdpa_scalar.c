@@ -103,6 +103,8 @@ static float hsum16(const float l[16])
     return u0 + u1;
 }
 
+float oracle_hsum16(const float *l) { return hsum16(l); }
+
 /* hmax (base.rs:271-282): the same halving, then two vshufps/vmaxps steps;
  * operand order kept (dst first) so signed zeros resolve like the code. */
 static float hmax16(const float l[16])

@@ -107,3 +107,55 @@ def test_kv_append_without_gpu_reports_no_device():
     if torch.cuda.is_available():
         pytest.skip("a GPU is present")
     assert call_rc(spec(), 1, 0) == 11
+
+
+# ---- head-norm-rope and output-gate refusals (host side) ----------------------
+
+def nr_rc(**kw):
+    d = dict(heads=16, head_dim=256, head_stride=256, row_stride=8192, rotary_dims=64, table_row=32,
+             positions=100, plus_one=1, reserved=0)
+    call_kw = {k[5:]: kw.pop(k) for k in list(kw) if k.startswith("call_")}
+    d.update(kw)
+    s = binding.NormRopeSpec(**d)
+    c = dict(data=16, weight=16, cos=16, sin=16, rows=4, past=0, eps=1e-6, reserved=0.0)
+    c.update(call_kw)
+    call = binding.NormRopeCall(**c)
+    return binding.library().hsdpa_head_norm_rope(ctypes.byref(s), ctypes.byref(call), None)
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(heads=0), 1), (dict(head_dim=0), 1),
+    (dict(head_dim=100), 2), (dict(head_dim=1024, head_stride=1024), 2),   # multiple of 32, at most 512
+    (dict(rotary_dims=48), 2), (dict(rotary_dims=512), 2),                 # multiple of 32, at most head_dim
+    (dict(head_stride=128), 4), (dict(row_stride=4000), 4), (dict(table_row=16), 4),
+    (dict(call_past=97), 6),                                                # past + rows > table positions
+    (dict(call_data=0), 9), (dict(call_cos=0), 9),
+])
+def test_head_norm_rope_refusals(kw, code):
+    assert nr_rc(**kw) == code
+
+
+def test_head_norm_rope_empty_and_device():
+    import torch
+
+    assert nr_rc(call_rows=0) == 0
+    assert nr_rc(rotary_dims=0, call_cos=0, call_sin=0, call_past=10 ** 6) in (0, 11)  # no tables needed
+    if not torch.cuda.is_available():
+        assert nr_rc() == 11
+
+
+def gate_rc(width=4096, attn_row=4096, gate_row=8192, attn=16, gate=16, rows=2):
+    s = binding.GateSpec(width, attn_row, gate_row)
+    c = binding.GateCall(attn, gate, rows)
+    return binding.library().hsdpa_output_gate(ctypes.byref(s), ctypes.byref(c), None)
+
+
+def test_output_gate_refusals():
+    import torch
+
+    assert gate_rc(width=0) == 1
+    assert gate_rc(attn_row=100) == 4 and gate_rc(gate_row=100) == 4
+    assert gate_rc(rows=0) == 0
+    assert gate_rc(attn=0) == 9
+    if not torch.cuda.is_available():
+        assert gate_rc() == 11
