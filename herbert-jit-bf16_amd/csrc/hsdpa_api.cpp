@@ -152,6 +152,73 @@ hsdpa_status hsdpa_output_gate(const hsdpa_gate_spec *spec, const hsdpa_gate_cal
     return HSDPA_OK;
 }
 
+// One layer's KV between a snapshot block (host: K[heads][snap_positions][head_dim]
+// then V, model.rs:675-697) and the live cache (device: head h at h * stride):
+// the copy loops of Runner::snapshot_take (model.rs:749-766) and
+// Runner::restore_from (model.rs:820-851), keys then values, the leading
+// `positions` of every head, as one 2-D copy per half. restore_from skips rows
+// the live cache already holds (first_different_row, model.rs:861-865); copying
+// them again leaves the same bytes, so the cache ends identical.
+static hsdpa_status kv_snapshot_check(const hsdpa_kv_spec *spec, const void *snapshot_layer, const void *keys,
+                                      const void *values, uint64_t snap_positions, uint64_t positions,
+                                      bool *nothing)
+{
+    *nothing = false;
+    if (!spec) return HSDPA_ERR_NULL;
+    const hsdpa_status st = check_kv_spec(*spec);
+    if (st != HSDPA_OK) return st;
+    if (positions > snap_positions || positions > spec->capacity) return HSDPA_ERR_CAPACITY;
+    // A layer's block is one u16 run of the format: 64 GiB at most (MAX_BLOCK_SNAPSHOT, model.rs:105-108)
+    if (snap_positions > (uint64_t{64} << 30) / (4 * spec->heads * spec->head_dim)) return HSDPA_ERR_CAPACITY;
+    if (positions == 0) {
+        *nothing = true;
+        return HSDPA_OK;
+    }
+    if (!snapshot_layer || !keys || !values) return HSDPA_ERR_NULL;
+    return check_device();
+}
+
+static hsdpa_status kv_snapshot_copy(const hsdpa_kv_spec *spec, bool to_device, uint16_t *snapshot_layer,
+                                     uint16_t *keys, uint16_t *values, uint64_t snap_positions, uint64_t positions,
+                                     void *stream)
+{
+    const uint64_t snap_pitch = snap_positions * spec->head_dim * 2, live_pitch = spec->stride * 2;
+    const uint64_t width = positions * spec->head_dim * 2;
+    uint16_t *const snap[2] = {snapshot_layer, snapshot_layer + spec->heads * snap_positions * spec->head_dim};
+    uint16_t *const live[2] = {keys, values};
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    for (int half = 0; half < 2; half++) {
+        const hipError_t e =
+            to_device
+                ? hipMemcpy2DAsync(live[half], live_pitch, snap[half], snap_pitch, width, spec->heads,
+                                   hipMemcpyHostToDevice, s)
+                : hipMemcpy2DAsync(snap[half], snap_pitch, live[half], live_pitch, width, spec->heads,
+                                   hipMemcpyDeviceToHost, s);
+        if (e != hipSuccess) return HSDPA_ERR_HIP;
+    }
+    return HSDPA_OK;
+}
+
+hsdpa_status hsdpa_kv_restore(const hsdpa_kv_spec *spec, const uint16_t *snapshot_layer, uint64_t snap_positions,
+                              uint16_t *keys, uint16_t *values, uint64_t positions, void *stream)
+{
+    bool nothing;
+    const hsdpa_status st = kv_snapshot_check(spec, snapshot_layer, keys, values, snap_positions, positions, &nothing);
+    if (st != HSDPA_OK || nothing) return st;
+    return kv_snapshot_copy(spec, true, const_cast<uint16_t *>(snapshot_layer), keys, values, snap_positions,
+                            positions, stream);
+}
+
+hsdpa_status hsdpa_kv_take(const hsdpa_kv_spec *spec, const uint16_t *keys, const uint16_t *values,
+                           uint16_t *snapshot_layer, uint64_t snap_positions, uint64_t positions, void *stream)
+{
+    bool nothing;
+    const hsdpa_status st = kv_snapshot_check(spec, snapshot_layer, keys, values, snap_positions, positions, &nothing);
+    if (st != HSDPA_OK || nothing) return st;
+    return kv_snapshot_copy(spec, false, snapshot_layer, const_cast<uint16_t *>(keys), const_cast<uint16_t *>(values),
+                            snap_positions, positions, stream);
+}
+
 hsdpa_status hsdpa_kv_check(const hsdpa_kv_spec *spec)
 {
     if (!spec) return HSDPA_ERR_NULL;

@@ -23,7 +23,7 @@ STATUS = {
 }
 EXPORTS = ["hsdpa_plan_create", "hsdpa_plan_destroy", "hsdpa_workspace_bytes", "hsdpa_attention",
            "hsdpa_status_string", "hsdpa_version", "hsdpa_kv_check", "hsdpa_kv_append",
-           "hsdpa_head_norm_rope", "hsdpa_output_gate"]
+           "hsdpa_head_norm_rope", "hsdpa_output_gate", "hsdpa_kv_restore", "hsdpa_kv_take"]
 
 
 class HsdpaError(RuntimeError):
@@ -112,6 +112,13 @@ def library():
         L.hsdpa_head_norm_rope.restype = ctypes.c_int
         L.hsdpa_output_gate.argtypes = [ctypes.POINTER(GateSpec), ctypes.POINTER(GateCall), ctypes.c_void_p]
         L.hsdpa_output_gate.restype = ctypes.c_int
+        u16p = ctypes.c_void_p
+        L.hsdpa_kv_restore.argtypes = [ctypes.POINTER(KvSpec), u16p, ctypes.c_uint64, u16p, u16p, ctypes.c_uint64,
+                                       ctypes.c_void_p]
+        L.hsdpa_kv_restore.restype = ctypes.c_int
+        L.hsdpa_kv_take.argtypes = [ctypes.POINTER(KvSpec), u16p, u16p, u16p, ctypes.c_uint64, ctypes.c_uint64,
+                                    ctypes.c_void_p]
+        L.hsdpa_kv_take.restype = ctypes.c_int
         _lib = L
     return _lib
 
@@ -237,3 +244,23 @@ def output_gate_torch(attn, gate, width: int, attn_row: int, gate_row: int, rows
     rc = library().hsdpa_output_gate(ctypes.byref(spec), ctypes.byref(call), ctypes.c_void_p(s.cuda_stream))
     if rc != 0:
         raise HsdpaError(rc, "hsdpa_output_gate")
+
+
+def kv_restore_raw(spec: KvSpec, snapshot_layer: int, snap_positions: int, keys: int, values: int,
+                   positions: int, stream: int = 0) -> None:
+    """Copy the leading `positions` of every head of one snapshot layer (host,
+    K[heads][snap_positions][head_dim] then V) into the live cache (device)."""
+    rc = library().hsdpa_kv_restore(ctypes.byref(spec), snapshot_layer, snap_positions, keys, values, positions,
+                                    ctypes.c_void_p(stream))
+    if rc != 0:
+        raise HsdpaError(rc, "hsdpa_kv_restore")
+
+
+def kv_take_raw(spec: KvSpec, keys: int, values: int, snapshot_layer: int, snap_positions: int, positions: int,
+                stream: int = 0) -> None:
+    """Copy the leading `positions` of every head of the live cache (device)
+    into one snapshot layer (host)."""
+    rc = library().hsdpa_kv_take(ctypes.byref(spec), keys, values, snapshot_layer, snap_positions, positions,
+                                 ctypes.c_void_p(stream))
+    if rc != 0:
+        raise HsdpaError(rc, "hsdpa_kv_take")

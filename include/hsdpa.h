@@ -36,6 +36,10 @@
  *                           (src/jit/target/x86/emit_elem.rs:239-335, 479-520)
  *   hsdpa_output_gate       the attention-output-gate node (lowering.rs:642-666):
  *                           ElemOp::SigmoidMul per row (emit_elem.rs:350-440)
+ *   hsdpa_kv_restore        the KV half of Runner::restore_from (src/jit/model.rs:786-856)
+ *                           for one layer: snapshot (host) to the live cache (device)
+ *   hsdpa_kv_take           the KV half of Runner::snapshot_take (model.rs:728-773)
+ *                           for one layer: live cache (device) to the snapshot (host)
  *
  * All strides are in bf16 elements, like the reference. All pointers are
  * device pointers (HBM) except the spec/call/plan structs themselves, which
@@ -203,6 +207,21 @@ typedef struct hsdpa_gate_call {
 } hsdpa_gate_call;
 
 hsdpa_status hsdpa_output_gate(const hsdpa_gate_spec *spec, const hsdpa_gate_call *call, void *stream);
+
+/* ---- KV snapshot of one layer ----------------------------------------------
+ * A snapshot layer holds K[heads][snap_positions][head_dim] then
+ * V[heads][snap_positions][head_dim] bf16 (model.rs:675-697), host memory; the
+ * live cache is the device layout of hsdpa_kv_spec. `positions` leading
+ * positions of every head are copied; positions > snap_positions or >
+ * capacity, or a layer block beyond 64 GiB (MAX_BLOCK_SNAPSHOT,
+ * model.rs:105-108), is HSDPA_ERR_CAPACITY (snapshot_take's "slot buffer too
+ * short" refusal, model.rs:749-755); positions == 0 copies nothing. Enqueued
+ * on `stream`; for an asynchronous copy the host buffer must be pinned
+ * (hipHostMalloc), pageable memory makes the call return after the copy. */
+hsdpa_status hsdpa_kv_restore(const hsdpa_kv_spec *spec, const uint16_t *snapshot_layer, uint64_t snap_positions,
+                              uint16_t *keys, uint16_t *values, uint64_t positions, void *stream);
+hsdpa_status hsdpa_kv_take(const hsdpa_kv_spec *spec, const uint16_t *keys, const uint16_t *values,
+                           uint16_t *snapshot_layer, uint64_t snap_positions, uint64_t positions, void *stream);
 
 /* Static, human-readable name of a status. */
 const char *hsdpa_status_string(hsdpa_status status);
