@@ -94,27 +94,55 @@ def time_steps(torch, plan, w, q, ks, vs, out, ws, steps, warmup):
     return ms, wall, eager, out.clone()
 
 
+def host_description():
+    """CPU model, sockets and logical CPUs of this host (from /proc/cpuinfo)."""
+    model, sockets = "?", set()
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                key, _, val = line.partition(":")
+                key = key.strip()
+                if key == "model name" and model == "?":
+                    model = val.strip()
+                elif key == "physical id":
+                    sockets.add(val.strip())
+    except OSError:
+        pass
+    return f"{model}, {max(len(sockets), 1)} socket(s), {os.cpu_count()} logical CPUs"
+
+
+def median_time(fn, warm, runs):
+    ts = []
+    for i in range(warm + runs):
+        t0 = time.perf_counter()
+        fn()
+        if i >= warm:
+            ts.append(time.perf_counter() - t0)
+    ts.sort()
+    return ts[len(ts) // 2]
+
+
 def cpu_baseline(w_decode, decode_gbs_gpu):
-    """Time the AVX-512 BF16 restatement of the reference on this host."""
+    """Time the AVX-512 BF16 restatement of the reference on this host: the
+    reference's decode node has Hq tasks, so it uses min(cores, Hq) threads;
+    a 1-thread figure is reported beside it."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle
 
     if not oracle.avx512_available():
         return None, "host lacks AVX-512 BF16"
     cores = oracle.lib().oracle_physical_cores()
-    used = min(cores, w_decode.heads)     # the reference's decode node has Hq tasks
-    ts = []
-    for i in range(3 + 20):
-        t0 = time.perf_counter()
-        oracle.attention(w_decode, "avx512", threads=used)
-        if i >= 3:
-            ts.append(time.perf_counter() - t0)
-    ts.sort()
-    med = ts[len(ts) // 2]
-    return {"value": round(w_decode.decode_bytes() / med / 1e9, 3), "unit": "GB/s", "cores": used,
+    used = min(cores, w_decode.heads)
+    med = median_time(lambda: oracle.attention(w_decode, "avx512", threads=used), 3, 20)
+    med1 = median_time(lambda: oracle.attention(w_decode, "avx512", threads=1), 1, 5)
+    nbytes = w_decode.decode_bytes()
+    return {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": used,
             "kind": "port",
-            "sample": f"decode 32K (same inputs), {len(ts)} runs after 3 warm-ups, median {med*1e3:.2f} ms, "
-                      f"{used} of {cores} physical cores, pinned"}, None
+            "sample": f"decode 32K (same inputs), 20 runs after 3 warm-ups, median {med*1e3:.2f} ms, "
+                      f"{used} of {cores} physical cores, pinned",
+            "host": host_description(),
+            "one_thread": {"value": round(nbytes / med1 / 1e9, 3), "unit": "GB/s",
+                           "sample": f"5 runs after 1 warm-up, median {med1*1e3:.2f} ms"}}, None
 
 
 def cpu_prefill_sample(wp, threads):
@@ -127,14 +155,7 @@ def cpu_prefill_sample(wp, threads):
     past = wp.past + wp.rows - rows
     ws = W.Workload("prefill_sample", wp.heads, wp.kv_heads, wp.head_dim, rows, past, wp.capacity,
                     wp.q[-rows:], wp.k, wp.v, wp.scale)
-    ts = []
-    for i in range(1 + 3):
-        t0 = time.perf_counter()
-        oracle.attention(ws, "avx512", threads=threads)
-        if i >= 1:
-            ts.append(time.perf_counter() - t0)
-    ts.sort()
-    med = ts[len(ts) // 2]
+    med = median_time(lambda: oracle.attention(ws, "avx512", threads=threads), 1, 3)
     return {"value": round(ws.prefill_flops() / med / 1e12, 4), "unit": "TFLOP/s", "cores": threads,
             "kind": "port",
             "sample": f"last 256-row pass of the 4096-row chunk (past {past}), 3 runs after 1 warm-up, "
