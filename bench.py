@@ -15,7 +15,11 @@ the 256 MB Infinity Cache cannot hold the working set. The K timed steps
 are captured once into a HIP graph and replayed, so the figure is GPU time,
 not Python launch time; the replay's output is checked against an eager call.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-prefill]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-prefill] [--no-layer]
+
+Also timed: the whole attention chain of a gated Qwen3.5 layer (q/k norm and
+RoPE, KV append, attention, output gate) fused into one call against the same
+nodes called one by one.
 """
 from __future__ import annotations
 
@@ -122,6 +126,88 @@ def median_time(fn, warm, runs):
     return ts[len(ts) // 2]
 
 
+def layer_buffers(torch, w, copies, seed=7):
+    """Device buffers of a gated layer chain on workload w's cache: q rows of
+    [Q ; gate] (2*q_dim), the block's k and v projections, norm weights, RoPE
+    tables over the capacity (rotary 64 of head_dim, the Qwen3.5 layout)."""
+    import numpy as np
+    from hsdpa import workloads as W
+
+    rng = np.random.default_rng(seed)
+    dev = torch.device("cuda")
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).to(dev)
+    bf = lambda a: W.f32_to_bf16(np.asarray(a, np.float32))
+    q_dim, kv_row, rot = w.heads * w.head_dim, w.kv_heads * w.head_dim, 64
+    ang = np.arange(w.capacity, dtype=np.float64)[:, None] * (1e7 ** (-np.arange(rot // 2) * 2.0 / rot))[None, :]
+    b = dict(q=t(bf(rng.normal(0, 2, w.rows * 2 * q_dim))), k=t(bf(rng.normal(0, 2, w.rows * kv_row))),
+             v=t(bf(rng.normal(0, 1, w.rows * kv_row))), q_norm=t(bf(rng.normal(0, 0.1, w.head_dim))),
+             k_norm=t(bf(rng.normal(0, 0.1, w.head_dim))), cos=t(bf(np.cos(ang))), sin=t(bf(np.sin(ang))),
+             out=torch.zeros(w.rows * q_dim, dtype=torch.int16, device=dev))
+    k0 = t(w.k)
+    v0 = t(w.v)
+    b["keys"] = [k0] + [k0.clone() for _ in range(copies - 1)]
+    b["values"] = [v0] + [v0.clone() for _ in range(copies - 1)]
+    return b, q_dim, kv_row, rot
+
+
+def layer_step(hsdpa, plan, w, b, i, ws, fused, stream):
+    """One layer step: the fused call, or the five nodes in order."""
+    q_dim, kv_row, rot = w.heads * w.head_dim, w.kv_heads * w.head_dim, 64
+    keys, values = b["keys"][i % len(b["keys"])], b["values"][i % len(b["values"])]
+    gate = b["q"][q_dim:]
+    if fused:
+        hsdpa.attention_layer_torch(plan, b["q"], b["k"], b["v"], keys, values, b["out"], b["q_norm"], b["k_norm"],
+                                    b["cos"], b["sin"], w.rows, w.past, w.scale, 1e-6, ws, kv_row, rot, gate=gate,
+                                    gate_row=2 * q_dim, positions=w.capacity, stream=stream)
+        return
+    hsdpa.head_norm_rope_torch(b["q"], b["q_norm"], b["cos"], b["sin"], w.heads, w.head_dim, w.head_dim, 2 * q_dim,
+                               rot, w.rows, w.past, 1e-6, positions=w.capacity, stream=stream)
+    hsdpa.head_norm_rope_torch(b["k"], b["k_norm"], b["cos"], b["sin"], w.kv_heads, w.head_dim, w.head_dim, kv_row,
+                               rot, w.rows, w.past, 1e-6, positions=w.capacity, stream=stream)
+    spec = hsdpa.kv_spec(w.kv_heads, w.head_dim, w.capacity, w.rows)
+    hsdpa.kv_append_torch(spec, keys, values, b["k"], b["v"], w.rows, w.past, stream=stream)
+    hsdpa.attention_torch(plan, b["q"], keys, values, b["out"], w.rows, w.past, w.scale, ws, stream)
+    hsdpa.output_gate_torch(b["out"], gate, q_dim, q_dim, 2 * q_dim, w.rows, stream=stream)
+
+
+def time_layer(torch, hsdpa, w, copies, steps, warmup):
+    """The gated layer chain (norms, append, attention, gate) on workload w:
+    ms per step fused (hsdpa_attention_layer) and as separate nodes, each a
+    HIP graph of `steps` steps. First checks one eager step of each on fresh
+    buffers for equal outputs, cache and q/k."""
+    plan = hsdpa.Plan(w.heads, w.gqa, w.head_dim, w.capacity, q_row=2 * w.heads * w.head_dim)
+    ws = torch.empty(plan.workspace_bytes, dtype=torch.uint8, device="cuda")
+    stream = torch.cuda.Stream()
+    results = {}
+    check = []
+    for fused in (True, False):
+        b = layer_buffers(torch, w, copies)[0]
+        with torch.cuda.stream(stream):
+            layer_step(hsdpa, plan, w, b, 0, ws, fused, stream)
+        torch.cuda.synchronize()
+        check.append([b[n].clone() for n in ("q", "k", "out")] + [b["keys"][0].clone(), b["values"][0].clone()])
+        with torch.cuda.stream(stream):
+            for i in range(warmup):
+                layer_step(hsdpa, plan, w, b, i, ws, fused, stream)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            for i in range(steps):
+                layer_step(hsdpa, plan, w, b, i, ws, fused, stream)
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(stream):
+            start.record(stream)
+            graph.replay()
+            end.record(stream)
+        torch.cuda.synchronize()
+        results["fused" if fused else "nodes"] = start.elapsed_time(end) / steps
+        del b, graph
+        torch.cuda.empty_cache()
+    same = all(torch.equal(x, y) for x, y in zip(check[0], check[1]))
+    return results["fused"], results["nodes"], same
+
+
 def cpu_baseline(w_decode, decode_gbs_gpu):
     """Time the AVX-512 BF16 restatement of the reference on this host: the
     reference's decode node has Hq tasks, so it uses min(cores, Hq) threads;
@@ -169,6 +255,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-layer", action="store_true", help="skip the fused layer chain timing")
     ap.add_argument("--prefill-steps", type=int, default=0, help="timed prefill steps (default: --steps, max 20)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -254,6 +341,34 @@ def main():
         wp_cpu = wp
     else:
         wp_cpu = None
+
+    # ---- the layer chain: norms, append, attention, gate -------------------------
+    if not args.no_layer:
+        wl = W.config("decode_32k", seed=1)
+        f_ms, n_ms, same = time_layer(torch, hsdpa, wl, 16, args.steps, args.warmup)
+        if not same:
+            print("fused layer chain differs from the separate nodes", file=sys.stderr)
+            sys.exit(3)
+        layer = {"decode_32k": {"fused_us": round(f_ms * 1e3, 2), "nodes_us": round(n_ms * 1e3, 2),
+                                "launches": {"fused": 4, "nodes": 7}}}
+        log(f"layer decode_32k: fused {f_ms*1e3:.2f} us, nodes {n_ms*1e3:.2f} us")
+        del wl
+        if not args.no_prefill:
+            wl = W.config("prefill_4096_after_8192", seed=1)
+            psteps = args.prefill_steps or min(args.steps, 20)
+            f_ms, n_ms, same = time_layer(torch, hsdpa, wl, 1, psteps, min(args.warmup, 3))
+            if not same:
+                print("fused layer chain differs from the separate nodes", file=sys.stderr)
+                sys.exit(3)
+            layer["prefill_4096_after_8192"] = {"fused_ms": round(f_ms, 4), "nodes_ms": round(n_ms, 4),
+                                                "launches": {"fused": 2, "nodes": 5}}
+            log(f"layer prefill: fused {f_ms:.3f} ms, nodes {n_ms:.3f} ms")
+            del wl
+        result["layer"] = dict(layer, workload="gated Qwen3.5 attention layer: q and k RMS-norm (1+w) + RoPE 64 of 256, "
+                                               "KV append, attention, output gate; fused = hsdpa_attention_layer, "
+                                               "nodes = the five calls in order; bit-identical results checked",
+                               timing="HIP graph of the timed steps")
+        torch.cuda.empty_cache()
 
     # ---- CPU baseline ------------------------------------------------------------
     if not args.no_cpu:

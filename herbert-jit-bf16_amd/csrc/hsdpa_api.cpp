@@ -286,22 +286,13 @@ void hsdpa_plan_destroy(hsdpa_plan *plan) { delete plan; }
 
 uint64_t hsdpa_workspace_bytes(const hsdpa_plan *plan) { return plan ? plan->ws_bytes : 0; }
 
-hsdpa_status hsdpa_attention(const hsdpa_plan *plan, const hsdpa_call *call, void *stream)
+// The attention node on validated arguments; `gate`, when not null, is
+// applied to the output as it is written (row r, head h at gate +
+// r*gate_row + h*head_dim).
+static hsdpa_status run_attention(const hsdpa_plan *plan, const hsdpa_call *call, const uint16_t *gate,
+                                  uint64_t gate_row, hipStream_t st)
 {
-    if (!plan || !call) return HSDPA_ERR_NULL;
     const hsdpa_spec &s = plan->spec;
-    if (call->sink != 0.0f) return HSDPA_ERR_SINK_UNSUPPORTED;
-    if (call->rows == 0) return HSDPA_OK;  // the selector's empty call (attention.rs:129-130)
-    if (call->rows > s.kv_capacity || call->past > s.kv_capacity - call->rows) return HSDPA_ERR_CAPACITY;
-    if (!call->q || !call->keys || !call->values || !call->output || !call->workspace) return HSDPA_ERR_NULL;
-    if (!aligned16(call->q) || !aligned16(call->keys) || !aligned16(call->values) || !aligned16(call->output) ||
-        !aligned16(call->workspace))
-        return HSDPA_ERR_ALIGNMENT;
-    if (call->workspace_bytes < plan->ws_bytes) return HSDPA_ERR_WORKSPACE;
-    const hsdpa_status dev = check_device();
-    if (dev != HSDPA_OK) return dev;
-
-    hipStream_t st = static_cast<hipStream_t>(stream);
     char *ws = static_cast<char *>(call->workspace);
     const uint64_t n = call->past + call->rows;
     const int d = static_cast<int>(s.head_dim);
@@ -328,6 +319,7 @@ hsdpa_status hsdpa_attention(const hsdpa_plan *plan, const hsdpa_call *call, voi
         a.nwg_qk = static_cast<int>((n + a.keys_qk - 1) / a.keys_qk);
         a.nwg_pv = static_cast<int>((n + a.keys_pv - 1) / a.keys_pv);
         a.scale = call->scale;
+        a.gate = gate;
         const hipError_t e = hsdpa::launch_decode(a, d, static_cast<int>(plan->kv_heads), st);
         return e == hipSuccess ? HSDPA_OK : HSDPA_ERR_HIP;
     }
@@ -345,8 +337,94 @@ hsdpa_status hsdpa_attention(const hsdpa_plan *plan, const hsdpa_call *call, voi
     a.kv_stride = s.kv_stride;
     a.gqa = static_cast<int>(s.gqa);
     a.scale = call->scale;
+    a.gate = gate;
+    a.gate_row = gate_row;
     const hipError_t e = hsdpa::launch_prefill(a, d, static_cast<int>(s.heads), st);
     return e == hipSuccess ? HSDPA_OK : HSDPA_ERR_HIP;
+}
+
+// The host checks of the attention node (rows > 0 already established).
+static hsdpa_status check_attention_call(const hsdpa_plan *plan, const hsdpa_call *call)
+{
+    const hsdpa_spec &s = plan->spec;
+    if (call->rows > s.kv_capacity || call->past > s.kv_capacity - call->rows) return HSDPA_ERR_CAPACITY;
+    if (!call->q || !call->keys || !call->values || !call->output || !call->workspace) return HSDPA_ERR_NULL;
+    if (!aligned16(call->q) || !aligned16(call->keys) || !aligned16(call->values) || !aligned16(call->output) ||
+        !aligned16(call->workspace))
+        return HSDPA_ERR_ALIGNMENT;
+    if (call->workspace_bytes < plan->ws_bytes) return HSDPA_ERR_WORKSPACE;
+    return HSDPA_OK;
+}
+
+hsdpa_status hsdpa_attention(const hsdpa_plan *plan, const hsdpa_call *call, void *stream)
+{
+    if (!plan || !call) return HSDPA_ERR_NULL;
+    if (call->sink != 0.0f) return HSDPA_ERR_SINK_UNSUPPORTED;
+    if (call->rows == 0) return HSDPA_OK;  // the selector's empty call (attention.rs:129-130)
+    const hsdpa_status st = check_attention_call(plan, call);
+    if (st != HSDPA_OK) return st;
+    const hsdpa_status dev = check_device();
+    if (dev != HSDPA_OK) return dev;
+    return run_attention(plan, call, nullptr, 0, static_cast<hipStream_t>(stream));
+}
+
+hsdpa_status hsdpa_attention_layer(const hsdpa_plan *plan, const hsdpa_layer_call *call, void *stream)
+{
+    if (!plan || !call) return HSDPA_ERR_NULL;
+    if (call->rows == 0) return HSDPA_OK;
+    const hsdpa_spec &s = plan->spec;
+    // the two head-norm-rope nodes (q, then k), checked as hsdpa_head_norm_rope does
+    const hsdpa_norm_rope_spec qs = {s.heads, s.head_dim, s.q_head, s.q_row, call->rotary_dims,
+                                     call->table_row, call->positions, call->plus_one, 0};
+    const hsdpa_norm_rope_spec ks = {plan->kv_heads, s.head_dim, s.head_dim, call->kv_row, call->rotary_dims,
+                                     call->table_row, call->positions, call->plus_one, 0};
+    hsdpa_status st = check_norm_rope(qs);
+    if (st == HSDPA_OK) st = check_norm_rope(ks);
+    if (st != HSDPA_OK) return st;
+    if (call->rotary_dims && (call->past > call->positions || call->rows > call->positions - call->past))
+        return HSDPA_ERR_CAPACITY;
+    if (call->rows > (1u << 31) - 1) return HSDPA_ERR_CAPACITY;
+    // the attention node
+    const hsdpa_call ac = {call->q,     call->keys, call->values, call->output,    call->rows,
+                           call->past,  call->scale, 0.0f,        call->workspace, call->workspace_bytes};
+    st = check_attention_call(plan, &ac);
+    if (st != HSDPA_OK) return st;
+    if (!call->k || !call->v || !call->q_norm || !call->k_norm || (call->rotary_dims && (!call->cos || !call->sin)))
+        return HSDPA_ERR_NULL;
+    // the gate node: compact heads on each row, read 8 bytes at a time
+    if (call->gate) {
+        if (call->gate_row < s.heads * s.head_dim || call->gate_row > static_cast<uint64_t>(INT32_MAX) / 2)
+            return HSDPA_ERR_STRIDE;
+        if (!aligned16(call->gate) || call->gate_row % 8 != 0) return HSDPA_ERR_ALIGNMENT;
+    }
+    const hsdpa_status dev = check_device();
+    if (dev != HSDPA_OK) return dev;
+    hipStream_t stream_h = static_cast<hipStream_t>(stream);
+    hsdpa::LayerPrepArgs p{};
+    p.q = call->q;
+    p.k = call->k;
+    p.v = call->v;
+    p.keys = call->keys;
+    p.values = call->values;
+    p.q_norm = call->q_norm;
+    p.k_norm = call->k_norm;
+    p.cos = call->cos;
+    p.sin = call->sin;
+    p.rows = call->rows;
+    p.past = call->past;
+    p.q_row = s.q_row;
+    p.q_head = s.q_head;
+    p.kv_row = call->kv_row;
+    p.kv_stride = s.kv_stride;
+    p.table_row = call->table_row;
+    p.heads = static_cast<int>(s.heads);
+    p.kv_heads = static_cast<int>(plan->kv_heads);
+    p.dim = static_cast<int>(s.head_dim);
+    p.rotary = static_cast<int>(call->rotary_dims);
+    p.plus_one = call->plus_one ? 1 : 0;
+    p.eps = call->eps;
+    if (hsdpa::launch_layer_prep(p, stream_h) != hipSuccess) return HSDPA_ERR_HIP;
+    return run_attention(plan, &ac, call->gate, call->gate_row, stream_h);
 }
 
 const char *hsdpa_status_string(hsdpa_status status)

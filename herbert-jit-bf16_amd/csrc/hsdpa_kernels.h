@@ -25,6 +25,7 @@ struct DecodeArgs {
     int nwg_qk, nwg_pv;     // workgroups per KV head of the two passes
     int keys_qk, keys_pv;   // keys per workgroup of the two passes
     float scale;
+    const uint16_t *gate;   // null, or the output gate: head h at gate + h*head_dim
 };
 
 // Causal prefill: `rows` query rows after `past` cached positions.
@@ -37,6 +38,8 @@ struct PrefillArgs {
     uint64_t q_row, q_head, out_row, kv_stride;
     int gqa;
     float scale;
+    const uint16_t *gate;   // null, or the output gate: row r, head h at gate + r*gate_row + h*head_dim
+    uint64_t gate_row;
 };
 
 // Constants of the kernels the host needs to size grids and workspaces.
@@ -68,7 +71,22 @@ struct GateArgs {
     uint64_t rows, width, attn_row, gate_row;
 };
 
+// The element work of a layer before its attention, one wave per (row, head):
+// query heads are normalised and rotated in place; KV heads have k normalised
+// and rotated in place and copied, with the v row, into the cache at position
+// past + row.
+struct LayerPrepArgs {
+    uint16_t *q, *k;
+    const uint16_t *v;
+    uint16_t *keys, *values;
+    const uint16_t *q_norm, *k_norm, *cos, *sin;
+    uint64_t rows, past, q_row, q_head, kv_row, kv_stride, table_row;
+    int heads, kv_heads, dim, rotary, plus_one;
+    float eps;
+};
+
 bool head_dim_supported(int d);
+hipError_t launch_layer_prep(const LayerPrepArgs &a, hipStream_t s);
 hipError_t launch_norm_rope(const NormRopeArgs &a, hipStream_t s);
 hipError_t launch_gate(const GateArgs &a, hipStream_t s);
 hipError_t launch_kv_append(const KvAppendArgs &a, bool vec, hipStream_t s);

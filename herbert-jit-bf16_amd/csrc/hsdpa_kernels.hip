@@ -99,6 +99,18 @@ __device__ __forceinline__ uint32_t cvt_out(float x)
     return e == 0 ? ((b >> 16) & 0x8000u) : r;
 }
 
+// The output gate of one element (ElemOp::SigmoidMul, emit_elem.rs:350-440):
+// e = 0 - g; e = e < 88 ? e : 88 (vminps: the bound when e is NaN); the
+// softmax's exponential; bf16(a / (e + 1)), a the bf16 attention output.
+__device__ __forceinline__ uint16_t gate_bf16(uint16_t a, uint16_t g)
+{
+    float e = 0.0f - __uint_as_float(static_cast<uint32_t>(g) << 16);
+    e = e < 88.0f ? e : 88.0f;
+    e = exp_poly(e);
+    e = e + 1.0f;
+    return static_cast<uint16_t>(cvt_out(__uint_as_float(static_cast<uint32_t>(a) << 16) / e));
+}
+
 // Split eight exponentials into hi and lo bf16 halves, packed in k order.
 __device__ __forceinline__ void split_pack(const float *e, u32x4 &hi, u32x4 &lo)
 {
@@ -595,7 +607,9 @@ __global__ __launch_bounds__(512) void decode_combine(DecodeArgs a)
             os += ored[i][t];
             ls += lred[i];
         }
-        a.out[static_cast<uint64_t>(h) * D + dim] = static_cast<uint16_t>(cvt_out(os / ls));
+        uint16_t ob = static_cast<uint16_t>(cvt_out(os / ls));
+        if (a.gate) ob = gate_bf16(ob, a.gate[static_cast<uint64_t>(h) * D + dim]);
+        a.out[static_cast<uint64_t>(h) * D + dim] = ob;
     }
 }
 
@@ -800,14 +814,23 @@ __global__ __launch_bounds__(512, 1) void prefill_attn(PrefillArgs a)
     lsum += __shfl_xor(lsum, 32);
     if (rowv) {
         uint16_t *op = a.out + row * a.out_row + static_cast<uint64_t>(head) * D;
+        const uint16_t *gp = a.gate ? a.gate + row * a.gate_row + static_cast<uint64_t>(head) * D : nullptr;
 #pragma unroll
         for (int dt = 0; dt < D / 32; dt++)
 #pragma unroll
             for (int c = 0; c < 4; c++) {
-                const uint32_t b0 = cvt_out(o[dt][4 * c] / lsum), b1 = cvt_out(o[dt][4 * c + 1] / lsum);
-                const uint32_t b2 = cvt_out(o[dt][4 * c + 2] / lsum), b3 = cvt_out(o[dt][4 * c + 3] / lsum);
+                uint32_t b0 = cvt_out(o[dt][4 * c] / lsum), b1 = cvt_out(o[dt][4 * c + 1] / lsum);
+                uint32_t b2 = cvt_out(o[dt][4 * c + 2] / lsum), b3 = cvt_out(o[dt][4 * c + 3] / lsum);
+                const int at = 32 * dt + 8 * c + 4 * grp;
+                if (gp) {
+                    const uint2 g = *reinterpret_cast<const uint2 *>(gp + at);
+                    b0 = gate_bf16(static_cast<uint16_t>(b0), static_cast<uint16_t>(g.x));
+                    b1 = gate_bf16(static_cast<uint16_t>(b1), static_cast<uint16_t>(g.x >> 16));
+                    b2 = gate_bf16(static_cast<uint16_t>(b2), static_cast<uint16_t>(g.y));
+                    b3 = gate_bf16(static_cast<uint16_t>(b3), static_cast<uint16_t>(g.y >> 16));
+                }
                 uint2 w = {b0 | (b1 << 16), b2 | (b3 << 16)};
-                *reinterpret_cast<uint2 *>(op + 32 * dt + 8 * c + 4 * grp) = w;
+                *reinterpret_cast<uint2 *>(op + at) = w;
             }
     }
 }
@@ -870,13 +893,15 @@ __device__ __forceinline__ float ftz(float x)
 
 __device__ __forceinline__ float bf16f(uint16_t b) { return __uint_as_float(static_cast<uint32_t>(b) << 16); }
 
-__global__ __launch_bounds__(64) void head_norm_rope(NormRopeArgs a)
+// One (row, head), one wave: x (dim bf16) normalised and rotated in place;
+// `copy`, when not null, receives the same dim values. cs and sn are the
+// table rows of the position (read only when rotary > 0).
+__device__ __forceinline__ void norm_rope_head(uint16_t *x, uint16_t *copy, const uint16_t *w, const uint16_t *cs,
+                                               const uint16_t *sn, int dim, int rotary, int plus_one, float eps,
+                                               uint16_t *ybuf, int l)
 {
-    __shared__ uint16_t ybuf[512];
-    const int l = threadIdx.x, c = l >> 4, L = l & 15;
-    const uint64_t row = blockIdx.x;
-    uint16_t *x = a.data + row * a.row_stride + static_cast<uint64_t>(blockIdx.y) * a.head_stride;
-    const int nb = a.dim / 32, nacc = nb < 4 ? nb : 4;
+    const int c = l >> 4, L = l & 15;
+    const int nb = dim / 32, nacc = nb < 4 ? nb : 4;
     float acc = 0.0f;
     if (c < nacc)
         for (int b = c; b < nb; b += nacc) {
@@ -901,12 +926,12 @@ __global__ __launch_bounds__(64) void head_norm_rope(NormRopeArgs a)
     for (int i = 0; i < 4; i++) h4[i] = h8[i] + h8[i + 4];
     const float u0 = h4[0] + h4[1], u1 = h4[2] + h4[3];
     float ms = u0 + u1;
-    ms = ms * (1.0f / static_cast<float>(a.dim));
-    ms = ms + a.eps;
+    ms = ms * (1.0f / static_cast<float>(dim));
+    ms = ms + eps;
     const float inv = 1.0f / __builtin_sqrtf(ms);
-    for (int i = l; i < a.dim; i += 64) {
-        float ww = bf16f(a.w[i]);
-        if (a.plus_one) ww = ww + 1.0f;
+    for (int i = l; i < dim; i += 64) {
+        float ww = bf16f(w[i]);
+        if (plus_one) ww = ww + 1.0f;
         float v = bf16f(x[i]) * inv;
         v = v * ww;
         ybuf[i] = static_cast<uint16_t>(cvt_out(v));
@@ -914,12 +939,10 @@ __global__ __launch_bounds__(64) void head_norm_rope(NormRopeArgs a)
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    const int half = a.rotary / 2;
-    const uint16_t *cs = a.cos + (a.past + row) * a.table_row;
-    const uint16_t *sn = a.sin + (a.past + row) * a.table_row;
-    for (int i = l; i < a.dim; i += 64) {
+    const int half = rotary / 2;
+    for (int i = l; i < dim; i += 64) {
         uint16_t out = ybuf[i];
-        if (i < a.rotary) {
+        if (i < rotary) {
             const int j = i < half ? i : i - half;
             const float av = bf16f(ybuf[j]), bv = bf16f(ybuf[j + half]);
             const float cv = bf16f(cs[j]), sv = bf16f(sn[j]);
@@ -927,13 +950,44 @@ __global__ __launch_bounds__(64) void head_norm_rope(NormRopeArgs a)
             out = static_cast<uint16_t>(cvt_out(r));
         }
         x[i] = out;
+        if (copy) copy[i] = out;
     }
 }
 
+__global__ __launch_bounds__(64) void head_norm_rope(NormRopeArgs a)
+{
+    __shared__ uint16_t ybuf[512];
+    const uint64_t row = blockIdx.x;
+    uint16_t *x = a.data + row * a.row_stride + static_cast<uint64_t>(blockIdx.y) * a.head_stride;
+    norm_rope_head(x, nullptr, a.w, a.cos + (a.past + row) * a.table_row, a.sin + (a.past + row) * a.table_row,
+                   a.dim, a.rotary, a.plus_one, a.eps, ybuf, static_cast<int>(threadIdx.x));
+}
+
+// The layer chain's element work before the attention (the head-norm-rope
+// node for q then k, and the kv-append node, lowering.rs:549-592) in one
+// launch: grid (rows, heads + kv_heads), one wave per (row, head). A KV
+// head's wave writes the normalised k row both in place and into the cache,
+// then copies the v row; the results equal the three nodes run in order.
+__global__ __launch_bounds__(64) void layer_prep(LayerPrepArgs a)
+{
+    __shared__ uint16_t ybuf[512];
+    const uint64_t row = blockIdx.x, pos = a.past + row;
+    const int y = static_cast<int>(blockIdx.y), l = static_cast<int>(threadIdx.x);
+    const uint16_t *cs = a.cos + pos * a.table_row, *sn = a.sin + pos * a.table_row;
+    if (y < a.heads) {
+        norm_rope_head(a.q + row * a.q_row + static_cast<uint64_t>(y) * a.q_head, nullptr, a.q_norm, cs, sn, a.dim,
+                       a.rotary, a.plus_one, a.eps, ybuf, l);
+        return;
+    }
+    const uint64_t h = static_cast<uint64_t>(y - a.heads);
+    const uint64_t dst = h * a.kv_stride + pos * a.dim, src = row * a.kv_row + h * a.dim;
+    norm_rope_head(a.k + src, a.keys + dst, a.k_norm, cs, sn, a.dim, a.rotary, a.plus_one, a.eps, ybuf, l);
+    for (int i = l; i < a.dim; i += 64) a.values[dst + i] = a.v[src + i];
+}
+
 // ---------------------------------------------------------------------------
-// Output gate (ElemOp::SigmoidMul, emit_elem.rs:350-440): e = 0 - g;
-// e = e < 88 ? e : 88 (vminps: the bound when e is NaN); the softmax's
-// exponential; y = bf16(a / (e + 1)). Grid-stride over rows x width.
+// Output gate (the attention-output-gate node): gate_bf16 per element,
+// grid-stride over rows x width.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void output_gate(GateArgs a)
 {
@@ -942,11 +996,7 @@ __global__ __launch_bounds__(256) void output_gate(GateArgs a)
          i += static_cast<uint64_t>(gridDim.x) * blockDim.x) {
         const uint64_t r = i / a.width, c = i - r * a.width;
         uint16_t *ap = a.attn + r * a.attn_row + c;
-        float e = 0.0f - bf16f(a.gate[r * a.gate_row + c]);
-        e = e < 88.0f ? e : 88.0f;
-        e = exp_poly(e);
-        e = e + 1.0f;
-        *ap = static_cast<uint16_t>(cvt_out(bf16f(*ap) / e));
+        *ap = gate_bf16(*ap, a.gate[r * a.gate_row + c]);
     }
 }
 
@@ -1015,6 +1065,13 @@ hipError_t launch_norm_rope(const NormRopeArgs &a, hipStream_t s)
 {
     hipLaunchKernelGGL(head_norm_rope, dim3(static_cast<unsigned>(a.rows), static_cast<unsigned>(a.heads)), dim3(64), 0,
                        s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_layer_prep(const LayerPrepArgs &a, hipStream_t s)
+{
+    hipLaunchKernelGGL(layer_prep, dim3(static_cast<unsigned>(a.rows), static_cast<unsigned>(a.heads + a.kv_heads)),
+                       dim3(64), 0, s, a);
     return hipGetLastError();
 }
 

@@ -11,6 +11,6 @@ from .binding import (  # noqa: F401
     HsdpaError, Plan, Spec, Call, STATUS, library, library_path, attention_torch,
     KvSpec, KvCall, kv_spec, kv_append_raw, kv_append_torch,
     NormRopeSpec, NormRopeCall, GateSpec, GateCall, head_norm_rope_torch, output_gate_torch,
-    kv_restore_raw, kv_take_raw,
+    kv_restore_raw, kv_take_raw, LayerCall, attention_layer_torch,
 )
 from . import snapshot  # noqa: F401

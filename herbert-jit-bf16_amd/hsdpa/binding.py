@@ -23,7 +23,8 @@ STATUS = {
 }
 EXPORTS = ["hsdpa_plan_create", "hsdpa_plan_destroy", "hsdpa_workspace_bytes", "hsdpa_attention",
            "hsdpa_status_string", "hsdpa_version", "hsdpa_kv_check", "hsdpa_kv_append",
-           "hsdpa_head_norm_rope", "hsdpa_output_gate", "hsdpa_kv_restore", "hsdpa_kv_take"]
+           "hsdpa_head_norm_rope", "hsdpa_output_gate", "hsdpa_kv_restore", "hsdpa_kv_take",
+           "hsdpa_attention_layer"]
 
 
 class HsdpaError(RuntimeError):
@@ -80,6 +81,16 @@ class GateCall(ctypes.Structure):
     _fields_ = [("attn", ctypes.c_void_p), ("gate", ctypes.c_void_p), ("rows", ctypes.c_uint64)]
 
 
+class LayerCall(ctypes.Structure):
+    """hsdpa_layer_call: the attention chain of one layer."""
+    _fields_ = [(n, ctypes.c_void_p) for n in ("q", "k", "v", "keys", "values", "output", "gate", "q_norm",
+                                                "k_norm", "cos", "sin")] + \
+               [(n, ctypes.c_uint64) for n in ("rows", "past", "kv_row", "gate_row", "rotary_dims", "table_row",
+                                                "positions")] + \
+               [("scale", ctypes.c_float), ("eps", ctypes.c_float), ("plus_one", ctypes.c_uint32),
+                ("reserved", ctypes.c_uint32), ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_uint64)]
+
+
 def library_path() -> str:
     return os.path.join(_HERE, _LIB_NAME)
 
@@ -119,6 +130,8 @@ def library():
         L.hsdpa_kv_take.argtypes = [ctypes.POINTER(KvSpec), u16p, u16p, u16p, ctypes.c_uint64, ctypes.c_uint64,
                                     ctypes.c_void_p]
         L.hsdpa_kv_take.restype = ctypes.c_int
+        L.hsdpa_attention_layer.argtypes = [ctypes.c_void_p, ctypes.POINTER(LayerCall), ctypes.c_void_p]
+        L.hsdpa_attention_layer.restype = ctypes.c_int
         _lib = L
     return _lib
 
@@ -264,3 +277,25 @@ def kv_take_raw(spec: KvSpec, keys: int, values: int, snapshot_layer: int, snap_
                                  ctypes.c_void_p(stream))
     if rc != 0:
         raise HsdpaError(rc, "hsdpa_kv_take")
+
+
+def attention_layer_torch(plan: Plan, q, k, v, keys, values, out, q_norm, k_norm, cos, sin, rows: int, past: int,
+                          scale: float, eps: float, workspace, kv_row: int, rotary_dims: int, gate=None,
+                          gate_row: int = 0, plus_one: bool = True, table_row: int | None = None,
+                          positions: int | None = None, stream=None) -> None:
+    """The layer chain (hsdpa_attention_layer) on torch device tensors holding
+    bf16 bits: q and k normalised and rotated in place, k and v appended to
+    the cache at `past`, the attention into `out`, gated when `gate` (a view,
+    e.g. of q at q_dim) is given."""
+    import torch
+
+    tr = rotary_dims // 2 if table_row is None else table_row
+    pos = (cos.numel() // tr if tr else 0) if positions is None else positions
+    ptr = lambda t: t.data_ptr() if t is not None else 0
+    call = LayerCall(ptr(q), ptr(k), ptr(v), ptr(keys), ptr(values), ptr(out), ptr(gate), ptr(q_norm), ptr(k_norm),
+                     ptr(cos), ptr(sin), rows, past, kv_row, gate_row, rotary_dims, tr, pos, scale, eps,
+                     int(plus_one), 0, ptr(workspace), workspace.numel() * workspace.element_size())
+    s = torch.cuda.current_stream() if stream is None else stream
+    rc = library().hsdpa_attention_layer(plan.handle, ctypes.byref(call), ctypes.c_void_p(s.cuda_stream))
+    if rc != 0:
+        raise HsdpaError(rc, "hsdpa_attention_layer")

@@ -36,6 +36,9 @@
  *                           (src/jit/target/x86/emit_elem.rs:239-335, 479-520)
  *   hsdpa_output_gate       the attention-output-gate node (lowering.rs:642-666):
  *                           ElemOp::SigmoidMul per row (emit_elem.rs:350-440)
+ *   hsdpa_attention_layer   the attention chain of one layer, lowering.rs:549-666:
+ *                           head-norm-rope (q, k), kv-append, attention and
+ *                           attention-output-gate in one call and fewer launches
  *   hsdpa_kv_restore        the KV half of Runner::restore_from (src/jit/model.rs:786-856)
  *                           for one layer: snapshot (host) to the live cache (device)
  *   hsdpa_kv_take           the KV half of Runner::snapshot_take (model.rs:728-773)
@@ -207,6 +210,51 @@ typedef struct hsdpa_gate_call {
 } hsdpa_gate_call;
 
 hsdpa_status hsdpa_output_gate(const hsdpa_gate_spec *spec, const hsdpa_gate_call *call, void *stream);
+
+/* ---- The attention chain of one layer --------------------------------------
+ * The nodes the engine emits for a full-attention layer
+ * (src/jit/schedule/lowering.rs:549-666): head-norm-rope on q, head-norm-rope on
+ * k, kv-append, attention, attention-output-gate. One launch does the two
+ * norms and the append (q and k normalised and rotated in place, as the
+ * node does; k and v then written into the cache at past .. past+rows-1);
+ * the attention follows and applies the gate as it writes the output. Every
+ * buffer (q, k, the cache, output) ends bit-identical to hsdpa_head_norm_rope
+ * (q), hsdpa_head_norm_rope (k), hsdpa_kv_append, hsdpa_attention and
+ * hsdpa_output_gate called in that order with the same arguments. Decode is 4
+ * launches instead of 7, prefill 2 instead of 5. The plan gives heads, gqa,
+ * head_dim, q_row, q_head, out_row and the cache geometry; the norms take
+ * head_dim weights and the RoPE tables as in hsdpa_norm_rope_spec. */
+typedef struct hsdpa_layer_call {
+    uint16_t *q;              /* [rows][q_row]: each head normalised and rotated in place */
+    uint16_t *k;              /* the block's K projections, normalised and rotated in place:
+                                 row r, KV head h at k + r*kv_row + h*head_dim */
+    const uint16_t *v;        /* the block's V projections, same layout */
+    uint16_t *keys;           /* the cache, as hsdpa_call, written at past .. past+rows-1 */
+    uint16_t *values;
+    uint16_t *output;         /* as hsdpa_call; gated when gate is not null */
+    const uint16_t *gate;     /* null: no gate; else row r, head h at gate + r*gate_row + h*head_dim
+                                 (q + q_dim with gate_row = q_row on the gated model); 16-byte
+                                 aligned, gate_row a multiple of 8 */
+    const uint16_t *q_norm;   /* head_dim bf16 */
+    const uint16_t *k_norm;   /* head_dim bf16 */
+    const uint16_t *cos;      /* [positions][table_row] bf16 (unused when rotary_dims = 0) */
+    const uint16_t *sin;
+    uint64_t rows;            /* 0 = nothing */
+    uint64_t past;
+    uint64_t kv_row;          /* elements between rows of k and v (>= kv_heads*head_dim) */
+    uint64_t gate_row;
+    uint64_t rotary_dims;     /* a multiple of 32, at most head_dim; 0 = none */
+    uint64_t table_row;
+    uint64_t positions;       /* positions the tables hold */
+    float scale;              /* the attention's scale */
+    float eps;                /* RMSNorm epsilon */
+    uint32_t plus_one;        /* 1: (1 + w), the Gemma convention of Qwen3.5 */
+    uint32_t reserved;        /* 0 */
+    void *workspace;          /* as hsdpa_call */
+    uint64_t workspace_bytes;
+} hsdpa_layer_call;
+
+hsdpa_status hsdpa_attention_layer(const hsdpa_plan *plan, const hsdpa_layer_call *call, void *stream);
 
 /* ---- KV snapshot of one layer ----------------------------------------------
  * A snapshot layer holds K[heads][snap_positions][head_dim] then

@@ -143,3 +143,38 @@ def test_outlier_workload():
         assert (std > 10).sum() == 4
         rows = np.abs(v[h]).max(axis=1)
         assert (rows > 12).sum() >= 5
+
+
+# ---- record layouts: the ctypes mirrors against the C header -------------------
+
+RECORDS = {
+    "hsdpa_spec": binding.Spec, "hsdpa_call": binding.Call, "hsdpa_kv_spec": binding.KvSpec,
+    "hsdpa_kv_call": binding.KvCall, "hsdpa_norm_rope_spec": binding.NormRopeSpec,
+    "hsdpa_norm_rope_call": binding.NormRopeCall, "hsdpa_gate_spec": binding.GateSpec,
+    "hsdpa_gate_call": binding.GateCall, "hsdpa_layer_call": binding.LayerCall,
+}
+
+
+def test_record_layouts_match_the_header(tmp_path):
+    """Every field of every record sits at the same offset, and every record
+    has the same size, in the C compiler's layout and in the binding's."""
+    if subprocess.run(["which", "gcc"], capture_output=True).returncode != 0:
+        pytest.skip("no C compiler")
+    lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "hsdpa.h"', "int main(void) {"]
+    for rec, cls in RECORDS.items():
+        lines.append(f'printf("{rec} size %zu\\n", sizeof({rec}));')
+        for fname, _ in cls._fields_:
+            lines.append(f'printf("{rec} {fname} %zu\\n", offsetof({rec}, {fname}));')
+    lines.append("return 0; }")
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-I", os.path.join(ROOT, "include"), str(src), "-o", str(exe)], check=True)
+    got = {}
+    for line in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.splitlines():
+        rec, field, value = line.split()
+        got[(rec, field)] = int(value)
+    for rec, cls in RECORDS.items():
+        assert got[(rec, "size")] == ctypes.sizeof(cls), rec
+        for fname, _ in cls._fields_:
+            assert got[(rec, fname)] == getattr(cls, fname).offset, (rec, fname)
