@@ -954,13 +954,115 @@ __device__ __forceinline__ void norm_rope_head(uint16_t *x, uint16_t *copy, cons
     }
 }
 
+// norm_rope_head for a compile-time dim (64, 128, 256): the same operations in
+// the same order, with every global load (the sum-of-squares elements, x and w
+// in output order, the table entries) issued before the first use, so that the
+// wave waits on one round trip instead of three.
+template <int DIM>
+__device__ __forceinline__ void norm_rope_head_d(uint16_t *x, uint16_t *copy, const uint16_t *w, const uint16_t *cs,
+                                                 const uint16_t *sn, int rotary, int plus_one, float eps,
+                                                 uint16_t *ybuf, int l)
+{
+    constexpr int NB = DIM / 32, NACC = NB < 4 ? NB : 4, PB = (NB + NACC - 1) / NACC, PE = DIM / 64;
+    const int c = l >> 4, L = l & 15, half = rotary / 2;
+    uint16_t s1[PB], s0[PB], xe[PE], we[PE], ce[PE] = {}, se[PE] = {};
+#pragma unroll
+    for (int p = 0; p < PB; p++) {
+        const int b = c + NACC * p, bb = (c < NACC && b < NB) ? b : 0;
+        s1[p] = x[32 * bb + 2 * L + 1];
+        s0[p] = x[32 * bb + 2 * L];
+    }
+#pragma unroll
+    for (int p = 0; p < PE; p++) {
+        xe[p] = x[l + 64 * p];
+        we[p] = w[l + 64 * p];
+    }
+    if (rotary) {
+#pragma unroll
+        for (int p = 0; p < PE; p++) {
+            const int i = l + 64 * p, j = i < rotary ? (i < half ? i : i - half) : 0;
+            ce[p] = cs[j];
+            se[p] = sn[j];
+        }
+    }
+    float acc = 0.0f;
+    if (c < NACC) {
+#pragma unroll
+        for (int p = 0; p < PB; p++)
+            if (c + NACC * p < NB) {
+                const float x1 = bf16_daz(s1[p]), x0 = bf16_daz(s0[p]);
+                acc = ftz(__builtin_fmaf(x1, x1, acc));
+                acc = ftz(__builtin_fmaf(x0, x0, acc));
+            }
+    }
+    // chains 1..3 added in order into chain 0
+    const float c1 = __shfl(acc, L + 16), c2 = __shfl(acc, L + 32), c3 = __shfl(acc, L + 48);
+    float s = acc;
+    if (NACC > 1) s = s + c1;
+    if (NACC > 2) s = s + c2;
+    if (NACC > 3) s = s + c3;
+    // the hsum tree over the 16 lanes of chain 0, in every lane
+    float lv[16];
+#pragma unroll
+    for (int i = 0; i < 16; i++) lv[i] = __shfl(s, i);
+    float h8[8], h4[4];
+#pragma unroll
+    for (int i = 0; i < 8; i++) h8[i] = lv[i] + lv[i + 8];
+#pragma unroll
+    for (int i = 0; i < 4; i++) h4[i] = h8[i] + h8[i + 4];
+    const float u0 = h4[0] + h4[1], u1 = h4[2] + h4[3];
+    float ms = u0 + u1;
+    ms = ms * (1.0f / static_cast<float>(DIM));
+    ms = ms + eps;
+    const float inv = 1.0f / __builtin_sqrtf(ms);
+#pragma unroll
+    for (int p = 0; p < PE; p++) {
+        float ww = bf16f(we[p]);
+        if (plus_one) ww = ww + 1.0f;
+        float v = bf16f(xe[p]) * inv;
+        v = v * ww;
+        ybuf[l + 64 * p] = static_cast<uint16_t>(cvt_out(v));
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int p = 0; p < PE; p++) {
+        const int i = l + 64 * p;
+        uint16_t out = ybuf[i];
+        if (i < rotary) {
+            const int j = i < half ? i : i - half;
+            const float av = bf16f(ybuf[j]), bv = bf16f(ybuf[j + half]);
+            const float cv = bf16f(ce[p]), sv = bf16f(se[p]);
+            const float r = i < half ? __builtin_fmaf(-bv, sv, av * cv) : __builtin_fmaf(bv, cv, av * sv);
+            out = static_cast<uint16_t>(cvt_out(r));
+        }
+        x[i] = out;
+        if (copy) copy[i] = out;
+    }
+}
+
+// One (row, head) of the node by the wave: the compile-time routine for the
+// engine's head dims, the general one otherwise.
+__device__ __forceinline__ void norm_rope_any(uint16_t *x, uint16_t *copy, const uint16_t *w, const uint16_t *cs,
+                                              const uint16_t *sn, int dim, int rotary, int plus_one, float eps,
+                                              uint16_t *ybuf, int l)
+{
+    switch (dim) {
+    case 64: norm_rope_head_d<64>(x, copy, w, cs, sn, rotary, plus_one, eps, ybuf, l); break;
+    case 128: norm_rope_head_d<128>(x, copy, w, cs, sn, rotary, plus_one, eps, ybuf, l); break;
+    case 256: norm_rope_head_d<256>(x, copy, w, cs, sn, rotary, plus_one, eps, ybuf, l); break;
+    default: norm_rope_head(x, copy, w, cs, sn, dim, rotary, plus_one, eps, ybuf, l); break;
+    }
+}
+
 __global__ __launch_bounds__(64) void head_norm_rope(NormRopeArgs a)
 {
     __shared__ uint16_t ybuf[512];
     const uint64_t row = blockIdx.x;
     uint16_t *x = a.data + row * a.row_stride + static_cast<uint64_t>(blockIdx.y) * a.head_stride;
-    norm_rope_head(x, nullptr, a.w, a.cos + (a.past + row) * a.table_row, a.sin + (a.past + row) * a.table_row,
-                   a.dim, a.rotary, a.plus_one, a.eps, ybuf, static_cast<int>(threadIdx.x));
+    norm_rope_any(x, nullptr, a.w, a.cos + (a.past + row) * a.table_row, a.sin + (a.past + row) * a.table_row, a.dim,
+                  a.rotary, a.plus_one, a.eps, ybuf, static_cast<int>(threadIdx.x));
 }
 
 // The layer chain's element work before the attention (the head-norm-rope
@@ -975,13 +1077,13 @@ __global__ __launch_bounds__(64) void layer_prep(LayerPrepArgs a)
     const int y = static_cast<int>(blockIdx.y), l = static_cast<int>(threadIdx.x);
     const uint16_t *cs = a.cos + pos * a.table_row, *sn = a.sin + pos * a.table_row;
     if (y < a.heads) {
-        norm_rope_head(a.q + row * a.q_row + static_cast<uint64_t>(y) * a.q_head, nullptr, a.q_norm, cs, sn, a.dim,
-                       a.rotary, a.plus_one, a.eps, ybuf, l);
+        norm_rope_any(a.q + row * a.q_row + static_cast<uint64_t>(y) * a.q_head, nullptr, a.q_norm, cs, sn, a.dim,
+                      a.rotary, a.plus_one, a.eps, ybuf, l);
         return;
     }
     const uint64_t h = static_cast<uint64_t>(y - a.heads);
     const uint64_t dst = h * a.kv_stride + pos * a.dim, src = row * a.kv_row + h * a.dim;
-    norm_rope_head(a.k + src, a.keys + dst, a.k_norm, cs, sn, a.dim, a.rotary, a.plus_one, a.eps, ybuf, l);
+    norm_rope_any(a.k + src, a.keys + dst, a.k_norm, cs, sn, a.dim, a.rotary, a.plus_one, a.eps, ybuf, l);
     for (int i = l; i < a.dim; i += 64) a.values[dst + i] = a.v[src + i];
 }
 

@@ -33,10 +33,10 @@ class Chain:
     when gated), k and v [rows][kv_heads*hd], the cache (positions < past hold
     earlier keys, the rest stale bytes), the norm weights and RoPE tables."""
 
-    def __init__(self, heads, kvh, hd, rows, past, cap, gated, rotary, seed):
+    def __init__(self, heads, kvh, hd, rows, past, cap, gated, rotary, seed, kv_offset=0):
         rng = np.random.default_rng(seed)
         self.heads, self.kvh, self.hd, self.rows, self.past, self.cap = heads, kvh, hd, rows, past, cap
-        self.gated, self.rotary = gated, rotary
+        self.gated, self.rotary, self.kv_offset = gated, rotary, kv_offset
         self.q_dim = heads * hd
         self.q_row = 2 * self.q_dim if gated else self.q_dim
         self.kv_row = kvh * hd
@@ -54,7 +54,9 @@ class Chain:
     def device(self, torch):
         dev = torch.device("cuda")
         t = lambda a: torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).to(dev)
-        return dict(q=t(self.q), k=t(self.k), v=t(self.v), keys=t(self.keys), values=t(self.values),
+        o = self.kv_offset   # k and v may start o elements into their allocation
+        pad = lambda a: t(np.concatenate([np.zeros(o, np.uint16), a]))[o:]
+        return dict(q=t(self.q), k=pad(self.k), v=pad(self.v), keys=t(self.keys), values=t(self.values),
                     q_norm=t(self.q_norm), k_norm=t(self.k_norm), cos=t(self.cos), sin=t(self.sin),
                     out=torch.full((self.rows * self.q_dim,), -1, dtype=torch.int16, device=dev))
 
@@ -103,14 +105,16 @@ CASES = [
     ("prefill_ragged_d64_g2", 8, 4, 64, 70, 33, 200, True, 32),
     ("decode_g16_no_rope", 16, 1, 256, 1, 5000, 5100, True, 0),
     ("decode_g32_through_prefill", 32, 1, 128, 1, 700, 800, True, 64),
+    # k and v 2 bytes off: the decode takes the separate element launch
+    ("decode_unaligned_kv", 16, 2, 256, 1, 1000, 1100, True, 64, 1),
 ]
 
 
 @pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
 def test_layer_equals_the_nodes(torch_cuda, case):
-    name, heads, kvh, hd, rows, past, cap, gated, rotary = case
+    name, heads, kvh, hd, rows, past, cap, gated, rotary = case[:9]
     print(f"layer case {name}", flush=True)
-    c = Chain(heads, kvh, hd, rows, past, cap, gated, rotary, seed=len(name))
+    c = Chain(heads, kvh, hd, rows, past, cap, gated, rotary, seed=len(name), kv_offset=case[9] if len(case) > 9 else 0)
     fused = run_fused(torch_cuda, c)
     nodes = run_nodes(torch_cuda, c)
     for n in ("q", "k", "keys", "values", "out"):
