@@ -51,11 +51,12 @@ hsdpa_status check_spec(const hsdpa_spec &s)
     return HSDPA_OK;
 }
 
-// One architecture check per device, cached.
+// One architecture check per device, cached with its compute-unit count.
 std::mutex g_dev_mu;
 int g_dev_state[64];  // 0 unknown, 1 gfx950, 2 other
+int g_dev_cus[64];
 
-hsdpa_status check_device()
+hsdpa_status check_device(int *cus = nullptr)
 {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return HSDPA_ERR_NO_DEVICE;
@@ -65,7 +66,9 @@ hsdpa_status check_device()
         hipDeviceProp_t p;
         if (hipGetDeviceProperties(&p, dev) != hipSuccess) return HSDPA_ERR_NO_DEVICE;
         g_dev_state[dev] = std::strncmp(p.gcnArchName, "gfx950", 6) == 0 ? 1 : 2;
+        g_dev_cus[dev] = p.multiProcessorCount;
     }
+    if (cus) *cus = g_dev_cus[dev];
     return g_dev_state[dev] == 1 ? HSDPA_OK : HSDPA_ERR_NO_DEVICE;
 }
 
@@ -290,7 +293,7 @@ uint64_t hsdpa_workspace_bytes(const hsdpa_plan *plan) { return plan ? plan->ws_
 // applied to the output as it is written (row r, head h at gate +
 // r*gate_row + h*head_dim).
 static hsdpa_status run_attention(const hsdpa_plan *plan, const hsdpa_call *call, const uint16_t *gate,
-                                  uint64_t gate_row, hipStream_t st)
+                                  uint64_t gate_row, hipStream_t st, int cus)
 {
     const hsdpa_spec &s = plan->spec;
     char *ws = static_cast<char *>(call->workspace);
@@ -315,7 +318,11 @@ static hsdpa_status run_attention(const hsdpa_plan *plan, const hsdpa_call *call
         a.q_head = s.q_head;
         a.g = static_cast<int>(s.gqa);
         a.keys_qk = hsdpa::kDecodeKeysQK;
-        a.keys_pv = hsdpa::kDecodeKeysPV;
+        // pass 2 takes 8 tiles per workgroup, or 4 while the smaller
+        // workgroups still fit the compute units in one round (short caches:
+        // twice the workgroups, measured faster up to 16K keys at 2 KV heads)
+        const uint64_t nwg4 = (n + 4 * hsdpa::kKeyTile - 1) / (4 * hsdpa::kKeyTile);
+        a.keys_pv = plan->kv_heads * nwg4 <= static_cast<uint64_t>(cus) ? 4 * hsdpa::kKeyTile : hsdpa::kDecodeKeysPV;
         a.nwg_qk = static_cast<int>((n + a.keys_qk - 1) / a.keys_qk);
         a.nwg_pv = static_cast<int>((n + a.keys_pv - 1) / a.keys_pv);
         a.scale = call->scale;
@@ -363,9 +370,10 @@ hsdpa_status hsdpa_attention(const hsdpa_plan *plan, const hsdpa_call *call, voi
     if (call->rows == 0) return HSDPA_OK;  // the selector's empty call (attention.rs:129-130)
     const hsdpa_status st = check_attention_call(plan, call);
     if (st != HSDPA_OK) return st;
-    const hsdpa_status dev = check_device();
+    int cus = 0;
+    const hsdpa_status dev = check_device(&cus);
     if (dev != HSDPA_OK) return dev;
-    return run_attention(plan, call, nullptr, 0, static_cast<hipStream_t>(stream));
+    return run_attention(plan, call, nullptr, 0, static_cast<hipStream_t>(stream), cus);
 }
 
 hsdpa_status hsdpa_attention_layer(const hsdpa_plan *plan, const hsdpa_layer_call *call, void *stream)
@@ -397,7 +405,8 @@ hsdpa_status hsdpa_attention_layer(const hsdpa_plan *plan, const hsdpa_layer_cal
             return HSDPA_ERR_STRIDE;
         if (!aligned16(call->gate) || call->gate_row % 8 != 0) return HSDPA_ERR_ALIGNMENT;
     }
-    const hsdpa_status dev = check_device();
+    int cus = 0;
+    const hsdpa_status dev = check_device(&cus);
     if (dev != HSDPA_OK) return dev;
     hipStream_t stream_h = static_cast<hipStream_t>(stream);
     hsdpa::LayerPrepArgs p{};
@@ -424,7 +433,7 @@ hsdpa_status hsdpa_attention_layer(const hsdpa_plan *plan, const hsdpa_layer_cal
     p.plus_one = call->plus_one ? 1 : 0;
     p.eps = call->eps;
     if (hsdpa::launch_layer_prep(p, stream_h) != hipSuccess) return HSDPA_ERR_HIP;
-    return run_attention(plan, &ac, call->gate, call->gate_row, stream_h);
+    return run_attention(plan, &ac, call->gate, call->gate_row, stream_h, cus);
 }
 
 const char *hsdpa_status_string(hsdpa_status status)

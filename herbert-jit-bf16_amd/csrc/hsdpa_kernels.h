@@ -45,7 +45,7 @@ struct PrefillArgs {
 // Constants of the kernels the host needs to size grids and workspaces.
 constexpr int kKeyTile = 32;          // keys per MFMA key block
 constexpr int kDecodeKeysQK = 128;    // keys per decode pass-1 workgroup (4 waves x 1 tile)
-constexpr int kDecodeKeysPV = 256;    // keys per decode pass-2 workgroup (8 waves x 1 tile)
+constexpr int kDecodeKeysPV = 256;    // keys per decode pass-2 workgroup (8 waves x 1 tile; 4 x 1 on short caches)
 constexpr int kDecodeMaxGroup = 16;   // query heads per KV head the decode kernels take
 
 // KV append: token-major block rows into the head-major cache.

@@ -160,14 +160,17 @@ __device__ __forceinline__ float fmaxnn(float a, float b) { return b > a ? b : a
 // Maximum over each half wave (lanes 0..31 in lane 31, 32..63 in lane 63) and
 // over the whole wave (in lane 63) when `whole`. -inf is the identity; NaN
 // inputs are ignored like in the scalar reductions.
-__device__ __forceinline__ float wave_max_hi(float x, bool whole)
+// The maximum over groups of `lanes` (16, 32 or 64) consecutive lanes: after
+// the row steps every lane of a row holds the row's maximum; row_bcast:15
+// leaves a 32-lane group's in its lane 31, row_bcast:31 the wave's in lane 63.
+__device__ __forceinline__ float group_max_hi(float x, int lanes)
 {
     x = fmaxnn(x, dpp<0xB1, 0xF>(x, kNegInf));
     x = fmaxnn(x, dpp<0x4E, 0xF>(x, kNegInf));
     x = fmaxnn(x, dpp<0x141, 0xF>(x, kNegInf));
     x = fmaxnn(x, dpp<0x140, 0xF>(x, kNegInf));
-    x = fmaxnn(x, dpp<0x142, 0xA>(x, kNegInf));
-    if (whole) x = fmaxnn(x, dpp<0x143, 0xC>(x, kNegInf));
+    if (lanes >= 32) x = fmaxnn(x, dpp<0x142, 0xA>(x, kNegInf));
+    if (lanes >= 64) x = fmaxnn(x, dpp<0x143, 0xC>(x, kNegInf));
     return x;
 }
 
@@ -396,7 +399,7 @@ __global__ __launch_bounds__(256) void decode_qk(DecodeArgs a)
 
 // ---------------------------------------------------------------------------
 // Decode pass 2: exponentials at the exact maximum and P.V partial sums.
-// grid (nwg_pv, kv_heads), 512 threads, keys_pv = 256 (8 tiles of 32).
+// grid (nwg_pv, kv_heads), 64 W threads, keys_pv = 32 W (W tiles of 32).
 //  1. wave w loads V tile w (whole rows) into registers;
 //  2. the exact maximum per query head is reduced from the pass-1 maxima;
 //  3. the g x 256 exponentials are computed once, split into hi + lo bf16 and
@@ -406,24 +409,27 @@ __global__ __launch_bounds__(256) void decode_qk(DecodeArgs a)
 //  4. the V tiles go to LDS (swizzled for the 16-row transpose reads);
 //  5. wave w computes O^T = V^T . P^T for its dimension blocks over its
 //     share of the tiles; O = O(hi columns) + O(lo columns).
-// Static LDS at D = 256: 131 072 + 16 896 + ~2 600 bytes.
+// W waves (and W tiles of keys) per workgroup: W = 8 holds 131 072 + 16 896 +
+// ~2 600 bytes of LDS at D = 256, one workgroup per CU; W = 4 half of that, two
+// per CU, so that one workgroup's work after its last load overlaps another's
+// stream when the grid takes several rounds.
 // ---------------------------------------------------------------------------
-constexpr int kPvWaves = 8;
-
-template <int D>
-__global__ __launch_bounds__(512, 1) void decode_pv(DecodeArgs a)
+template <int D, int W>
+__global__ __launch_bounds__(64 * W, 8 / W) void decode_pv(DecodeArgs a)
 {
-    constexpr int KEYS = kPvWaves * kKeyTile;                   // 256
+    constexpr int THREADS = 64 * W;
+    constexpr int KEYS = W * kKeyTile;                          // 256 or 128
     constexpr int PS = KEYS + 8;                                // P column stride, bf16
     constexpr int DB = D / 16;                                  // 16-dimension blocks
-    constexpr int DBW = DB >= kPvWaves ? DB / kPvWaves : 1;     // blocks per wave
-    constexpr int PARTS = DB >= kPvWaves ? 1 : kPvWaves / DB;   // waves per block
-    constexpr int WPP = kPvWaves / PARTS;                       // waves per part
-    constexpr int TPP = kPvWaves / PARTS;                       // tiles per wave
-    __shared__ __attribute__((aligned(16))) uint16_t vt[kPvWaves][kKeyTile * D];
+    constexpr int DBW = DB >= W ? DB / W : 1;                   // blocks per wave
+    constexpr int PARTS = DB >= W ? 1 : W / DB;                 // waves per block
+    constexpr int WPP = W / PARTS;                              // waves per part
+    constexpr int TPP = W / PARTS;                              // tiles per wave
+    static_assert(THREADS / KEYS == 2, "two head parities per workgroup");
+    __shared__ __attribute__((aligned(16))) uint16_t vt[W][kKeyTile * D];
     __shared__ __attribute__((aligned(16))) uint16_t pc[2 * kDecodeMaxGroup * PS];
     __shared__ float smax[kDecodeMaxGroup];
-    __shared__ float lpart[kPvWaves][kDecodeMaxGroup];
+    __shared__ float lpart[W][kDecodeMaxGroup];
     __shared__ __attribute__((aligned(16))) float ored[PARTS > 1 ? (PARTS - 1) * WPP * 2 * DBW * 4 * 64 : 1];
     const int kvh = blockIdx.y, wg = blockIdx.x, tid = threadIdx.x;
     const int wave = tid >> 6, l = tid & 63, j = l & 15, G = l >> 4;
@@ -443,11 +449,11 @@ __global__ __launch_bounds__(512, 1) void decode_pv(DecodeArgs a)
         const int hc = h < a.g ? h : 0;
         sv[i] = a.scores[static_cast<uint64_t>(kvh * a.g + hc) * a.npad + (kv_e ? gk_e : 0)];
     }
-    // Pass-1 maxima: T lanes per head (a whole wave for g <= 8, half a wave
+    // Pass-1 maxima: T lanes per head (THREADS / 8 for g <= 8, THREADS / 16
     // for g <= 16); lane u reads entries u, u + T, .. of head t / T. The first
     // batch is loaded before the V tile, later batches (more than 8 T
     // workgroups in pass 1) after it.
-    const int T = a.g <= 8 ? 64 : 32;
+    const int T = a.g <= 8 ? THREADS / 8 : THREADS / 16;
     const int jh = tid / T, u = tid % T;
     const float *msrc = a.wgmax + (static_cast<uint64_t>(kvh) * a.g + (jh < a.g ? jh : 0)) * a.nwg_qk;
     constexpr int BATCH = 8;
@@ -474,12 +480,13 @@ __global__ __launch_bounds__(512, 1) void decode_pv(DecodeArgs a)
     }
 
     // 2. exact maximum per query head: a DPP reduction over the head's lanes
-    m = wave_max_hi(m, T == 64);
+    m = group_max_hi(m, T);
     if (u == T - 1 && jh < a.g) smax[jh] = m;
     __syncthreads();
 
-    // 3. dense exponentials: thread t owns key j0 + t % 256 for heads t/256,
-    //    t/256 + 2, ...; a wave covers 64 consecutive keys of one head set
+    // 3. dense exponentials: thread t owns key j0 + t % KEYS for heads
+    //    t / KEYS, t / KEYS + 2, ...; a wave covers 64 consecutive keys of one
+    //    head set
     {
 #pragma unroll
         for (int i = 0; i < kDecodeMaxGroup / 2; i++) {
@@ -555,8 +562,8 @@ __global__ __launch_bounds__(512, 1) void decode_pv(DecodeArgs a)
         }
     }
     if (tid < a.g) {
-        // heads of parity p were summed by waves 4p .. 4p+3, 64 keys each
-        const int p0 = (tid % (512 / KEYS)) * (KEYS / 64);
+        // heads of parity p were summed by waves p KEYS/64 .., 64 keys each
+        const int p0 = (tid % (THREADS / KEYS)) * (KEYS / 64);
         float L = 0.0f;
         for (int w = 0; w < KEYS / 64; w++) L += lpart[p0 + w][tid];
         a.part_l[pbase + tid] = L;
@@ -1120,7 +1127,8 @@ template <int D>
 static hipError_t decode_d(const DecodeArgs &a, int kv_heads, hipStream_t s)
 {
     hipLaunchKernelGGL(decode_qk<D>, dim3(a.nwg_qk, kv_heads), dim3(256), 0, s, a);
-    hipLaunchKernelGGL(decode_pv<D>, dim3(a.nwg_pv, kv_heads), dim3(64 * kPvWaves), 0, s, a);
+    if (a.keys_pv == 4 * kKeyTile) hipLaunchKernelGGL((decode_pv<D, 4>), dim3(a.nwg_pv, kv_heads), dim3(256), 0, s, a);
+    else hipLaunchKernelGGL((decode_pv<D, 8>), dim3(a.nwg_pv, kv_heads), dim3(512), 0, s, a);
     hipLaunchKernelGGL(decode_combine<D>, dim3(kv_heads * a.g, D / 64), dim3(64 * kCombineSubs), 0, s, a);
     return hipGetLastError();
 }
