@@ -317,7 +317,13 @@ static hsdpa_status run_attention(const hsdpa_plan *plan, const hsdpa_call *call
         a.kv_stride = s.kv_stride;
         a.q_head = s.q_head;
         a.g = static_cast<int>(s.gqa);
-        a.keys_qk = hsdpa::kDecodeKeysQK;
+        // pass 1: a tile per wave, or several in turn (the next one in flight)
+        // once one tile per wave would need more than one round of two
+        // workgroups per compute unit; this bounds the maxima pass 2 reads
+        const uint64_t nqk1 = (n + hsdpa::kDecodeKeysQK - 1) / hsdpa::kDecodeKeysQK;
+        const uint64_t slots = 2 * static_cast<uint64_t>(cus > 0 ? cus : 1);
+        const uint64_t rq = (plan->kv_heads * nqk1 + slots - 1) / slots;
+        a.keys_qk = hsdpa::kDecodeKeysQK * static_cast<int>(rq > 1 ? rq : 1);
         // pass 2 takes 8 tiles per workgroup, or 4 while the smaller
         // workgroups still fit the compute units in one round (short caches:
         // twice the workgroups, measured faster up to 16K keys at 2 KV heads)

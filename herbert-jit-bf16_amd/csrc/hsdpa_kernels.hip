@@ -258,6 +258,22 @@ __device__ __forceinline__ void tile_lstore_v16(uint16_t *tile, int tid, const u
     }
 }
 
+// tile_mask and tile_lstore_v16 chunk by chunk: each chunk is stored as soon
+// as its own load has returned, so the stores overlap the later chunks' arrival.
+template <int D, int THREADS>
+__device__ __forceinline__ void tile_mask_lstore_v16(uint16_t *tile, uint64_t t0, uint64_t lim, int tid,
+                                                     const u32x4 (&r)[Tile<D, THREADS>::kPer])
+{
+    const uint32_t nvalid = t0 < lim ? static_cast<uint32_t>(lim - t0 < kKeyTile ? lim - t0 : kKeyTile) : 0u;
+#pragma unroll
+    for (int i = 0; i < Tile<D, THREADS>::kPer; i++) {
+        const int c = tid + THREADS * i, key = c / (D / 8), dc = c % (D / 8);
+        if (c < Tile<D, THREADS>::kChunks)
+            store16(tile + key * D + 8 * swz16<D>(key, dc),
+                    static_cast<uint32_t>(key) < nvalid ? r[i] : u32x4{0, 0, 0, 0});
+    }
+}
+
 // The V^T A operand of v_mfma_f32_16x16x32_bf16 for dimensions [d0, d0+16)
 // and the 32 keys of a swizzled tile: lane (i, G) receives keys 8G..8G+7 of
 // dimension d0 + i from two transpose reads of four keys each.
@@ -317,7 +333,7 @@ __device__ __forceinline__ u32x4 vt_operand_padded(const uint16_t *vtile, int kb
 // straight from HBM would request 64 bytes of 16 rows per instruction, which
 // streams measurably slower than whole rows.
 // ---------------------------------------------------------------------------
-template <int D>
+template <int D, bool LOOP>
 __global__ __launch_bounds__(256) void decode_qk(DecodeArgs a)
 {
     constexpr int KS = D / 32;
@@ -328,7 +344,6 @@ __global__ __launch_bounds__(256) void decode_qk(DecodeArgs a)
     const int wave = threadIdx.x >> 6, l = threadIdx.x & 63, i = l & 15, G = l >> 4;
     const uint64_t j0 = static_cast<uint64_t>(wg) * a.keys_qk;
     const uint64_t j1 = j0 + a.keys_qk < a.n ? j0 + a.keys_qk : a.n;
-    const uint64_t t0 = j0 + kKeyTile * wave;
     const bool colv = i < a.g;
     // Rows past the visible keys (loaded from row 0) and columns past g are
     // computed and discarded: an MFMA output element depends only on its own
@@ -337,50 +352,75 @@ __global__ __launch_bounds__(256) void decode_qk(DecodeArgs a)
     u32x4 qb[KS];
 #pragma unroll
     for (int s = 0; s < KS; s++) qb[s] = load16(qp + 32 * s);
-    u32x4 kr[Tile<D, 64>::kPer];
-    tile_gload<D, 64>(a.k + static_cast<uint64_t>(kvh) * a.kv_stride, t0, j1, l, kr);
-    // Every load is in flight before the first use waits on one: left to
-    // itself the scheduler interleaves them and keeps only a few outstanding.
-    __builtin_amdgcn_sched_barrier(0);
+    const uint16_t *kbase = a.k + static_cast<uint64_t>(kvh) * a.kv_stride;
     uint16_t *my = kt[wave];
-#pragma unroll
-    for (int c0 = 0; c0 < Tile<D, 64>::kPer; c0++) {
-        const int c = l + 64 * c0, key = c / C, dc = c % C;
-        store16(my + key * D + 8 * (dc ^ (key & KM)), kr[c0]);
-    }
-    // The rows are this wave's own: LDS operations of one wave complete in
-    // order, so only the compiler has to be kept from reordering them.
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    u32x4 ka[2][KS];
-#pragma unroll
-    for (int b = 0; b < 2; b++)
-#pragma unroll
-        for (int s = 0; s < KS; s++) {
-            const int row = 16 * b + i;
-            ka[b][s] = load16(my + row * D + 8 * ((4 * s + G) ^ (row & KM)));
-        }
-    f32x4 acc[2] = {};
-#pragma unroll
-    for (int s = 0; s < KS; s++)
-#pragma unroll
-        for (int b = 0; b < 2; b++) acc[b] = mfma16(ka[b][s], qb[s], acc[b]);
     float m = kNegInf;
-    if (colv && t0 < j1) {
-        float *sp = a.scores + static_cast<uint64_t>(kvh * a.g + i) * a.npad + t0 + 4 * G;
+    // One 32-key tile of the wave: staged through its LDS rows, scored, stored.
+    auto tile = [&](uint64_t t0, const u32x4 (&kr)[Tile<D, 64>::kPer]) {
 #pragma unroll
-        for (int b = 0; b < 2; b++) {
-            float4 v4;
-            float *v = reinterpret_cast<float *>(&v4);
+        for (int c0 = 0; c0 < Tile<D, 64>::kPer; c0++) {
+            const int c = l + 64 * c0, key = c / C, dc = c % C;
+            store16(my + key * D + 8 * (dc ^ (key & KM)), kr[c0]);
+        }
+        // The rows are this wave's own: LDS operations of one wave complete in
+        // order, so only the compiler has to be kept from reordering them.
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        u32x4 ka[2][KS];
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const bool valid = t0 + 16 * b + 4 * G + r < j1;
-                const float s = acc[b][r] * a.scale;
-                v[r] = valid ? s : kNegInf;
-                if (valid) m = s > m ? s : m;
+        for (int b = 0; b < 2; b++)
+#pragma unroll
+            for (int s = 0; s < KS; s++) {
+                const int row = 16 * b + i;
+                ka[b][s] = load16(my + row * D + 8 * ((4 * s + G) ^ (row & KM)));
             }
-            *reinterpret_cast<float4 *>(sp + 16 * b) = v4;
+        f32x4 acc[2] = {};
+#pragma unroll
+        for (int s = 0; s < KS; s++)
+#pragma unroll
+            for (int b = 0; b < 2; b++) acc[b] = mfma16(ka[b][s], qb[s], acc[b]);
+        if (colv && t0 < j1) {
+            float *sp = a.scores + static_cast<uint64_t>(kvh * a.g + i) * a.npad + t0 + 4 * G;
+#pragma unroll
+            for (int b = 0; b < 2; b++) {
+                float4 v4;
+                float *v = reinterpret_cast<float *>(&v4);
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const bool valid = t0 + 16 * b + 4 * G + r < j1;
+                    const float s = acc[b][r] * a.scale;
+                    v[r] = valid ? s : kNegInf;
+                    if (valid) m = s > m ? s : m;
+                }
+                *reinterpret_cast<float4 *>(sp + 16 * b) = v4;
+            }
+        }
+    };
+    if constexpr (!LOOP) {
+        u32x4 kr[Tile<D, 64>::kPer];
+        tile_gload<D, 64>(kbase, j0 + kKeyTile * wave, j1, l, kr);
+        // Every load is in flight before the first use waits on one: left to
+        // itself the scheduler interleaves them and keeps only a few outstanding.
+        __builtin_amdgcn_sched_barrier(0);
+        tile(j0 + kKeyTile * wave, kr);
+    } else {
+        // keys_qk / 128 rounds of one tile per wave, the next round's tile in
+        // flight while this one is scored; the prefetch after the last round
+        // falls past j1 and reads row 0 (clamped, unused)
+        const int rounds = a.keys_qk / (4 * kKeyTile);
+        u32x4 kr0[Tile<D, 64>::kPer], kr1[Tile<D, 64>::kPer];
+        tile_gload<D, 64>(kbase, j0 + kKeyTile * wave, j1, l, kr0);
+        for (int it = 0; it < rounds; it += 2) {
+            const uint64_t t0 = j0 + 4 * kKeyTile * it + kKeyTile * wave;
+            tile_gload<D, 64>(kbase, t0 + 4 * kKeyTile, j1, l, kr1);
+            __builtin_amdgcn_sched_barrier(0);
+            tile(t0, kr0);
+            if (it + 1 < rounds) {
+                tile_gload<D, 64>(kbase, t0 + 8 * kKeyTile, j1, l, kr0);
+                __builtin_amdgcn_sched_barrier(0);
+                tile(t0 + 4 * kKeyTile, kr1);
+            }
         }
     }
     float mo = __shfl_xor(m, 16);
@@ -501,8 +541,7 @@ __global__ __launch_bounds__(64 * W, 8 / W) void decode_pv(DecodeArgs a)
         }
     }
     // 4. V tile to LDS
-    tile_mask<D, 64>(j0 + kKeyTile * wave, j1, l, vr);
-    tile_lstore_v16<D, 64>(vt[wave], l, vr);
+    tile_mask_lstore_v16<D, 64>(vt[wave], j0 + kKeyTile * wave, j1, l, vr);
     __syncthreads();
 
     // 5. P.V for this wave's dimension blocks. Columns that hold no head read
@@ -1126,7 +1165,8 @@ static bool scale_is_pow2(float s)
 template <int D>
 static hipError_t decode_d(const DecodeArgs &a, int kv_heads, hipStream_t s)
 {
-    hipLaunchKernelGGL(decode_qk<D>, dim3(a.nwg_qk, kv_heads), dim3(256), 0, s, a);
+    if (a.keys_qk > 4 * kKeyTile) hipLaunchKernelGGL((decode_qk<D, true>), dim3(a.nwg_qk, kv_heads), dim3(256), 0, s, a);
+    else hipLaunchKernelGGL((decode_qk<D, false>), dim3(a.nwg_qk, kv_heads), dim3(256), 0, s, a);
     if (a.keys_pv == 4 * kKeyTile) hipLaunchKernelGGL((decode_pv<D, 4>), dim3(a.nwg_pv, kv_heads), dim3(256), 0, s, a);
     else hipLaunchKernelGGL((decode_pv<D, 8>), dim3(a.nwg_pv, kv_heads), dim3(512), 0, s, a);
     hipLaunchKernelGGL(decode_combine<D>, dim3(kv_heads * a.g, D / 64), dim3(64 * kCombineSubs), 0, s, a);

@@ -22,6 +22,9 @@ SMALL = [
     ("prefill_d128_r70_p5", 8, 8, 128, 70, 5),
     ("prefill_d64_r33_p100_g2", 8, 4, 64, 33, 100),
     ("prefill_d256_r129_p0_g3", 6, 2, 256, 129, 0),
+    # pass 1 in several rounds per workgroup, the last workgroup partial
+    ("decode_d256_n50001_two_rounds", 16, 2, 256, 1, 50000),
+    ("decode_d128_n70001_five_rounds", 16, 4, 128, 1, 70000),
 ]
 
 
