@@ -447,14 +447,16 @@ __global__ __launch_bounds__(256) void decode_qk(DecodeArgs a)
 //     lo, so one v_mfma_f32_16x16x32_bf16 covers both halves; with g > 8 the
 //     hi and lo halves are two 16-column blocks;
 //  4. the V tiles go to LDS (swizzled for the 16-row transpose reads);
-//  5. wave w computes O^T = V^T . P^T for its dimension blocks over its
-//     share of the tiles; O = O(hi columns) + O(lo columns).
+//  5. wave w reads all its P and V^T operands from LDS, then computes
+//     O^T = V^T . P^T for its dimension blocks over its share of the tiles;
+//     O = O(hi columns) + O(lo columns).
+// NCB: P column blocks, 1 for g <= 8, 2 for g <= 16.
 // W waves (and W tiles of keys) per workgroup: W = 8 holds 131 072 + 16 896 +
 // ~2 600 bytes of LDS at D = 256, one workgroup per CU; W = 4 half of that, two
 // per CU, so that one workgroup's work after its last load overlaps another's
 // stream when the grid takes several rounds.
 // ---------------------------------------------------------------------------
-template <int D, int W>
+template <int D, int W, int NCB>
 __global__ __launch_bounds__(64 * W, 8 / W) void decode_pv(DecodeArgs a)
 {
     constexpr int THREADS = 64 * W;
@@ -470,13 +472,13 @@ __global__ __launch_bounds__(64 * W, 8 / W) void decode_pv(DecodeArgs a)
     __shared__ __attribute__((aligned(16))) uint16_t pc[2 * kDecodeMaxGroup * PS];
     __shared__ float smax[kDecodeMaxGroup];
     __shared__ float lpart[W][kDecodeMaxGroup];
-    __shared__ __attribute__((aligned(16))) float ored[PARTS > 1 ? (PARTS - 1) * WPP * 2 * DBW * 4 * 64 : 1];
+    __shared__ __attribute__((aligned(16))) float ored[PARTS > 1 ? (PARTS - 1) * WPP * NCB * DBW * 4 * 64 : 1];
     const int kvh = blockIdx.y, wg = blockIdx.x, tid = threadIdx.x;
     const int wave = tid >> 6, l = tid & 63, j = l & 15, G = l >> 4;
     const uint64_t j0 = static_cast<uint64_t>(wg) * KEYS;
     const uint64_t j1 = j0 + KEYS < a.n ? j0 + KEYS : a.n;
     const uint16_t *vbase = a.v + static_cast<uint64_t>(kvh) * a.kv_stride;
-    const int nh = a.g <= 8 ? 8 : 16;                           // lo columns start here
+    constexpr int nh = 8 * NCB;                                 // lo columns start here
     // The small loads go first: the vector-memory counter completes in order,
     // so anything issued after the V tile would wait for all of it.
     const int key_e = tid % KEYS;
@@ -493,7 +495,7 @@ __global__ __launch_bounds__(64 * W, 8 / W) void decode_pv(DecodeArgs a)
     // for g <= 16); lane u reads entries u, u + T, .. of head t / T. The first
     // batch is loaded before the V tile, later batches (more than 8 T
     // workgroups in pass 1) after it.
-    const int T = a.g <= 8 ? THREADS / 8 : THREADS / 16;
+    constexpr int T = THREADS / nh;
     const int jh = tid / T, u = tid % T;
     const float *msrc = a.wgmax + (static_cast<uint64_t>(kvh) * a.g + (jh < a.g ? jh : 0)) * a.nwg_qk;
     constexpr int BATCH = 8;
@@ -545,28 +547,32 @@ __global__ __launch_bounds__(64 * W, 8 / W) void decode_pv(DecodeArgs a)
     __syncthreads();
 
     // 5. P.V for this wave's dimension blocks. Columns that hold no head read
-    //    whatever the LDS holds; their outputs are never used.
+    //    whatever the LDS holds; their outputs are never used. Every operand
+    //    read is issued before the first MFMA: reading each just before its
+    //    MFMA waits out the LDS latency once per MFMA.
     const int dgi = wave % WPP, part = wave / WPP;
-    const int ncb = a.g <= 8 ? 1 : 2;
-    f32x4 o[2][DBW] = {};
+    u32x4 bp[TPP][NCB], av[TPP][DBW];
 #pragma unroll
     for (int tt = 0; tt < TPP; tt++) {
         const int t = part * TPP + tt;
-        const u32x4 b0 = load16(pc + j * PS + kKeyTile * t + 8 * G);
-        u32x4 b1 = b0;
-        if (ncb == 2) b1 = load16(pc + (16 + j) * PS + kKeyTile * t + 8 * G);
 #pragma unroll
-        for (int db = 0; db < DBW; db++) {
-            const u32x4 av = vt16_operand<D>(vt[t], 16 * (dgi * DBW + db), l);
-            o[0][db] = mfma16(av, b0, o[0][db]);
-            if (ncb == 2) o[1][db] = mfma16(av, b1, o[1][db]);
-        }
+        for (int c = 0; c < NCB; c++) bp[tt][c] = load16(pc + (16 * c + j) * PS + kKeyTile * t + 8 * G);
+#pragma unroll
+        for (int db = 0; db < DBW; db++) av[tt][db] = vt16_operand<D>(vt[t], 16 * (dgi * DBW + db), l);
     }
+    __builtin_amdgcn_sched_barrier(0);
+    f32x4 o[NCB][DBW] = {};
+#pragma unroll
+    for (int tt = 0; tt < TPP; tt++)
+#pragma unroll
+        for (int db = 0; db < DBW; db++)
+#pragma unroll
+            for (int c = 0; c < NCB; c++) o[c][db] = mfma16(av[tt][db], bp[tt][c], o[c][db]);
     if (PARTS > 1) {
         if (part > 0) {
-            float *dst = ored + ((part - 1) * WPP + dgi) * (2 * DBW * 4 * 64);
+            float *dst = ored + ((part - 1) * WPP + dgi) * (NCB * DBW * 4 * 64);
 #pragma unroll
-            for (int c = 0; c < 2; c++)
+            for (int c = 0; c < NCB; c++)
 #pragma unroll
                 for (int db = 0; db < DBW; db++)
 #pragma unroll
@@ -575,9 +581,9 @@ __global__ __launch_bounds__(64 * W, 8 / W) void decode_pv(DecodeArgs a)
         __syncthreads();
         if (part == 0)
             for (int p = 1; p < PARTS; p++) {
-                const float *src = ored + ((p - 1) * WPP + dgi) * (2 * DBW * 4 * 64);
+                const float *src = ored + ((p - 1) * WPP + dgi) * (NCB * DBW * 4 * 64);
 #pragma unroll
-                for (int c = 0; c < 2; c++)
+                for (int c = 0; c < NCB; c++)
 #pragma unroll
                     for (int db = 0; db < DBW; db++)
 #pragma unroll
@@ -592,10 +598,10 @@ __global__ __launch_bounds__(64 * W, 8 / W) void decode_pv(DecodeArgs a)
         f32x4 s;
 #pragma unroll
         for (int r = 0; r < 4; r++) {
-            const float lo8 = __shfl_xor(o[0][db][r], 8);
-            s[r] = ncb == 1 ? o[0][db][r] + lo8 : o[0][db][r] + o[1][db][r];
+            if constexpr (NCB == 1) s[r] = o[0][db][r] + __shfl_xor(o[0][db][r], 8);
+            else s[r] = o[0][db][r] + o[NCB - 1][db][r];
         }
-        if (part == 0 && j < (ncb == 1 ? 8 : 16) && j < a.g) {
+        if (part == 0 && j < 8 * NCB && j < a.g) {
             float *dst = a.part_o + (pbase + j) * D + 16 * (dgi * DBW + db) + 4 * G;
             *reinterpret_cast<float4 *>(dst) = float4{s[0], s[1], s[2], s[3]};
         }
@@ -1167,8 +1173,14 @@ static hipError_t decode_d(const DecodeArgs &a, int kv_heads, hipStream_t s)
 {
     if (a.keys_qk > 4 * kKeyTile) hipLaunchKernelGGL((decode_qk<D, true>), dim3(a.nwg_qk, kv_heads), dim3(256), 0, s, a);
     else hipLaunchKernelGGL((decode_qk<D, false>), dim3(a.nwg_qk, kv_heads), dim3(256), 0, s, a);
-    if (a.keys_pv == 4 * kKeyTile) hipLaunchKernelGGL((decode_pv<D, 4>), dim3(a.nwg_pv, kv_heads), dim3(256), 0, s, a);
-    else hipLaunchKernelGGL((decode_pv<D, 8>), dim3(a.nwg_pv, kv_heads), dim3(512), 0, s, a);
+    const dim3 gpv(a.nwg_pv, kv_heads);
+    if (a.g <= 8) {
+        if (a.keys_pv == 4 * kKeyTile) hipLaunchKernelGGL((decode_pv<D, 4, 1>), gpv, dim3(256), 0, s, a);
+        else hipLaunchKernelGGL((decode_pv<D, 8, 1>), gpv, dim3(512), 0, s, a);
+    } else {
+        if (a.keys_pv == 4 * kKeyTile) hipLaunchKernelGGL((decode_pv<D, 4, 2>), gpv, dim3(256), 0, s, a);
+        else hipLaunchKernelGGL((decode_pv<D, 8, 2>), gpv, dim3(512), 0, s, a);
+    }
     hipLaunchKernelGGL(decode_combine<D>, dim3(kv_heads * a.g, D / 64), dim3(64 * kCombineSubs), 0, s, a);
     return hipGetLastError();
 }
