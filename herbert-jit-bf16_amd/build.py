@@ -12,12 +12,16 @@ import os
 import shutil
 import subprocess
 import sys
+import tempfile
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 SRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "hsdpa", "libhsdpa.so")
-SOURCES = ["hsdpa_kernels.hip", "hsdpa_api.cpp"]
+# translation units, compiled in parallel and linked: the tuned attention
+# kernels and the element kernels, the attention kernels of the other head
+# dimensions, the C ABI
+SOURCES = ["hsdpa_kernels.hip", "hsdpa_attn_more.hip", "hsdpa_api.cpp"]
 HIPCC = os.environ.get("HIPCC", shutil.which("hipcc") or "/opt/rocm/bin/hipcc")
 
 # -ffp-contract=off: the exponential and the score scaling must round exactly
@@ -27,24 +31,48 @@ FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=o
          "-Wall", "-Wno-unused-function", "-I", os.path.join(ROOT, "include"), "-I", SRC]
 
 
+def _errors(stderr: str) -> str:
+    # hipcc's host pass warns that it does not know the packed-fp32 feature
+    return "\n".join(line for line in stderr.splitlines()
+                     if "unknown target feature" not in line and "-packed-fp32-ops" not in line)
+
+
 def build(asm: bool = False, verbose: bool = False) -> str:
     tmp = OUT + ".tmp"
-    cmd = [HIPCC] + FLAGS + ["-shared", "-o", tmp] + [os.path.join(SRC, s) for s in SOURCES]
-    if verbose:
-        print(" ".join(cmd), flush=True)
-    r = subprocess.run(cmd, capture_output=True, text=True)
-    noise = "unknown target feature"
-    err = "\n".join(line for line in r.stderr.splitlines() if noise not in line and "-packed-fp32-ops" not in line)
-    if r.returncode != 0:
-        raise RuntimeError(f"hipcc failed ({r.returncode}):\n{err}")
-    if err.strip() and verbose:
-        print(err, file=sys.stderr)
+    with tempfile.TemporaryDirectory(prefix="hsdpa_build_") as objdir:
+        objs, procs = [], []
+        for src in SOURCES:
+            obj = os.path.join(objdir, os.path.splitext(src)[0] + ".o")
+            cmd = [HIPCC] + FLAGS + ["-c", "-o", obj, os.path.join(SRC, src)]
+            if verbose:
+                print(" ".join(cmd), flush=True)
+            objs.append(obj)
+            procs.append(subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True))
+        failed = []
+        for src, p in zip(SOURCES, procs):
+            _, stderr = p.communicate()
+            err = _errors(stderr)
+            if p.returncode != 0:
+                failed.append(f"{src} ({p.returncode}):\n{err}")
+            elif err.strip() and verbose:
+                print(err, file=sys.stderr)
+        if failed:
+            raise RuntimeError("hipcc failed: " + "\n".join(failed))
+        cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp] + objs
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        r = subprocess.run(cmd, capture_output=True, text=True)
+        if r.returncode != 0:
+            raise RuntimeError(f"hipcc link failed ({r.returncode}):\n{_errors(r.stderr)}")
     os.replace(tmp, OUT)
     if asm:
         d = os.path.join(HERE, "_asm")
         os.makedirs(d, exist_ok=True)
-        subprocess.run([HIPCC] + FLAGS + ["--cuda-device-only", "-S", "-o", os.path.join(d, "hsdpa_kernels.s"),
-                                          os.path.join(SRC, "hsdpa_kernels.hip")], check=True)
+        for src in SOURCES:
+            if src.endswith(".hip"):
+                out = os.path.join(d, os.path.splitext(src)[0] + ".s")
+                subprocess.run([HIPCC] + FLAGS + ["--cuda-device-only", "-S", "-o", out, os.path.join(SRC, src)],
+                               check=True)
     return OUT
 
 

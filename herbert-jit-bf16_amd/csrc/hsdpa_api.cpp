@@ -322,13 +322,15 @@ static hsdpa_status run_attention(const hsdpa_plan *plan, const hsdpa_call *call
         // workgroups per compute unit; this bounds the maxima pass 2 reads
         const uint64_t nqk1 = (n + hsdpa::kDecodeKeysQK - 1) / hsdpa::kDecodeKeysQK;
         const uint64_t slots = 2 * static_cast<uint64_t>(cus > 0 ? cus : 1);
-        const uint64_t rq = (plan->kv_heads * nqk1 + slots - 1) / slots;
+        const uint64_t rq = hsdpa::decode_loop_ok(d) ? (plan->kv_heads * nqk1 + slots - 1) / slots : 1;
         a.keys_qk = hsdpa::kDecodeKeysQK * static_cast<int>(rq > 1 ? rq : 1);
         // pass 2 takes 8 tiles per workgroup, or 4 while the smaller
         // workgroups still fit the compute units in one round (short caches:
         // twice the workgroups, measured faster up to 16K keys at 2 KV heads)
         const uint64_t nwg4 = (n + 4 * hsdpa::kKeyTile - 1) / (4 * hsdpa::kKeyTile);
-        a.keys_pv = plan->kv_heads * nwg4 <= static_cast<uint64_t>(cus) ? 4 * hsdpa::kKeyTile : hsdpa::kDecodeKeysPV;
+        a.keys_pv = plan->kv_heads * nwg4 <= static_cast<uint64_t>(cus) || !hsdpa::decode_wide_ok(d)
+                        ? 4 * hsdpa::kKeyTile
+                        : hsdpa::kDecodeKeysPV;
         a.nwg_qk = static_cast<int>((n + a.keys_qk - 1) / a.keys_qk);
         a.nwg_pv = static_cast<int>((n + a.keys_pv - 1) / a.keys_pv);
         a.scale = call->scale;
@@ -447,7 +449,7 @@ const char *hsdpa_status_string(hsdpa_status status)
     switch (status) {
     case HSDPA_OK: return "ok";
     case HSDPA_ERR_EMPTY: return "empty shape (heads, gqa or head_dim is 0)";
-    case HSDPA_ERR_HEAD_DIM: return "head_dim out of domain (multiple of 32; 64, 128 or 256 on gfx950)";
+    case HSDPA_ERR_HEAD_DIM: return "head_dim out of domain (a multiple of 32 from 32 to 512)";
     case HSDPA_ERR_GQA: return "heads is not a multiple of gqa";
     case HSDPA_ERR_STRIDE: return "invalid q/out/kv strides for this geometry";
     case HSDPA_ERR_SINK_UNSUPPORTED: return "softmax sink is not supported";

@@ -1,0 +1,81 @@
+// hsdpa_attn_more.hip — the attention kernels for the head dimensions other
+// than 64, 128 and 256: every multiple of 32 from 32 to 512, the range the
+// reference's SdpaShape::check accepts (src/jit/ir.rs:130-162). Same templates
+// and numerics as hsdpa_kernels.hip, in a translation unit of their own so that
+// the tuned instantiations there are compiled exactly as before.
+//
+// Configurations: the causal kernel serves one query head per workgroup
+// (HPW = 1, valid for every group size) and always scales the scores first
+// (the general path; with a power-of-two scale it rounds identically to the
+// folded one). Up to D = 256 it runs 8 waves, two per SIMD; above, the O and
+// Q registers of a 32-row wave (D/2 + D/4) exceed the 256 of two waves per
+// SIMD, so it runs 4 waves, one per SIMD. The decode passes take the
+// configurations decode_loop_ok / decode_wide_ok allow.
+
+#include "hsdpa_attn_kernels.h"
+
+namespace hsdpa {
+
+template <int D>
+static hipError_t decode_more_d(const DecodeArgs &a, int kv_heads, hipStream_t s)
+{
+    const dim3 gqk(a.nwg_qk, kv_heads), gpv(a.nwg_pv, kv_heads);
+    if constexpr (D <= 256) {
+        if (a.keys_qk > 4 * kKeyTile) hipLaunchKernelGGL((decode_qk<D, true>), gqk, dim3(256), 0, s, a);
+        else hipLaunchKernelGGL((decode_qk<D, false>), gqk, dim3(256), 0, s, a);
+    } else {
+        if (a.keys_qk != 4 * kKeyTile) return hipErrorInvalidValue;
+        hipLaunchKernelGGL((decode_qk<D, false>), gqk, dim3(256), 0, s, a);
+    }
+    constexpr bool WIDE = D <= 256 && (D / 16 >= 8 || 8 % (D / 16) == 0);   // decode_wide_ok
+    if (a.keys_pv == 4 * kKeyTile) {
+        if (a.g <= 8) hipLaunchKernelGGL((decode_pv<D, 4, 1>), gpv, dim3(256), 0, s, a);
+        else hipLaunchKernelGGL((decode_pv<D, 4, 2>), gpv, dim3(256), 0, s, a);
+    } else {
+        if constexpr (WIDE) {
+            if (a.g <= 8) hipLaunchKernelGGL((decode_pv<D, 8, 1>), gpv, dim3(512), 0, s, a);
+            else hipLaunchKernelGGL((decode_pv<D, 8, 2>), gpv, dim3(512), 0, s, a);
+        } else {
+            return hipErrorInvalidValue;
+        }
+    }
+    hipLaunchKernelGGL(decode_combine<D>, dim3(kv_heads * a.g, (D + 63) / 64), dim3(64 * kCombineSubs), 0, s, a);
+    return hipGetLastError();
+}
+
+template <int D>
+static hipError_t prefill_more_d(const PrefillArgs &a, int heads, hipStream_t s)
+{
+    constexpr int NW = D > 256 ? 4 : 8;
+    constexpr int ROWS = 32 * NW;                                // HPW = 1: NW row blocks of one head
+    const dim3 grid(static_cast<unsigned>((a.rows + ROWS - 1) / ROWS), heads);
+    hipLaunchKernelGGL((prefill_attn<D, 1, false, NW>), grid, dim3(64 * NW), 0, s, a);
+    return hipGetLastError();
+}
+
+#define HSDPA_MORE_DIMS(X) \
+    X(32) X(96) X(160) X(192) X(224) X(288) X(320) X(352) X(384) X(416) X(448) X(480) X(512)
+
+hipError_t launch_decode_more(const DecodeArgs &a, int head_dim, int kv_heads, hipStream_t s)
+{
+    switch (head_dim) {
+#define HSDPA_CASE(D) \
+    case D: return decode_more_d<D>(a, kv_heads, s);
+        HSDPA_MORE_DIMS(HSDPA_CASE)
+#undef HSDPA_CASE
+    default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_prefill_more(const PrefillArgs &a, int head_dim, int heads, hipStream_t s)
+{
+    switch (head_dim) {
+#define HSDPA_CASE(D) \
+    case D: return prefill_more_d<D>(a, heads, s);
+        HSDPA_MORE_DIMS(HSDPA_CASE)
+#undef HSDPA_CASE
+    default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace hsdpa

@@ -85,12 +85,24 @@ struct LayerPrepArgs {
     float eps;
 };
 
+// Head dimensions the kernels take: multiples of 32 from 32 to 512 (the
+// reference's SdpaShape::check, ir.rs:130-162).
 bool head_dim_supported(int d);
+
+// Decode configurations a head dimension allows. Pass 1 loops over several key
+// tiles per wave up to D = 256 (above, one tile's registers are the budget);
+// pass 2 takes 8 waves (256 keys) only where their V tiles fit the LDS (D <=
+// 256) and the waves split the D/16 dimension blocks evenly or take whole ones.
+inline bool decode_loop_ok(int d) { return d <= 256; }
+inline bool decode_wide_ok(int d) { return d <= 256 && (d / 16 >= 8 || 8 % (d / 16) == 0); }
 hipError_t launch_layer_prep(const LayerPrepArgs &a, hipStream_t s);
 hipError_t launch_norm_rope(const NormRopeArgs &a, hipStream_t s);
 hipError_t launch_gate(const GateArgs &a, hipStream_t s);
 hipError_t launch_kv_append(const KvAppendArgs &a, bool vec, hipStream_t s);
 hipError_t launch_decode(const DecodeArgs &a, int head_dim, int kv_heads, hipStream_t s);
 hipError_t launch_prefill(const PrefillArgs &a, int head_dim, int heads, hipStream_t s);
+// the head dimensions other than 64, 128 and 256 (hsdpa_attn_more.hip)
+hipError_t launch_decode_more(const DecodeArgs &a, int head_dim, int kv_heads, hipStream_t s);
+hipError_t launch_prefill_more(const PrefillArgs &a, int head_dim, int heads, hipStream_t s);
 
 }  // namespace hsdpa

@@ -1,891 +1,10 @@
-// hsdpa_kernels.hip — gfx950 kernels of the attention step.
-//
-// Numerical contract (the reference's emitted SDPA, x86 AVX-512 BF16):
-//   s_j   = fl(dot(q, K_j) * scale)           bf16 products, f32 sums
-//   M     = max_j s_j over the visible keys   (the EXACT row maximum)
-//   e_j   = P(fl(s_j - M))                    the reference's degree-4 exp
-//   out   = bf16_rne(sum_j e_j V_j / sum_j e_j)
-// (src/jit/target/x86/emit_sdpa/x86/decode.rs:212-293 for the softmax,
-//  base.rs:189-212 for P, decode.rs:348-428 for the SV pass.)
-//
-// Two choices follow from matching that contract to within one bf16 ulp:
-//  * P is evaluated at the exact row maximum, so the softmax is two-pass
-//    (maximum, then exponentials): an online softmax rescaled by P(m_old -
-//    m_new) mixes the polynomial's error across blocks and drifts by more
-//    than the tolerance allows.
-//  * P.V runs on bf16 MFMA with P carried as hi + lo bf16 halves
-//    (e = hi + lo exactly to 16 significant bits), two MFMAs per block.
-//
-// MFMA layout (v_mfma_f32_32x32x16_bf16): lane l, c = l % 32, g = l / 32.
-// A[i][k]: lane (i, g) holds k = 8g..8g+7; B[k][j]: lane (j, g) holds the same
-// k slots; D[i][j]: lane (j, g) register r holds row i = 8(r/4) + 4g + r%4.
-// Scores are computed transposed (S^T = K . Q^T): the key is the MFMA row and
-// the query the column, so each lane owns one query and its P^T values feed
-// the P.V MFMA (O^T = V^T . P^T) with no data movement. The A-operand rows
-// are loaded as K row swap23(i) (bits 2 and 3 of the row swapped), which
-// makes score register r of lane group g hold key 16(r/8) + 8g + r%8: eight
-// consecutive keys per P.V k-block.
-//
-// V stays row-major in LDS; its V^T operands come from the gfx950 transpose
-// read ds_read_b64_tr_b16. In each 16-lane group, lane j supplies the address
-// of four consecutive b16 and lane i receives element i%4 of the chunks of
-// lanes i/4 + 4k, k = 0..3. Pointing lane j at V[base + j/4][d0 + 4(j%4)]
-// hands lane i the four keys base..base+3 of dimension d0 + i.
+// hsdpa_kernels.hip — gfx950 kernels of the attention step: the attention
+// kernels for head dimensions 64, 128 and 256 (templates in
+// hsdpa_attn_kernels.h), the element kernels around them, and the launchers.
 
-#include "hsdpa_kernels.h"
-
-#include <type_traits>
+#include "hsdpa_attn_kernels.h"
 
 namespace hsdpa {
-
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef float f32x16 __attribute__((ext_vector_type(16)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-
-static constexpr float kNegInf = -__builtin_huge_valf();
-
-__device__ __forceinline__ f32x16 mfma(u32x4 a, u32x4 b, f32x16 c)
-{
-    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
-                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
-}
-
-// v_mfma_f32_16x16x32_bf16, lane l, i = l % 16, G = l / 16: A[i][k] and
-// B[k][i] for k = 8G..8G+7; D[4G + r][i] in register r.
-__device__ __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c)
-{
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
-                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
-}
-
-__device__ __forceinline__ u32x4 load16(const uint16_t *p) { return *reinterpret_cast<const u32x4 *>(p); }
-__device__ __forceinline__ void store16(uint16_t *p, u32x4 v) { *reinterpret_cast<u32x4 *>(p) = v; }
-
-// The emitted exponential (base.rs:189-212, constants exp_constants.rs:14-23):
-// clamp at -87.33654, t = x*log2(e), k = rne(t), f = t - k, Horner with FMA,
-// times 2^k built from the exponent bits. This file is compiled with
-// -ffp-contract=off so that only the written fmaf calls fuse.
-__device__ __forceinline__ float exp_poly(float x)
-{
-    float io = x > -87.33654f ? x : -87.33654f;
-    float t1 = io * 1.442695f;
-    float t2 = __builtin_rintf(t1);
-    t1 = t1 - t2;
-    float t3 = __builtin_fmaf(t1, 0.00967248f, 0.05550411f);
-    t3 = __builtin_fmaf(t1, t3, 0.2402265f);
-    t3 = __builtin_fmaf(t1, t3, 0.6931472f);
-    t3 = __builtin_fmaf(t1, t3, 1.0f);
-    const uint32_t sc = (static_cast<uint32_t>(static_cast<int32_t>(t2)) << 23) + 0x3F800000u;
-    return t3 * __uint_as_float(sc);
-}
-
-// Round a finite f32 to bf16 bits, nearest even.
-__device__ __forceinline__ uint32_t bf16_rne(float x)
-{
-    const uint32_t b = __float_as_uint(x);
-    return (b + 0x7FFFu + ((b >> 16) & 1u)) >> 16;
-}
-
-// The output conversion of the reference epilogue, vcvtneps2bf16: zeros and
-// denormals to signed zero, NaN quieted, otherwise nearest even.
-__device__ __forceinline__ uint32_t cvt_out(float x)
-{
-    const uint32_t b = __float_as_uint(x);
-    const uint32_t e = b & 0x7F800000u;
-    const uint32_t rne = (b + 0x7FFFu + ((b >> 16) & 1u)) >> 16;
-    const uint32_t special = (b & 0x7FFFFFu) ? ((b >> 16) | 0x40u) : (b >> 16);
-    const uint32_t r = e == 0x7F800000u ? special : rne;
-    return e == 0 ? ((b >> 16) & 0x8000u) : r;
-}
-
-// The output gate of one element (ElemOp::SigmoidMul, emit_elem.rs:350-440):
-// e = 0 - g; e = e < 88 ? e : 88 (vminps: the bound when e is NaN); the
-// softmax's exponential; bf16(a / (e + 1)), a the bf16 attention output.
-__device__ __forceinline__ uint16_t gate_bf16(uint16_t a, uint16_t g)
-{
-    float e = 0.0f - __uint_as_float(static_cast<uint32_t>(g) << 16);
-    e = e < 88.0f ? e : 88.0f;
-    e = exp_poly(e);
-    e = e + 1.0f;
-    return static_cast<uint16_t>(cvt_out(__uint_as_float(static_cast<uint32_t>(a) << 16) / e));
-}
-
-// Split eight exponentials into hi and lo bf16 halves, packed in k order.
-__device__ __forceinline__ void split_pack(const float *e, u32x4 &hi, u32x4 &lo)
-{
-#pragma unroll
-    for (int s = 0; s < 4; s++) {
-        const uint32_t h0 = bf16_rne(e[2 * s]), h1 = bf16_rne(e[2 * s + 1]);
-        const float r0 = e[2 * s] - __uint_as_float(h0 << 16);
-        const float r1 = e[2 * s + 1] - __uint_as_float(h1 << 16);
-        hi[s] = h0 | (h1 << 16);
-        lo[s] = bf16_rne(r0) | (bf16_rne(r1) << 16);
-    }
-}
-
-__device__ __forceinline__ int swap23(int i) { return (i & ~12) | ((i & 4) << 1) | ((i & 8) >> 1); }
-
-// Wave reductions on the DPP paths (no LDS round trips). Within each row of
-// 16 lanes: swap neighbours, swap pairs, half-row mirror, row mirror; every
-// lane of a row then holds the row's result. Across rows, row_bcast:15 folds
-// row 0 into row 1 and row 2 into row 3, row_bcast:31 folds lane 31 into rows
-// 2 and 3: lane 31 holds the result of lanes 0..31, lane 63 of all 64.
-template <int CTRL, int ROWS>
-__device__ __forceinline__ float dpp(float x, float old)
-{
-    return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(old), __float_as_int(x), CTRL, ROWS, 0xF, false));
-}
-
-__device__ __forceinline__ float row_sum16(float x)
-{
-    x += dpp<0xB1, 0xF>(x, 0.0f);    // quad_perm [1,0,3,2]
-    x += dpp<0x4E, 0xF>(x, 0.0f);    // quad_perm [2,3,0,1]
-    x += dpp<0x141, 0xF>(x, 0.0f);   // row_half_mirror
-    x += dpp<0x140, 0xF>(x, 0.0f);   // row_mirror
-    return x;
-}
-
-// Sum over the 64 lanes, valid in lane 63.
-__device__ __forceinline__ float wave_sum_hi(float x)
-{
-    x = row_sum16(x);
-    x += dpp<0x142, 0xA>(x, 0.0f);   // row_bcast:15 into rows 1 and 3
-    x += dpp<0x143, 0xC>(x, 0.0f);   // row_bcast:31 into rows 2 and 3
-    return x;
-}
-
-__device__ __forceinline__ float fmaxnn(float a, float b) { return b > a ? b : a; }
-
-// Maximum over each half wave (lanes 0..31 in lane 31, 32..63 in lane 63) and
-// over the whole wave (in lane 63) when `whole`. -inf is the identity; NaN
-// inputs are ignored like in the scalar reductions.
-// The maximum over groups of `lanes` (16, 32 or 64) consecutive lanes: after
-// the row steps every lane of a row holds the row's maximum; row_bcast:15
-// leaves a 32-lane group's in its lane 31, row_bcast:31 the wave's in lane 63.
-__device__ __forceinline__ float group_max_hi(float x, int lanes)
-{
-    x = fmaxnn(x, dpp<0xB1, 0xF>(x, kNegInf));
-    x = fmaxnn(x, dpp<0x4E, 0xF>(x, kNegInf));
-    x = fmaxnn(x, dpp<0x141, 0xF>(x, kNegInf));
-    x = fmaxnn(x, dpp<0x140, 0xF>(x, kNegInf));
-    if (lanes >= 32) x = fmaxnn(x, dpp<0x142, 0xA>(x, kNegInf));
-    if (lanes >= 64) x = fmaxnn(x, dpp<0x143, 0xC>(x, kNegInf));
-    return x;
-}
-
-__device__ __forceinline__ float lane_value(float x, int lane)
-{
-    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), lane));
-}
-
-// Key offset inside a 32-key tile of score register r for lane group g.
-__device__ __forceinline__ int key_of(int r, int g) { return 16 * (r >> 3) + 8 * g + (r & 7); }
-
-typedef short v4i16 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-
-__device__ __forceinline__ u32x2 tr_read(const uint16_t *p)
-{
-    const v4i16 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4i16 *)(p));
-    return __builtin_bit_cast(u32x2, r);
-}
-
-
-
-// A 32-key tile of K or V is 32 * D/8 chunks of 16 bytes. Lanes (or threads)
-// take consecutive chunks so every load instruction reads whole rows.
-template <int D, int THREADS> struct Tile {
-    static constexpr int kChunks = kKeyTile * (D / 8);
-    static constexpr int kPer = (kChunks + THREADS - 1) / THREADS;
-};
-
-// Loads are unconditional from a clamped in-bounds address (row 0 of the head
-// when the chunk is out of range): a conditional load becomes control flow
-// that waits on each load before issuing the next. tile_mask zeroes the
-// out-of-range chunks afterwards; it waits on the loads, so it goes where the
-// data is consumed, not next to the loads.
-template <int D, int THREADS>
-__device__ __forceinline__ void tile_gload(const uint16_t *base, uint64_t t0, uint64_t lim, int tid,
-                                           u32x4 (&r)[Tile<D, THREADS>::kPer])
-{
-    // t0 and lim are uniform: the tile base stays in scalar registers and each
-    // lane adds a 32-bit offset. A tile starting at or past lim reads row 0.
-    const bool any = t0 < lim;
-    const uint16_t *tb = base + (any ? t0 : 0) * D;
-    const uint32_t nvalid = any ? static_cast<uint32_t>(lim - t0 < kKeyTile ? lim - t0 : kKeyTile) : 0u;
-#pragma unroll
-    for (int i = 0; i < Tile<D, THREADS>::kPer; i++) {
-        const int c = tid + THREADS * i, key = c / (D / 8), dc = c % (D / 8);
-        const bool ok = c < Tile<D, THREADS>::kChunks && static_cast<uint32_t>(key) < nvalid;
-        const uint32_t off = ok ? static_cast<uint32_t>(key * D + 8 * dc) : 0u;
-        r[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(tb + off));
-    }
-}
-
-template <int D, int THREADS>
-__device__ __forceinline__ void tile_mask(uint64_t t0, uint64_t lim, int tid, u32x4 (&r)[Tile<D, THREADS>::kPer])
-{
-    const uint32_t nvalid = t0 < lim ? static_cast<uint32_t>(lim - t0 < kKeyTile ? lim - t0 : kKeyTile) : 0u;
-#pragma unroll
-    for (int i = 0; i < Tile<D, THREADS>::kPer; i++) {
-        const int c = tid + THREADS * i;
-        const bool ok = c < Tile<D, THREADS>::kChunks && static_cast<uint32_t>(c / (D / 8)) < nvalid;
-        r[i] = ok ? r[i] : u32x4{0, 0, 0, 0};
-    }
-}
-
-// Decode V tiles are [32 keys][D] bf16 without padding. The V^T operand of
-// v_mfma_f32_16x16x32_bf16 is two transpose reads; half a wave of one read
-// covers rows {k, k+1, k+2, k+3, k+8, .., k+11} (k a multiple of 16) at the
-// same 32 bytes of dimensions. XOR-ing the 32-byte slot index of each row
-// with f(key) = key % 4 + 4 ((key / 8) % 2) puts those eight rows on eight
-// distinct 32-byte bank slots.
-template <int D> __device__ __forceinline__ int swz16(int key, int chunk)
-{
-    constexpr int C = D / 8;                     // 16-byte chunks per row
-    const int f = (key & 3) | (((key >> 3) & 1) << 2);
-    return chunk ^ ((2 * f) & (C - 1));
-}
-
-template <int D, int THREADS>
-__device__ __forceinline__ void tile_lstore_v16(uint16_t *tile, int tid, const u32x4 (&r)[Tile<D, THREADS>::kPer])
-{
-#pragma unroll
-    for (int i = 0; i < Tile<D, THREADS>::kPer; i++) {
-        const int c = tid + THREADS * i, key = c / (D / 8), dc = c % (D / 8);
-        if (c < Tile<D, THREADS>::kChunks) store16(tile + key * D + 8 * swz16<D>(key, dc), r[i]);
-    }
-}
-
-// tile_mask and tile_lstore_v16 chunk by chunk: each chunk is stored as soon
-// as its own load has returned, so the stores overlap the later chunks' arrival.
-template <int D, int THREADS>
-__device__ __forceinline__ void tile_mask_lstore_v16(uint16_t *tile, uint64_t t0, uint64_t lim, int tid,
-                                                     const u32x4 (&r)[Tile<D, THREADS>::kPer])
-{
-    const uint32_t nvalid = t0 < lim ? static_cast<uint32_t>(lim - t0 < kKeyTile ? lim - t0 : kKeyTile) : 0u;
-#pragma unroll
-    for (int i = 0; i < Tile<D, THREADS>::kPer; i++) {
-        const int c = tid + THREADS * i, key = c / (D / 8), dc = c % (D / 8);
-        if (c < Tile<D, THREADS>::kChunks)
-            store16(tile + key * D + 8 * swz16<D>(key, dc),
-                    static_cast<uint32_t>(key) < nvalid ? r[i] : u32x4{0, 0, 0, 0});
-    }
-}
-
-// The V^T A operand of v_mfma_f32_16x16x32_bf16 for dimensions [d0, d0+16)
-// and the 32 keys of a swizzled tile: lane (i, G) receives keys 8G..8G+7 of
-// dimension d0 + i from two transpose reads of four keys each.
-template <int D>
-__device__ __forceinline__ u32x4 vt16_operand(const uint16_t *vtile, int d0, int l)
-{
-    const int j = l & 15, G = l >> 4;
-    const int key = 8 * G + (j >> 2);
-    const int dim = d0 + 4 * (j & 3);
-    const u32x2 a = tr_read(vtile + key * D + 8 * swz16<D>(key, dim >> 3) + (dim & 7));
-    const u32x2 b = tr_read(vtile + (key + 4) * D + 8 * swz16<D>(key + 4, dim >> 3) + (dim & 7));
-    return u32x4{a.x, a.y, b.x, b.y};
-}
-
-// Padded tiles: row stride D + 8 for K (a read of 32 rows at one 16-byte
-// chunk walks all 16 chunk slots of the banks) and D + 32 for V (the 4 rows
-// of a transpose read land in the 4 quarters of the banks). Addresses stay
-// affine, so per-access offsets fold into immediates.
-template <int D> struct Pad {
-    static constexpr int K = D + 8;
-    static constexpr int V = D + 32;
-};
-
-template <int D, int THREADS>
-__device__ __forceinline__ void tile_lstore_padded(uint16_t *tile, int stride, int tid,
-                                                   const u32x4 (&r)[Tile<D, THREADS>::kPer])
-{
-#pragma unroll
-    for (int i = 0; i < Tile<D, THREADS>::kPer; i++) {
-        const int c = tid + THREADS * i, key = c / (D / 8), dc = c % (D / 8);
-        if (c < Tile<D, THREADS>::kChunks) store16(tile + key * stride + 8 * dc, r[i]);
-    }
-}
-
-// V^T operand from a padded V tile (row stride Pad<D>::V).
-template <int D>
-__device__ __forceinline__ u32x4 vt_operand_padded(const uint16_t *vtile, int kb, int d0, int l)
-{
-    constexpr int S = Pad<D>::V;
-    const int j = l & 15, G = l >> 4;
-    const int key = kb + 8 * (G >> 1) + (j >> 2);
-    const int dim = d0 + 16 * (G & 1) + 4 * (j & 3);
-    const u32x2 a = tr_read(vtile + key * S + dim);
-    const u32x2 b = tr_read(vtile + (key + 4) * S + dim);
-    return u32x4{a.x, a.y, b.x, b.y};
-}
-
-// ---------------------------------------------------------------------------
-// Decode pass 1: scores and per-workgroup maxima.
-// grid (nwg_qk, kv_heads), 256 threads, keys_qk = 128: wave w computes the
-// 32 keys j0 + 32w .. +32 as two 16-key blocks of v_mfma_f32_16x16x32_bf16
-// (S^T = K . Q^T, the g <= 16 query heads of the KV head as the columns).
-// The wave loads its 32 K rows whole (each load instruction reads 1 KB of
-// contiguous cache), stages them through its own LDS rows with the 16-byte
-// chunks XOR-swizzled by key % 16, and reads the A operands from there:
-// lane (i, G) takes row i, dimensions 32s + 8G .. +8. Loading the operands
-// straight from HBM would request 64 bytes of 16 rows per instruction, which
-// streams measurably slower than whole rows.
-// ---------------------------------------------------------------------------
-template <int D, bool LOOP>
-__global__ __launch_bounds__(256) void decode_qk(DecodeArgs a)
-{
-    constexpr int KS = D / 32;
-    constexpr int C = D / 8, KM = (C < 16 ? C : 16) - 1;        // chunks per row, swizzle mask
-    __shared__ __attribute__((aligned(16))) uint16_t kt[4][kKeyTile * D];
-    __shared__ float red[4][16];
-    const int kvh = blockIdx.y, wg = blockIdx.x;
-    const int wave = threadIdx.x >> 6, l = threadIdx.x & 63, i = l & 15, G = l >> 4;
-    const uint64_t j0 = static_cast<uint64_t>(wg) * a.keys_qk;
-    const uint64_t j1 = j0 + a.keys_qk < a.n ? j0 + a.keys_qk : a.n;
-    const bool colv = i < a.g;
-    // Rows past the visible keys (loaded from row 0) and columns past g are
-    // computed and discarded: an MFMA output element depends only on its own
-    // A row and B column.
-    const uint16_t *qp = a.q + static_cast<uint64_t>(kvh * a.g + (colv ? i : 0)) * a.q_head + 8 * G;
-    u32x4 qb[KS];
-#pragma unroll
-    for (int s = 0; s < KS; s++) qb[s] = load16(qp + 32 * s);
-    const uint16_t *kbase = a.k + static_cast<uint64_t>(kvh) * a.kv_stride;
-    uint16_t *my = kt[wave];
-    float m = kNegInf;
-    // One 32-key tile of the wave: staged through its LDS rows, scored, stored.
-    auto tile = [&](uint64_t t0, const u32x4 (&kr)[Tile<D, 64>::kPer]) {
-#pragma unroll
-        for (int c0 = 0; c0 < Tile<D, 64>::kPer; c0++) {
-            const int c = l + 64 * c0, key = c / C, dc = c % C;
-            store16(my + key * D + 8 * (dc ^ (key & KM)), kr[c0]);
-        }
-        // The rows are this wave's own: LDS operations of one wave complete in
-        // order, so only the compiler has to be kept from reordering them.
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        u32x4 ka[2][KS];
-#pragma unroll
-        for (int b = 0; b < 2; b++)
-#pragma unroll
-            for (int s = 0; s < KS; s++) {
-                const int row = 16 * b + i;
-                ka[b][s] = load16(my + row * D + 8 * ((4 * s + G) ^ (row & KM)));
-            }
-        f32x4 acc[2] = {};
-#pragma unroll
-        for (int s = 0; s < KS; s++)
-#pragma unroll
-            for (int b = 0; b < 2; b++) acc[b] = mfma16(ka[b][s], qb[s], acc[b]);
-        if (colv && t0 < j1) {
-            float *sp = a.scores + static_cast<uint64_t>(kvh * a.g + i) * a.npad + t0 + 4 * G;
-#pragma unroll
-            for (int b = 0; b < 2; b++) {
-                float4 v4;
-                float *v = reinterpret_cast<float *>(&v4);
-#pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    const bool valid = t0 + 16 * b + 4 * G + r < j1;
-                    const float s = acc[b][r] * a.scale;
-                    v[r] = valid ? s : kNegInf;
-                    if (valid) m = s > m ? s : m;
-                }
-                *reinterpret_cast<float4 *>(sp + 16 * b) = v4;
-            }
-        }
-    };
-    if constexpr (!LOOP) {
-        u32x4 kr[Tile<D, 64>::kPer];
-        tile_gload<D, 64>(kbase, j0 + kKeyTile * wave, j1, l, kr);
-        // Every load is in flight before the first use waits on one: left to
-        // itself the scheduler interleaves them and keeps only a few outstanding.
-        __builtin_amdgcn_sched_barrier(0);
-        tile(j0 + kKeyTile * wave, kr);
-    } else {
-        // keys_qk / 128 rounds of one tile per wave, the next round's tile in
-        // flight while this one is scored; the prefetch after the last round
-        // falls past j1 and reads row 0 (clamped, unused)
-        const int rounds = a.keys_qk / (4 * kKeyTile);
-        u32x4 kr0[Tile<D, 64>::kPer], kr1[Tile<D, 64>::kPer];
-        tile_gload<D, 64>(kbase, j0 + kKeyTile * wave, j1, l, kr0);
-        for (int it = 0; it < rounds; it += 2) {
-            const uint64_t t0 = j0 + 4 * kKeyTile * it + kKeyTile * wave;
-            tile_gload<D, 64>(kbase, t0 + 4 * kKeyTile, j1, l, kr1);
-            __builtin_amdgcn_sched_barrier(0);
-            tile(t0, kr0);
-            if (it + 1 < rounds) {
-                tile_gload<D, 64>(kbase, t0 + 8 * kKeyTile, j1, l, kr0);
-                __builtin_amdgcn_sched_barrier(0);
-                tile(t0 + 4 * kKeyTile, kr1);
-            }
-        }
-    }
-    float mo = __shfl_xor(m, 16);
-    m = mo > m ? mo : m;
-    mo = __shfl_xor(m, 32);
-    m = mo > m ? mo : m;
-    if (G == 0) red[wave][i] = m;
-    __syncthreads();
-    if (threadIdx.x < 16 && static_cast<int>(threadIdx.x) < a.g) {
-        float r = red[0][threadIdx.x];
-#pragma unroll
-        for (int w = 1; w < 4; w++) r = red[w][threadIdx.x] > r ? red[w][threadIdx.x] : r;
-        a.wgmax[(static_cast<uint64_t>(kvh) * a.g + threadIdx.x) * a.nwg_qk + wg] = r;
-    }
-}
-
-// ---------------------------------------------------------------------------
-// Decode pass 2: exponentials at the exact maximum and P.V partial sums.
-// grid (nwg_pv, kv_heads), 64 W threads, keys_pv = 32 W (W tiles of 32).
-//  1. wave w loads V tile w (whole rows) into registers;
-//  2. the exact maximum per query head is reduced from the pass-1 maxima;
-//  3. the g x 256 exponentials are computed once, split into hi + lo bf16 and
-//     stored in LDS as P columns: with g <= 8, columns 0..7 hold hi and 8..15
-//     lo, so one v_mfma_f32_16x16x32_bf16 covers both halves; with g > 8 the
-//     hi and lo halves are two 16-column blocks;
-//  4. the V tiles go to LDS (swizzled for the 16-row transpose reads);
-//  5. wave w reads all its P and V^T operands from LDS, then computes
-//     O^T = V^T . P^T for its dimension blocks over its share of the tiles;
-//     O = O(hi columns) + O(lo columns).
-// NCB: P column blocks, 1 for g <= 8, 2 for g <= 16.
-// W waves (and W tiles of keys) per workgroup: W = 8 holds 131 072 + 16 896 +
-// ~2 600 bytes of LDS at D = 256, one workgroup per CU; W = 4 half of that, two
-// per CU, so that one workgroup's work after its last load overlaps another's
-// stream when the grid takes several rounds.
-// ---------------------------------------------------------------------------
-template <int D, int W, int NCB>
-__global__ __launch_bounds__(64 * W, 8 / W) void decode_pv(DecodeArgs a)
-{
-    constexpr int THREADS = 64 * W;
-    constexpr int KEYS = W * kKeyTile;                          // 256 or 128
-    constexpr int PS = KEYS + 8;                                // P column stride, bf16
-    constexpr int DB = D / 16;                                  // 16-dimension blocks
-    constexpr int DBW = DB >= W ? DB / W : 1;                   // blocks per wave
-    constexpr int PARTS = DB >= W ? 1 : W / DB;                 // waves per block
-    constexpr int WPP = W / PARTS;                              // waves per part
-    constexpr int TPP = W / PARTS;                              // tiles per wave
-    static_assert(THREADS / KEYS == 2, "two head parities per workgroup");
-    __shared__ __attribute__((aligned(16))) uint16_t vt[W][kKeyTile * D];
-    __shared__ __attribute__((aligned(16))) uint16_t pc[2 * kDecodeMaxGroup * PS];
-    __shared__ float smax[kDecodeMaxGroup];
-    __shared__ float lpart[W][kDecodeMaxGroup];
-    __shared__ __attribute__((aligned(16))) float ored[PARTS > 1 ? (PARTS - 1) * WPP * NCB * DBW * 4 * 64 : 1];
-    const int kvh = blockIdx.y, wg = blockIdx.x, tid = threadIdx.x;
-    const int wave = tid >> 6, l = tid & 63, j = l & 15, G = l >> 4;
-    const uint64_t j0 = static_cast<uint64_t>(wg) * KEYS;
-    const uint64_t j1 = j0 + KEYS < a.n ? j0 + KEYS : a.n;
-    const uint16_t *vbase = a.v + static_cast<uint64_t>(kvh) * a.kv_stride;
-    constexpr int nh = 8 * NCB;                                 // lo columns start here
-    // The small loads go first: the vector-memory counter completes in order,
-    // so anything issued after the V tile would wait for all of it.
-    const int key_e = tid % KEYS;
-    const uint64_t gk_e = j0 + key_e;
-    const bool kv_e = gk_e < j1;
-    float sv[kDecodeMaxGroup / 2];
-#pragma unroll
-    for (int i = 0; i < kDecodeMaxGroup / 2; i++) {
-        const int h = tid / KEYS + 2 * i;
-        const int hc = h < a.g ? h : 0;
-        sv[i] = a.scores[static_cast<uint64_t>(kvh * a.g + hc) * a.npad + (kv_e ? gk_e : 0)];
-    }
-    // Pass-1 maxima: T lanes per head (THREADS / 8 for g <= 8, THREADS / 16
-    // for g <= 16); lane u reads entries u, u + T, .. of head t / T. The first
-    // batch is loaded before the V tile, later batches (more than 8 T
-    // workgroups in pass 1) after it.
-    constexpr int T = THREADS / nh;
-    const int jh = tid / T, u = tid % T;
-    const float *msrc = a.wgmax + (static_cast<uint64_t>(kvh) * a.g + (jh < a.g ? jh : 0)) * a.nwg_qk;
-    constexpr int BATCH = 8;
-    float mx[BATCH];
-#pragma unroll
-    for (int b = 0; b < BATCH; b++) {
-        const int w = u + b * T;
-        mx[b] = msrc[w < a.nwg_qk ? w : 0];
-    }
-    u32x4 vr[Tile<D, 64>::kPer];
-    tile_gload<D, 64>(vbase, j0 + kKeyTile * wave, j1, l, vr);
-    __builtin_amdgcn_sched_barrier(0);                          // all loads issued first
-    float m = kNegInf;
-#pragma unroll
-    for (int b = 0; b < BATCH; b++) m = (u + b * T < a.nwg_qk && mx[b] > m) ? mx[b] : m;
-    for (int w0 = u + BATCH * T; w0 < a.nwg_qk; w0 += BATCH * T) {
-#pragma unroll
-        for (int b = 0; b < BATCH; b++) {
-            const int w = w0 + b * T;
-            mx[b] = msrc[w < a.nwg_qk ? w : 0];
-        }
-#pragma unroll
-        for (int b = 0; b < BATCH; b++) m = (w0 + b * T < a.nwg_qk && mx[b] > m) ? mx[b] : m;
-    }
-
-    // 2. exact maximum per query head: a DPP reduction over the head's lanes
-    m = group_max_hi(m, T);
-    if (u == T - 1 && jh < a.g) smax[jh] = m;
-    __syncthreads();
-
-    // 3. dense exponentials: thread t owns key j0 + t % KEYS for heads
-    //    t / KEYS, t / KEYS + 2, ...; a wave covers 64 consecutive keys of one
-    //    head set
-    {
-#pragma unroll
-        for (int i = 0; i < kDecodeMaxGroup / 2; i++) {
-            const int h = tid / KEYS + 2 * i;
-            if (h >= a.g) break;
-            const float e = kv_e ? exp_poly(sv[i] - smax[h]) : 0.0f;
-            const uint32_t hb = bf16_rne(e);
-            pc[h * PS + key_e] = static_cast<uint16_t>(hb);
-            pc[(nh + h) * PS + key_e] = static_cast<uint16_t>(bf16_rne(e - __uint_as_float(hb << 16)));
-            const float sum = wave_sum_hi(e);
-            if (l == 63) lpart[wave][h] = sum;
-        }
-    }
-    // 4. V tile to LDS
-    tile_mask_lstore_v16<D, 64>(vt[wave], j0 + kKeyTile * wave, j1, l, vr);
-    __syncthreads();
-
-    // 5. P.V for this wave's dimension blocks. Columns that hold no head read
-    //    whatever the LDS holds; their outputs are never used. Every operand
-    //    read is issued before the first MFMA: reading each just before its
-    //    MFMA waits out the LDS latency once per MFMA.
-    const int dgi = wave % WPP, part = wave / WPP;
-    u32x4 bp[TPP][NCB], av[TPP][DBW];
-#pragma unroll
-    for (int tt = 0; tt < TPP; tt++) {
-        const int t = part * TPP + tt;
-#pragma unroll
-        for (int c = 0; c < NCB; c++) bp[tt][c] = load16(pc + (16 * c + j) * PS + kKeyTile * t + 8 * G);
-#pragma unroll
-        for (int db = 0; db < DBW; db++) av[tt][db] = vt16_operand<D>(vt[t], 16 * (dgi * DBW + db), l);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    f32x4 o[NCB][DBW] = {};
-#pragma unroll
-    for (int tt = 0; tt < TPP; tt++)
-#pragma unroll
-        for (int db = 0; db < DBW; db++)
-#pragma unroll
-            for (int c = 0; c < NCB; c++) o[c][db] = mfma16(av[tt][db], bp[tt][c], o[c][db]);
-    if (PARTS > 1) {
-        if (part > 0) {
-            float *dst = ored + ((part - 1) * WPP + dgi) * (NCB * DBW * 4 * 64);
-#pragma unroll
-            for (int c = 0; c < NCB; c++)
-#pragma unroll
-                for (int db = 0; db < DBW; db++)
-#pragma unroll
-                    for (int r = 0; r < 4; r++) dst[((c * DBW + db) * 4 + r) * 64 + l] = o[c][db][r];
-        }
-        __syncthreads();
-        if (part == 0)
-            for (int p = 1; p < PARTS; p++) {
-                const float *src = ored + ((p - 1) * WPP + dgi) * (NCB * DBW * 4 * 64);
-#pragma unroll
-                for (int c = 0; c < NCB; c++)
-#pragma unroll
-                    for (int db = 0; db < DBW; db++)
-#pragma unroll
-                        for (int r = 0; r < 4; r++) o[c][db][r] += src[((c * DBW + db) * 4 + r) * 64 + l];
-            }
-    }
-    // O(head) = O(hi column) + O(lo column): lane j + 8 holds the lo column
-    // of head j when g <= 8, the second block when g > 8.
-    const uint64_t pbase = (static_cast<uint64_t>(kvh) * a.nwg_pv + wg) * a.g;
-#pragma unroll
-    for (int db = 0; db < DBW; db++) {
-        f32x4 s;
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-            if constexpr (NCB == 1) s[r] = o[0][db][r] + __shfl_xor(o[0][db][r], 8);
-            else s[r] = o[0][db][r] + o[NCB - 1][db][r];
-        }
-        if (part == 0 && j < 8 * NCB && j < a.g) {
-            float *dst = a.part_o + (pbase + j) * D + 16 * (dgi * DBW + db) + 4 * G;
-            *reinterpret_cast<float4 *>(dst) = float4{s[0], s[1], s[2], s[3]};
-        }
-    }
-    if (tid < a.g) {
-        // heads of parity p were summed by waves p KEYS/64 .., 64 keys each
-        const int p0 = (tid % (THREADS / KEYS)) * (KEYS / 64);
-        float L = 0.0f;
-        for (int w = 0; w < KEYS / 64; w++) L += lpart[p0 + w][tid];
-        a.part_l[pbase + tid] = L;
-    }
-}
-
-// ---------------------------------------------------------------------------
-// Decode pass 3: out[h] = bf16(sum_w O_w / sum_w l_w).
-// grid (heads, D/64), 512 threads: 64 dimensions x 8 interleaved partial
-// subsets; every thread issues all its loads before adding (one round trip
-// for up to 8 * 16 partials), and the subsets are summed in a fixed order.
-// ---------------------------------------------------------------------------
-constexpr int kCombineSubs = 8;
-
-template <int D>
-__global__ __launch_bounds__(512) void decode_combine(DecodeArgs a)
-{
-    __shared__ float ored[kCombineSubs][64];
-    __shared__ float lred[kCombineSubs];
-    const int h = blockIdx.x, kvh = h / a.g, jh = h % a.g;
-    const int t = threadIdx.x & 63, sub = threadIdx.x >> 6, dim = blockIdx.y * 64 + t;
-    float o = 0.0f, L = 0.0f;
-    const uint64_t base = static_cast<uint64_t>(kvh) * a.nwg_pv * a.g + jh;
-    constexpr int BATCH = 16;
-    for (int w0 = sub; w0 < a.nwg_pv; w0 += kCombineSubs * BATCH) {
-        float xo[BATCH], xl[BATCH];
-#pragma unroll
-        for (int b = 0; b < BATCH; b++) {
-            const int w = w0 + kCombineSubs * b;
-            const uint64_t part = base + static_cast<uint64_t>(w < a.nwg_pv ? w : 0) * a.g;
-            xo[b] = a.part_o[part * D + dim];
-            xl[b] = a.part_l[part];
-        }
-#pragma unroll
-        for (int b = 0; b < BATCH; b++)
-            if (w0 + kCombineSubs * b < a.nwg_pv) {
-                o += xo[b];
-                L += xl[b];
-            }
-    }
-    ored[sub][t] = o;
-    if (t == 0) lred[sub] = L;
-    __syncthreads();
-    if (sub == 0) {
-        float os = 0.0f, ls = 0.0f;
-#pragma unroll
-        for (int i = 0; i < kCombineSubs; i++) {
-            os += ored[i][t];
-            ls += lred[i];
-        }
-        uint16_t ob = static_cast<uint16_t>(cvt_out(os / ls));
-        if (a.gate) ob = gate_bf16(ob, a.gate[static_cast<uint64_t>(h) * D + dim]);
-        a.out[static_cast<uint64_t>(h) * D + dim] = ob;
-    }
-}
-
-// ---------------------------------------------------------------------------
-// Prefill: the causal attention of a chunk, two passes over the keys in one
-// workgroup: the exact row maxima, then exponentials and P.V.
-// grid (row groups, heads / HPW), 512 threads = 8 waves, two per SIMD. Wave w
-// serves query head blockIdx.y * HPW + w % HPW and rows r0 + 32 (w / HPW) ..
-// +32, r0 the group's first row; the HPW heads of a workgroup share one KV
-// head (HPW = 8 when g is a multiple of 8), so all waves read the same K and V
-// tiles from LDS. Tiles are double-buffered: the global loads of tile t+1 are
-// in flight while tile t is computed. Tiles below the diagonal of all of a
-// wave's rows skip the causal mask.
-// POW2 (the scale is a positive power of two): fl(fl(dot * scale) - M) equals
-// fl(dot - Mraw) * scale exactly, Mraw being the maximum of the unscaled
-// dot products, and the scale folds exactly into the exponential's clamp
-// (-87.33654 / scale) and multiplier (log2(e) * scale). Otherwise every score
-// is scaled first, as in the reference.
-// ---------------------------------------------------------------------------
-struct ExpArgs {
-    float m;        // POW2: Mraw; otherwise the scaled maximum M
-    float scale;    // otherwise: the scale
-    float clamp;    // POW2: -87.33654 / scale; otherwise -87.33654
-    float mul;      // POW2: 1.442695 * scale; otherwise 1.442695
-};
-
-template <bool POW2>
-__device__ __forceinline__ float exp_score(float acc, const ExpArgs &x)
-{
-    const float d = POW2 ? acc - x.m : acc * x.scale - x.m;
-    const float t1 = __builtin_fmaxf(d, x.clamp) * x.mul;
-    const float t2 = __builtin_rintf(t1);
-    const float f = t1 - t2;
-    float p = __builtin_fmaf(f, 0.00967248f, 0.05550411f);
-    p = __builtin_fmaf(f, p, 0.2402265f);
-    p = __builtin_fmaf(f, p, 0.6931472f);
-    p = __builtin_fmaf(f, p, 1.0f);
-    return __builtin_ldexpf(p, static_cast<int>(t2));
-}
-
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-typedef float f32x2 __attribute__((ext_vector_type(2)));
-
-// Round two f32 to bf16, nearest even, packed low/high (v_cvt_pk_bf16_f32).
-__device__ __forceinline__ uint32_t pk_bf16(float a, float b)
-{
-    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{a, b}), bf16x2));
-}
-
-// Eight exponentials as hi and lo bf16 halves, packed in k order.
-__device__ __forceinline__ void split_pack_hw(const float *e, u32x4 &hi, u32x4 &lo)
-{
-#pragma unroll
-    for (int s = 0; s < 4; s++) {
-        const uint32_t h = pk_bf16(e[2 * s], e[2 * s + 1]);
-        const float r0 = e[2 * s] - __uint_as_float(h << 16);
-        const float r1 = e[2 * s + 1] - __uint_as_float(h & 0xFFFF0000u);
-        hi[s] = h;
-        lo[s] = pk_bf16(r0, r1);
-    }
-}
-
-template <int D, int HPW, bool POW2>
-__global__ __launch_bounds__(512, 1) void prefill_attn(PrefillArgs a)
-{
-    constexpr int NW = 8, RB = NW / HPW;
-    constexpr int SK = Pad<D>::K, SV = Pad<D>::V;
-    __shared__ __attribute__((aligned(16))) uint16_t kb[2][kKeyTile * SK];
-    __shared__ __attribute__((aligned(16))) uint16_t vb[2][kKeyTile * SV];
-    const int tid = threadIdx.x;
-    const int wave = tid >> 6, l = tid & 63, col = l & 31, grp = l >> 5;
-    const int head = blockIdx.y * HPW + (wave % HPW);
-    const int kvh = head / a.gqa;
-    const uint64_t rgroup = gridDim.x - 1 - blockIdx.x;       // heaviest rows first
-    const uint64_t wg_r0 = rgroup * (32 * RB);
-    const uint64_t w_r0 = wg_r0 + 32 * (wave / HPW);
-    const uint64_t row = w_r0 + col;
-    const bool rowv = row < a.rows;
-    const bool wact = w_r0 < a.rows;
-    const uint64_t wg_rend = wg_r0 + 32 * RB < a.rows ? wg_r0 + 32 * RB : a.rows;
-    const int ntiles = static_cast<int>((a.past + wg_rend + kKeyTile - 1) / kKeyTile);
-    const int nfull = wact ? static_cast<int>((a.past + w_r0 + 1) / kKeyTile) : 0;  // no mask needed
-    const uint64_t lim = a.past + row;                         // last visible key of this row
-
-    const uint16_t *kg = a.k + static_cast<uint64_t>(kvh) * a.kv_stride;
-    const uint16_t *vg = a.v + static_cast<uint64_t>(kvh) * a.kv_stride;
-    u32x4 kr[Tile<D, 512>::kPer], vr[Tile<D, 512>::kPer];
-    u32x4 qb[D / 16];
-    const uint16_t *qp = a.q + (rowv ? row : 0) * a.q_row + static_cast<uint64_t>(head) * a.q_head;
-#pragma unroll
-    for (int s = 0; s < D / 16; s++) {
-        const u32x4 v = load16(qp + 16 * s + 8 * grp);
-        qb[s] = rowv ? v : u32x4{0, 0, 0, 0};
-    }
-    tile_gload<D, 512>(kg, 0, a.n, tid, kr);
-    const int arow = swap23(col) * SK + 8 * grp;
-    // One accumulation chain: a second one would not fit the 256 registers
-    // of two waves per SIMD; the other wave on the SIMD fills the gaps.
-    auto qk = [&](const uint16_t *kt) {
-        f32x16 acc = {};
-#pragma unroll
-        for (int s = 0; s < D / 16; s++) acc = mfma(load16(kt + arow + 16 * s), qb[s], acc);
-        return acc;
-    };
-
-    // Every wave computes every tile of the workgroup's key range: tiles past
-    // a wave's last visible key take the masked path and contribute nothing.
-    // With no wave-dependent branches around them, the loads of the next
-    // tiles stay in flight across the compute.
-
-    // pass 1: exact row maxima (of the unscaled dot products when POW2).
-    // Out-of-range keys of the last tile read row 0 and are never visible.
-    tile_lstore_padded<D, 512>(kb[0], SK, tid, kr);
-    __syncthreads();
-    float m = kNegInf;
-    for (int t = 0; t < ntiles; t++) {
-        const uint64_t t0 = static_cast<uint64_t>(t) * kKeyTile;
-        const bool last = t + 1 == ntiles;
-        tile_gload<D, 512>(kg, last ? 0 : t0 + kKeyTile, a.n, tid, kr);   // after the last: pass 2's first tile
-        if (last) tile_gload<D, 512>(vg, 0, a.n, tid, vr);
-        __builtin_amdgcn_sched_barrier(0);
-        const f32x16 acc = qk(kb[t & 1]);
-        if (t < nfull) {
-#pragma unroll
-            for (int r = 0; r < 16; r++) m = __builtin_fmaxf(m, POW2 ? acc[r] : acc[r] * a.scale);
-        } else {
-            // keys t0 + k with k <= vis are visible to this row
-            const int vis = static_cast<int>(static_cast<int64_t>(lim) - static_cast<int64_t>(t0));
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const float s = POW2 ? acc[r] : acc[r] * a.scale;
-                if (key_of(r, grp) <= vis) m = __builtin_fmaxf(m, s);
-            }
-        }
-        if (!last) tile_lstore_padded<D, 512>(kb[(t + 1) & 1], SK, tid, kr);
-        __syncthreads();
-    }
-    m = __builtin_fmaxf(m, __shfl_xor(m, 32));
-    ExpArgs ex;
-    ex.m = m;
-    ex.scale = a.scale;
-    ex.clamp = POW2 ? -87.33654f / a.scale : -87.33654f;
-    ex.mul = POW2 ? 1.442695f * a.scale : 1.442695f;
-
-    // pass 2: exponentials at the exact maximum, P.V with P = hi + lo. The
-    // next K tile is loaded first, the next V tile after the first half's
-    // softmax, so that their staging registers are not live at the peak.
-    tile_lstore_padded<D, 512>(kb[0], SK, tid, kr);
-    tile_mask<D, 512>(0, a.n, tid, vr);
-    tile_lstore_padded<D, 512>(vb[0], SV, tid, vr);
-    __syncthreads();
-    f32x16 o[D / 32];
-#pragma unroll
-    for (int dt = 0; dt < D / 32; dt++) o[dt] = f32x16{};
-    float lsum = 0.0f;
-    for (int t = 0; t < ntiles; t++) {
-        const uint64_t t0 = static_cast<uint64_t>(t) * kKeyTile;
-        const int b = t & 1;
-        tile_gload<D, 512>(kg, t0 + kKeyTile, a.n, tid, kr);  // past the end: row 0, unused
-        __builtin_amdgcn_sched_barrier(0);
-        const f32x16 acc = qk(kb[b]);
-        const bool full = t < nfull;
-        const int vis = static_cast<int>(static_cast<int64_t>(lim) - static_cast<int64_t>(t0));
-        // exponentials of one half of the tile's keys as hi and lo operands
-        auto half = [&](int h, auto masked, u32x4 &hi, u32x4 &lo) {
-            constexpr bool MASKED = decltype(masked)::value;
-            float ev[8];
-#pragma unroll
-            for (int r = 0; r < 8; r++) {
-                const float e = exp_score<POW2>(acc[8 * h + r], ex);
-                ev[r] = !MASKED || key_of(8 * h + r, grp) <= vis ? e : 0.0f;
-                lsum += ev[r];
-            }
-            split_pack_hw(ev, hi, lo);
-        };
-        auto pv = [&](int h, const u32x4 &hi, const u32x4 &lo) {
-            __builtin_amdgcn_s_setprio(1);
-#pragma unroll
-            for (int dt = 0; dt < D / 32; dt++) {
-                const u32x4 av = vt_operand_padded<D>(vb[b], 16 * h, 32 * dt, l);
-                o[dt] = mfma(av, hi, o[dt]);
-                o[dt] = mfma(av, lo, o[dt]);
-            }
-            __builtin_amdgcn_s_setprio(0);
-        };
-        u32x4 hi, lo;
-        if (full) half(0, std::false_type{}, hi, lo);
-        else half(0, std::true_type{}, hi, lo);
-        tile_gload<D, 512>(vg, t0 + kKeyTile, a.n, tid, vr);
-        __builtin_amdgcn_sched_barrier(0);
-        pv(0, hi, lo);
-        if (full) half(1, std::false_type{}, hi, lo);
-        else half(1, std::true_type{}, hi, lo);
-        pv(1, hi, lo);
-        if (t + 1 < ntiles) {
-            tile_lstore_padded<D, 512>(kb[b ^ 1], SK, tid, kr);
-            tile_mask<D, 512>(t0 + kKeyTile, a.n, tid, vr);
-            tile_lstore_padded<D, 512>(vb[b ^ 1], SV, tid, vr);
-        }
-        __syncthreads();
-    }
-    lsum += __shfl_xor(lsum, 32);
-    if (rowv) {
-        uint16_t *op = a.out + row * a.out_row + static_cast<uint64_t>(head) * D;
-        const uint16_t *gp = a.gate ? a.gate + row * a.gate_row + static_cast<uint64_t>(head) * D : nullptr;
-#pragma unroll
-        for (int dt = 0; dt < D / 32; dt++)
-#pragma unroll
-            for (int c = 0; c < 4; c++) {
-                uint32_t b0 = cvt_out(o[dt][4 * c] / lsum), b1 = cvt_out(o[dt][4 * c + 1] / lsum);
-                uint32_t b2 = cvt_out(o[dt][4 * c + 2] / lsum), b3 = cvt_out(o[dt][4 * c + 3] / lsum);
-                const int at = 32 * dt + 8 * c + 4 * grp;
-                if (gp) {
-                    const uint2 g = *reinterpret_cast<const uint2 *>(gp + at);
-                    b0 = gate_bf16(static_cast<uint16_t>(b0), static_cast<uint16_t>(g.x));
-                    b1 = gate_bf16(static_cast<uint16_t>(b1), static_cast<uint16_t>(g.x >> 16));
-                    b2 = gate_bf16(static_cast<uint16_t>(b2), static_cast<uint16_t>(g.y));
-                    b3 = gate_bf16(static_cast<uint16_t>(b3), static_cast<uint16_t>(g.y >> 16));
-                }
-                uint2 w = {b0 | (b1 << 16), b2 | (b3 << 16)};
-                *reinterpret_cast<uint2 *>(op + at) = w;
-            }
-    }
-}
 
 // ---------------------------------------------------------------------------
 // KV append (src/jit/target/x86/execution/kv.rs:15-69): row r of KV head h of
@@ -1157,7 +276,7 @@ __global__ __launch_bounds__(256) void output_gate(GateArgs a)
 // ---------------------------------------------------------------------------
 // launchers
 // ---------------------------------------------------------------------------
-bool head_dim_supported(int d) { return d == 64 || d == 128 || d == 256; }
+bool head_dim_supported(int d) { return d >= 32 && d <= 512 && d % 32 == 0; }
 
 // A positive power of two in [2^-20, 2^20]: scaling by it is exact for the
 // scores and for the folded exponential constants.
@@ -1181,7 +300,7 @@ static hipError_t decode_d(const DecodeArgs &a, int kv_heads, hipStream_t s)
         if (a.keys_pv == 4 * kKeyTile) hipLaunchKernelGGL((decode_pv<D, 4, 2>), gpv, dim3(256), 0, s, a);
         else hipLaunchKernelGGL((decode_pv<D, 8, 2>), gpv, dim3(512), 0, s, a);
     }
-    hipLaunchKernelGGL(decode_combine<D>, dim3(kv_heads * a.g, D / 64), dim3(64 * kCombineSubs), 0, s, a);
+    hipLaunchKernelGGL(decode_combine<D>, dim3(kv_heads * a.g, (D + 63) / 64), dim3(64 * kCombineSubs), 0, s, a);
     return hipGetLastError();
 }
 
@@ -1191,7 +310,7 @@ hipError_t launch_decode(const DecodeArgs &a, int head_dim, int kv_heads, hipStr
     case 64: return decode_d<64>(a, kv_heads, s);
     case 128: return decode_d<128>(a, kv_heads, s);
     case 256: return decode_d<256>(a, kv_heads, s);
-    default: return hipErrorInvalidValue;
+    default: return launch_decode_more(a, head_dim, kv_heads, s);
     }
 }
 
@@ -1250,7 +369,7 @@ hipError_t launch_prefill(const PrefillArgs &a, int head_dim, int heads, hipStre
     case 64: prefill_d<64>(a, heads, s); break;
     case 128: prefill_d<128>(a, heads, s); break;
     case 256: prefill_d<256>(a, heads, s); break;
-    default: return hipErrorInvalidValue;
+    default: return launch_prefill_more(a, head_dim, heads, s);
     }
     return hipGetLastError();
 }

@@ -64,8 +64,8 @@ extern "C" {
 typedef enum hsdpa_status {
     HSDPA_OK = 0,
     HSDPA_ERR_EMPTY = 1,            /* Decline::Empty: heads, gqa or head_dim is 0 */
-    HSDPA_ERR_HEAD_DIM = 2,         /* Decline::HeadDim: not a multiple of 32, above 512,
-                                       or above what the GPU kernels hold (256) */
+    HSDPA_ERR_HEAD_DIM = 2,         /* Decline::HeadDim: not a multiple of 32, or above 512
+                                       (ir.rs:130-162) */
     HSDPA_ERR_GQA = 3,              /* heads not a multiple of gqa (attention.rs:61-64) */
     HSDPA_ERR_STRIDE = 4,           /* q_head < head_dim, heads*q_head > q_row,
                                        heads*head_dim > out_row, kv_stride < capacity*head_dim

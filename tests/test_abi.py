@@ -52,8 +52,9 @@ def test_status_strings_and_version():
 
 @pytest.mark.parametrize("kw,code", [
     (dict(heads=16, gqa=3, head_dim=256, kv_capacity=10), "HSDPA_ERR_GQA"),
-    (dict(heads=16, gqa=8, head_dim=96, kv_capacity=10), "HSDPA_ERR_HEAD_DIM"),
     (dict(heads=16, gqa=8, head_dim=48, kv_capacity=10), "HSDPA_ERR_HEAD_DIM"),
+    (dict(heads=16, gqa=8, head_dim=16, kv_capacity=10), "HSDPA_ERR_HEAD_DIM"),
+    (dict(heads=16, gqa=8, head_dim=544, kv_capacity=10), "HSDPA_ERR_HEAD_DIM"),
     (dict(heads=16, gqa=8, head_dim=1024, kv_capacity=10), "HSDPA_ERR_HEAD_DIM"),
     (dict(heads=16, gqa=8, head_dim=256, kv_capacity=10, sink=True), "HSDPA_ERR_SINK_UNSUPPORTED"),
     (dict(heads=0, gqa=1, head_dim=256, kv_capacity=1), "HSDPA_ERR_EMPTY"),
@@ -75,7 +76,9 @@ def test_plan_accepts_engine_geometries():
     # the gated layout: q rows carry Q then the gate, 2*q_dim apart
     p = hsdpa.Plan(16, 8, 256, 8192, q_row=2 * 16 * 256, out_row=16 * 256, grouped=True)
     assert p.workspace_bytes > 0
-    for d in (64, 128, 256):
+    # every head dimension the reference's SdpaShape::check accepts: multiples
+    # of 32 up to 512 (ir.rs:130-162)
+    for d in range(32, 513, 32):
         hsdpa.Plan(8, 2, d, 1024)
 
 
