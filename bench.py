@@ -42,8 +42,8 @@ MFMA_BF16_PEAK_TFS = 2500.0  # MI355X dense bf16 MFMA, TFLOP/s
 # every L2 fill from the memory fabric, so Infinity Cache hits are included.
 # Summary and commands: profiles/pmc_traffic_decode32k_prefill4096.md
 TRAFFIC_BYTES = {
-    "decode_32k": (2 * (16452.3 + 17547.9 + 1087.9) + (2176.4 + 2056.0 + 8.0)) * 1024,
-    "prefill_4096_after_8192": (2 * 1267085.2 + 35840.0) * 1024,
+    "decode_32k": (2 * (16451.5 + 17545.4 + 1091.5) + (2176.4 + 2056.0 + 8.0)) * 1024,
+    "prefill_4096_after_8192": (2 * 1204556.0 + 36352.0) * 1024,
 }
 
 
@@ -68,6 +68,8 @@ def time_steps(torch, plan, w, q, ks, vs, out, ws, steps, warmup):
     """Warm up eagerly, capture `steps` calls into a graph, replay it once
     after a synchronize, return (ms per step, eager output, graph output)."""
     stream = torch.cuda.Stream()
+    # the buffers were filled on the current stream (copies, clones, zeros)
+    stream.wait_stream(torch.cuda.current_stream())
     nb = ws.numel()
 
     def call(i):
@@ -182,10 +184,14 @@ def time_layer(torch, hsdpa, w, copies, steps, warmup):
     check = []
     for fused in (True, False):
         b = layer_buffers(torch, w, copies)[0]
+        stream.wait_stream(torch.cuda.current_stream())   # filled there: copies, clones, zeros
         with torch.cuda.stream(stream):
             layer_step(hsdpa, plan, w, b, 0, ws, fused, stream)
         torch.cuda.synchronize()
         check.append([b[n].clone() for n in ("q", "k", "out")] + [b["keys"][0].clone(), b["values"][0].clone()])
+        # the clones run on the current stream; the warm-up steps rewrite q, k
+        # and the cache in place on `stream`
+        stream.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(stream):
             for i in range(warmup):
                 layer_step(hsdpa, plan, w, b, i, ws, fused, stream)
