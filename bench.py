@@ -15,7 +15,7 @@ the 256 MB Infinity Cache cannot hold the working set. The K timed steps
 are captured once into a HIP graph and replayed, so the figure is GPU time,
 not Python launch time; the replay's output is checked against an eager call.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-prefill] [--no-layer]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-prefill] [--no-layer] [--no-sweep]
 
 Also timed: the whole attention chain of a gated Qwen3.5 layer (q/k norm and
 RoPE, KV append, attention, output gate) fused into one call against the same
@@ -262,6 +262,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-layer", action="store_true", help="skip the fused layer chain timing")
+    ap.add_argument("--no-sweep", action="store_true", help="skip the decode length sweep")
     ap.add_argument("--prefill-steps", type=int, default=0, help="timed prefill steps (default: --steps, max 20)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -347,6 +348,27 @@ def main():
         wp_cpu = wp
     else:
         wp_cpu = None
+
+    # ---- decode at other lengths (same heads): fixed latency vs stream ---------
+    if not args.no_sweep:
+        sweep = {}
+        for n in (1024, 8192, 32768, 131072):
+            wn = W.make(f"decode_{n}", heads=16, kv_heads=2, head_dim=256, rows=1, past=n - 1, seed=3)
+            copies = max(4, -(-(1 << 30) // (2 * 2 * n * 256 * 2)))       # at least 1 GiB of distinct caches
+            q, ks, vs, out = device_buffers(torch, wn, copies=copies)
+            plan_n = hsdpa.Plan(wn.heads, wn.gqa, wn.head_dim, wn.capacity)
+            ws_n = torch.empty(plan_n.workspace_bytes, dtype=torch.uint8, device="cuda")
+            n_ms, _, eager, replay = time_steps(torch, plan_n, wn, q, ks, vs, out, ws_n, 20, 3)
+            if not torch.equal(eager, replay):
+                print(f"decode {n}: graph replay differs from the eager call", file=sys.stderr)
+                sys.exit(3)
+            n_gbs = wn.decode_bytes() / (n_ms * 1e-3) / 1e9
+            sweep[str(n)] = {"us": round(n_ms * 1e3, 2), "GB/s": round(n_gbs, 1), "frac": round(n_gbs / HBM_PEAK_GBS, 4)}
+            log(f"decode {n:6d} keys: {n_ms*1e3:7.2f} us, {n_gbs:7.1f} GB/s ({n_gbs/HBM_PEAK_GBS:.1%})")
+            del q, ks, vs, out, ws_n
+            torch.cuda.empty_cache()
+        result["decode_sweep"] = {"keys": sweep, "config": "16 query heads on 2 KV heads, head_dim 256, 1 row; "
+                                                           "caches rotated over at least 1 GiB; 20 graph steps"}
 
     # ---- the layer chain: norms, append, attention, gate -------------------------
     if not args.no_layer:

@@ -107,6 +107,11 @@ CASES = [
     ("decode_g32_through_prefill", 32, 1, 128, 1, 700, 800, True, 64),
     # k and v 2 bytes off: the decode takes the separate element launch
     ("decode_unaligned_kv", 16, 2, 256, 1, 1000, 1100, True, 64, 1),
+    # head dimensions outside 64/128/256: the generic norm path and the other
+    # attention instantiations
+    ("decode_d160_gated", 8, 2, 160, 1, 900, 1000, True, 32),
+    ("prefill_d96_r40_after_60", 8, 4, 96, 40, 60, 120, True, 64),
+    ("decode_d512_ungated", 4, 1, 512, 1, 300, 400, False, 128),
 ]
 
 
