@@ -299,10 +299,12 @@ static hsdpa_status run_attention(const hsdpa_plan *plan, const hsdpa_call *call
     char *ws = static_cast<char *>(call->workspace);
     const uint64_t n = call->past + call->rows;
     const int d = static_cast<int>(s.head_dim);
-    // decode kernels: one query row and at most kDecodeMaxGroup query heads per
-    // KV head (their LDS holds the group's exponentials); otherwise the causal
-    // kernel serves the row.
-    if (call->rows == 1 && s.gqa <= static_cast<uint64_t>(hsdpa::kDecodeMaxGroup)) {
+    // decode kernels: one query row, the query heads of a KV head in `sub`
+    // equal groups of at most kDecodeMaxGroup (their LDS holds a group's
+    // exponentials; each group streams the KV head's cache); otherwise the
+    // causal kernel serves the row.
+    const int sub = hsdpa::decode_groups(static_cast<int>(s.gqa));
+    if (call->rows == 1 && sub > 0) {
         hsdpa::DecodeArgs a{};
         a.q = call->q;
         a.k = call->keys;
@@ -316,19 +318,21 @@ static hsdpa_status run_attention(const hsdpa_plan *plan, const hsdpa_call *call
         a.npad = plan->dec_npad;
         a.kv_stride = s.kv_stride;
         a.q_head = s.q_head;
-        a.g = static_cast<int>(s.gqa);
+        a.g = static_cast<int>(s.gqa) / sub;
+        a.sub = sub;
+        const uint64_t groups = plan->kv_heads * static_cast<uint64_t>(sub);
         // pass 1: a tile per wave, or several in turn (the next one in flight)
         // once one tile per wave would need more than one round of two
         // workgroups per compute unit; this bounds the maxima pass 2 reads
         const uint64_t nqk1 = (n + hsdpa::kDecodeKeysQK - 1) / hsdpa::kDecodeKeysQK;
         const uint64_t slots = 2 * static_cast<uint64_t>(cus > 0 ? cus : 1);
-        const uint64_t rq = hsdpa::decode_loop_ok(d) ? (plan->kv_heads * nqk1 + slots - 1) / slots : 1;
+        const uint64_t rq = hsdpa::decode_loop_ok(d) ? (groups * nqk1 + slots - 1) / slots : 1;
         a.keys_qk = hsdpa::kDecodeKeysQK * static_cast<int>(rq > 1 ? rq : 1);
         // pass 2 takes 8 tiles per workgroup, or 4 while the smaller
         // workgroups still fit the compute units in one round (short caches:
         // twice the workgroups, measured faster up to 16K keys at 2 KV heads)
         const uint64_t nwg4 = (n + 4 * hsdpa::kKeyTile - 1) / (4 * hsdpa::kKeyTile);
-        a.keys_pv = plan->kv_heads * nwg4 <= static_cast<uint64_t>(cus) || !hsdpa::decode_wide_ok(d)
+        a.keys_pv = groups * nwg4 <= static_cast<uint64_t>(cus) || !hsdpa::decode_wide_ok(d)
                         ? 4 * hsdpa::kKeyTile
                         : hsdpa::kDecodeKeysPV;
         a.nwg_qk = static_cast<int>((n + a.keys_qk - 1) / a.keys_qk);

@@ -352,7 +352,9 @@ __global__ __launch_bounds__(256) void decode_qk(DecodeArgs a)
     constexpr int C = D / 8, KM = swz_group<D>() - 1;          // chunks per row, swizzle mask
     __shared__ __attribute__((aligned(16))) uint16_t kt[4][kKeyTile * D];
     __shared__ float red[4][16];
-    const int kvh = blockIdx.y, wg = blockIdx.x;
+    // blockIdx.y: the KV head; blockIdx.z: which of its gridDim.z groups of g
+    // query heads (one unless a KV head has more than 16)
+    const int kvh = blockIdx.y * gridDim.z + blockIdx.z, wg = blockIdx.x;
     const int wave = threadIdx.x >> 6, l = threadIdx.x & 63, i = l & 15, G = l >> 4;
     const uint64_t j0 = static_cast<uint64_t>(wg) * a.keys_qk;
     const uint64_t j1 = j0 + a.keys_qk < a.n ? j0 + a.keys_qk : a.n;
@@ -364,7 +366,7 @@ __global__ __launch_bounds__(256) void decode_qk(DecodeArgs a)
     u32x4 qb[KS];
 #pragma unroll
     for (int s = 0; s < KS; s++) qb[s] = load16(qp + 32 * s);
-    const uint16_t *kbase = a.k + static_cast<uint64_t>(kvh) * a.kv_stride;
+    const uint16_t *kbase = a.k + static_cast<uint64_t>(blockIdx.y) * a.kv_stride;
     uint16_t *my = kt[wave];
     float m = kNegInf;
     // One 32-key tile of the wave: staged through its LDS rows, scored, stored.
@@ -489,11 +491,11 @@ __global__ __launch_bounds__(64 * W, D > 256 ? 1 : 8 / W) void decode_pv(DecodeA
     __shared__ float smax[kDecodeMaxGroup];
     __shared__ float lpart[W][kDecodeMaxGroup];
     __shared__ __attribute__((aligned(16))) float ored[PARTS > 1 ? (PARTS - 1) * WPP * NCB * DBW * 4 * 64 : 1];
-    const int kvh = blockIdx.y, wg = blockIdx.x, tid = threadIdx.x;
+    const int kvh = blockIdx.y * gridDim.z + blockIdx.z, wg = blockIdx.x, tid = threadIdx.x;   // as in decode_qk
     const int wave = tid >> 6, l = tid & 63, j = l & 15, G = l >> 4;
     const uint64_t j0 = static_cast<uint64_t>(wg) * KEYS;
     const uint64_t j1 = j0 + KEYS < a.n ? j0 + KEYS : a.n;
-    const uint16_t *vbase = a.v + static_cast<uint64_t>(kvh) * a.kv_stride;
+    const uint16_t *vbase = a.v + static_cast<uint64_t>(blockIdx.y) * a.kv_stride;
     constexpr int nh = 8 * NCB;                                 // lo columns start here
     // The small loads go first: the vector-memory counter completes in order,
     // so anything issued after the V tile would wait for all of it.

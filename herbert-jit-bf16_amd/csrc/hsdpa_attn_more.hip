@@ -19,7 +19,7 @@ namespace hsdpa {
 template <int D>
 static hipError_t decode_more_d(const DecodeArgs &a, int kv_heads, hipStream_t s)
 {
-    const dim3 gqk(a.nwg_qk, kv_heads), gpv(a.nwg_pv, kv_heads);
+    const dim3 gqk(a.nwg_qk, kv_heads, a.sub), gpv(a.nwg_pv, kv_heads, a.sub);
     if constexpr (D <= 256) {
         if (a.keys_qk > 4 * kKeyTile) hipLaunchKernelGGL((decode_qk<D, true>), gqk, dim3(256), 0, s, a);
         else hipLaunchKernelGGL((decode_qk<D, false>), gqk, dim3(256), 0, s, a);
@@ -39,7 +39,7 @@ static hipError_t decode_more_d(const DecodeArgs &a, int kv_heads, hipStream_t s
             return hipErrorInvalidValue;
         }
     }
-    hipLaunchKernelGGL(decode_combine<D>, dim3(kv_heads * a.g, (D + 63) / 64), dim3(64 * kCombineSubs), 0, s, a);
+    hipLaunchKernelGGL(decode_combine<D>, dim3(kv_heads * a.sub * a.g, (D + 63) / 64), dim3(64 * kCombineSubs), 0, s, a);
     return hipGetLastError();
 }
 

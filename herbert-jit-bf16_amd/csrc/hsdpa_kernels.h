@@ -13,15 +13,16 @@ struct DecodeArgs {
     const uint16_t *k;      // cache, head kvh at k + kvh*kv_stride
     const uint16_t *v;
     uint16_t *out;          // head h at out + h*head_dim
-    float *scores;          // [kv_heads][g][npad] scaled scores
-    float *wgmax;           // [kv_heads][g][nwg_qk] per-workgroup maxima
-    float *part_o;          // [kv_heads][nwg_pv][g][head_dim] unnormalised partial outputs
-    float *part_l;          // [kv_heads][nwg_pv][g] partial sums of exponentials
+    float *scores;          // [groups][g][npad] scaled scores (groups = kv_heads * sub)
+    float *wgmax;           // [groups][g][nwg_qk] per-workgroup maxima
+    float *part_o;          // [groups][nwg_pv][g][head_dim] unnormalised partial outputs
+    float *part_l;          // [groups][nwg_pv][g] partial sums of exponentials
     uint64_t n;             // visible keys (past + 1)
     uint64_t npad;          // scores row length, a multiple of the key tile
     uint64_t kv_stride;
     uint64_t q_head;
-    int g;                  // query heads per KV head (<= kDecodeMaxGroup)
+    int g;                  // query heads per group (<= kDecodeMaxGroup)
+    int sub;                // groups per KV head: g * sub query heads share one (the grid's z)
     int nwg_qk, nwg_pv;     // workgroups per KV head of the two passes
     int keys_qk, keys_pv;   // keys per workgroup of the two passes
     float scale;
@@ -94,6 +95,17 @@ bool head_dim_supported(int d);
 // pass 2 takes 8 waves (256 keys) only where their V tiles fit the LDS (D <=
 // 256) and the waves split the D/16 dimension blocks evenly or take whole ones.
 inline bool decode_loop_ok(int d) { return d <= 256; }
+
+// The decode kernels take the g query heads of a KV head in `sub` equal groups
+// of at most kDecodeMaxGroup; each group streams the KV head's cache, so up to
+// 4 of them (a larger g, or one without such a divisor, runs on the causal
+// kernel). Returns sub, or 0.
+inline int decode_groups(int g)
+{
+    for (int sub = 1; sub <= 4; sub++)
+        if (g % sub == 0 && g / sub <= kDecodeMaxGroup) return sub;
+    return 0;
+}
 inline bool decode_wide_ok(int d) { return d <= 256 && (d / 16 >= 8 || 8 % (d / 16) == 0); }
 hipError_t launch_layer_prep(const LayerPrepArgs &a, hipStream_t s);
 hipError_t launch_norm_rope(const NormRopeArgs &a, hipStream_t s);

@@ -290,9 +290,9 @@ static bool scale_is_pow2(float s)
 template <int D>
 static hipError_t decode_d(const DecodeArgs &a, int kv_heads, hipStream_t s)
 {
-    if (a.keys_qk > 4 * kKeyTile) hipLaunchKernelGGL((decode_qk<D, true>), dim3(a.nwg_qk, kv_heads), dim3(256), 0, s, a);
-    else hipLaunchKernelGGL((decode_qk<D, false>), dim3(a.nwg_qk, kv_heads), dim3(256), 0, s, a);
-    const dim3 gpv(a.nwg_pv, kv_heads);
+    const dim3 gqk(a.nwg_qk, kv_heads, a.sub), gpv(a.nwg_pv, kv_heads, a.sub);
+    if (a.keys_qk > 4 * kKeyTile) hipLaunchKernelGGL((decode_qk<D, true>), gqk, dim3(256), 0, s, a);
+    else hipLaunchKernelGGL((decode_qk<D, false>), gqk, dim3(256), 0, s, a);
     if (a.g <= 8) {
         if (a.keys_pv == 4 * kKeyTile) hipLaunchKernelGGL((decode_pv<D, 4, 1>), gpv, dim3(256), 0, s, a);
         else hipLaunchKernelGGL((decode_pv<D, 8, 1>), gpv, dim3(512), 0, s, a);
@@ -300,7 +300,7 @@ static hipError_t decode_d(const DecodeArgs &a, int kv_heads, hipStream_t s)
         if (a.keys_pv == 4 * kKeyTile) hipLaunchKernelGGL((decode_pv<D, 4, 2>), gpv, dim3(256), 0, s, a);
         else hipLaunchKernelGGL((decode_pv<D, 8, 2>), gpv, dim3(512), 0, s, a);
     }
-    hipLaunchKernelGGL(decode_combine<D>, dim3(kv_heads * a.g, (D + 63) / 64), dim3(64 * kCombineSubs), 0, s, a);
+    hipLaunchKernelGGL(decode_combine<D>, dim3(kv_heads * a.sub * a.g, (D + 63) / 64), dim3(64 * kCombineSubs), 0, s, a);
     return hipGetLastError();
 }
 

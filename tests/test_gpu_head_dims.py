@@ -40,7 +40,8 @@ CASES += [
     ("decode_d96_loop_n40001", 16, 2, 96, 1, 40000),              # pass 1 loops; 4-wave pass 2 only
     ("decode_d160_loop_n40001", 16, 2, 160, 1, 40000),
     ("decode_d384_n40001", 16, 2, 384, 1, 40000),                 # one tile per wave past 256
-    ("decode_d96_g32_through_prefill", 32, 1, 96, 1, 500),
+    ("decode_d96_g32_two_groups", 32, 1, 96, 1, 500),
+    ("decode_d96_g80_through_prefill", 80, 1, 96, 1, 500),
     ("prefill_d448_r300_p0_g1", 4, 4, 448, 300, 0),
     ("prefill_d160_r257_p1000", 8, 1, 160, 257, 1000),
 ]

@@ -104,7 +104,8 @@ CASES = [
     ("decode_ungated_d128_g4", 8, 2, 128, 1, 300, 400, False, 128),
     ("prefill_ragged_d64_g2", 8, 4, 64, 70, 33, 200, True, 32),
     ("decode_g16_no_rope", 16, 1, 256, 1, 5000, 5100, True, 0),
-    ("decode_g32_through_prefill", 32, 1, 128, 1, 700, 800, True, 64),
+    ("decode_g32_two_groups", 32, 1, 128, 1, 700, 800, True, 64),
+    ("decode_g17_through_prefill", 17, 1, 128, 1, 700, 800, True, 64),
     # k and v 2 bytes off: the decode takes the separate element launch
     ("decode_unaligned_kv", 16, 2, 256, 1, 1000, 1100, True, 64, 1),
     # head dimensions outside 64/128/256: the generic norm path and the other

@@ -64,10 +64,18 @@ def test_configs_full(torch_cuda, name):
 
 
 GROUPS = [
-    # GQA groups beyond the decode kernels' limit take the causal kernel for rows == 1
+    # more than 16 query heads per KV head: the decode kernels take them in 2, 3
+    # or 4 equal groups; beyond that (or with no such divisor) the causal kernel
+    # serves the row
     ("decode_g32_d128", 32, 1, 128, 1, 500),
     ("decode_g16_d256", 32, 2, 256, 1, 999),
     ("decode_g12_d256", 12, 1, 256, 1, 40),
+    ("decode_g48_d128_three_groups", 48, 1, 128, 1, 3000),
+    ("decode_g64_d64_four_groups", 128, 2, 64, 1, 20000),
+    ("decode_g24_d256_two_groups_8_wave", 48, 2, 256, 1, 33000),
+    ("decode_g20_d256_loop", 40, 2, 256, 1, 70000),
+    ("decode_g17_through_prefill", 17, 1, 128, 1, 900),
+    ("decode_g80_through_prefill", 80, 1, 64, 1, 300),
 ]
 
 
