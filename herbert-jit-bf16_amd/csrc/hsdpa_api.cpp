@@ -19,7 +19,10 @@ struct hsdpa_plan {
     uint64_t dec_npad;        // scores row length for a full cache
     uint64_t dec_nwg;         // workgroups per KV head for a full cache
     uint64_t off_scores, off_wgmax, off_part_o, off_part_l, dec_bytes;
-    uint64_t ws_bytes;       // prefill needs no workspace
+    // split causal workspace (floats), after the decode's: partial row maxima,
+    // outputs and sums of kSplitUnits (split, 32-row group, head) cells
+    uint64_t off_smax, off_so, off_sl;
+    uint64_t ws_bytes;
 };
 
 namespace {
@@ -280,7 +283,14 @@ hsdpa_status hsdpa_plan_create(const hsdpa_spec *spec, hsdpa_plan **out)
     p->off_part_l = off;
     off = align_up(off + kvh * p->dec_nwg * g * 4, kAlign);
     p->dec_bytes = off;
-    p->ws_bytes = p->dec_bytes;
+    const uint64_t cells = static_cast<uint64_t>(hsdpa::kSplitUnits) * 32;
+    p->off_smax = off;
+    off = align_up(off + cells * 4, kAlign);
+    p->off_so = off;
+    off = align_up(off + cells * d * 4, kAlign);
+    p->off_sl = off;
+    off = align_up(off + cells * 4, kAlign);
+    p->ws_bytes = off;
     *out = p;
     return HSDPA_OK;
 }
@@ -358,7 +368,13 @@ static hsdpa_status run_attention(const hsdpa_plan *plan, const hsdpa_call *call
     a.scale = call->scale;
     a.gate = gate;
     a.gate_row = gate_row;
-    const hipError_t e = hsdpa::launch_prefill(a, d, static_cast<int>(s.heads), st);
+    hsdpa::PrefillSplit ps{};
+    ps.smax = reinterpret_cast<float *>(ws + plan->off_smax);
+    ps.so = reinterpret_cast<float *>(ws + plan->off_so);
+    ps.sl = reinterpret_cast<float *>(ws + plan->off_sl);
+    ps.units = hsdpa::kSplitUnits;
+    ps.cus = cus;
+    const hipError_t e = hsdpa::launch_prefill(a, d, static_cast<int>(s.heads), ps, st);
     return e == hipSuccess ? HSDPA_OK : HSDPA_ERR_HIP;
 }
 

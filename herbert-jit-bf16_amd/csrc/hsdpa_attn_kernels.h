@@ -913,4 +913,254 @@ __global__ __launch_bounds__(64 * NW, 1) void prefill_attn(PrefillArgs a)
     }
 }
 
+// ---------------------------------------------------------------------------
+// Causal prefill split over the keys, for chunks whose grid of (row group,
+// head group) workgroups leaves compute units idle (a short chunk after a long
+// cache): gridDim.z workgroups share a row group's key tiles, tile range
+// [z per, (z + 1) per) of its ntiles, per = ceil(ntiles / gridDim.z).
+//   prefill_split_max     pass 1 over the range: partial row maxima
+//                         smax[z][head][row] (-inf where the range holds no
+//                         visible key)
+//   prefill_split_pv      the exact row maximum (the largest partial: max is
+//                         exact in any order, so the exponentials are those of
+//                         the one-workgroup kernel), then pass 2 over the range:
+//                         unnormalised so[z][row][head][D] and sl[z][row][head]
+//   prefill_split_combine out = bf16(sum_z O / sum_z l), z ascending (+ gate)
+// Same waves, tiles and numerics as prefill_attn.
+// ---------------------------------------------------------------------------
+struct SplitArgs {
+    float *smax;            // [splits][heads][rows]
+    float *so;              // [splits][rows][heads][D]
+    float *sl;              // [splits][rows][heads]
+    int heads;
+};
+
+template <int D, int HPW, bool POW2, int NW>
+__global__ __launch_bounds__(64 * NW, 1) void prefill_split_max(PrefillArgs a, SplitArgs sp)
+{
+    constexpr int RB = NW / HPW, THREADS = 64 * NW;
+    constexpr int SK = Pad<D>::K;
+    __shared__ __attribute__((aligned(16))) uint16_t kb[2][kKeyTile * SK];
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6, l = tid & 63, col = l & 31, grp = l >> 5;
+    const int head = blockIdx.y * HPW + (wave % HPW);
+    const int kvh = head / a.gqa;
+    const uint64_t rgroup = gridDim.x - 1 - blockIdx.x;
+    const uint64_t wg_r0 = rgroup * (32 * RB);
+    const uint64_t w_r0 = wg_r0 + 32 * (wave / HPW);
+    const uint64_t row = w_r0 + col;
+    const bool rowv = row < a.rows;
+    const bool wact = w_r0 < a.rows;
+    const uint64_t wg_rend = wg_r0 + 32 * RB < a.rows ? wg_r0 + 32 * RB : a.rows;
+    const int ntiles = static_cast<int>((a.past + wg_rend + kKeyTile - 1) / kKeyTile);
+    const int nfull = wact ? static_cast<int>((a.past + w_r0 + 1) / kKeyTile) : 0;
+    const uint64_t lim = a.past + row;
+    const int per = (ntiles + static_cast<int>(gridDim.z) - 1) / static_cast<int>(gridDim.z);
+    const int tb = static_cast<int>(blockIdx.z) * per < ntiles ? static_cast<int>(blockIdx.z) * per : ntiles;
+    const int te = tb + per < ntiles ? tb + per : ntiles;
+
+    const uint16_t *kg = a.k + static_cast<uint64_t>(kvh) * a.kv_stride;
+    u32x4 kr[Tile<D, THREADS>::kPer];
+    u32x4 qb[D / 16];
+    const uint16_t *qp = a.q + (rowv ? row : 0) * a.q_row + static_cast<uint64_t>(head) * a.q_head;
+#pragma unroll
+    for (int s = 0; s < D / 16; s++) {
+        const u32x4 v = load16(qp + 16 * s + 8 * grp);
+        qb[s] = rowv ? v : u32x4{0, 0, 0, 0};
+    }
+    const int arow = swap23(col) * SK + 8 * grp;
+    float m = kNegInf;
+    if (tb < te) {
+        tile_gload<D, THREADS>(kg, static_cast<uint64_t>(tb) * kKeyTile, a.n, tid, kr);
+        tile_lstore_padded<D, THREADS>(kb[0], SK, tid, kr);
+        __syncthreads();
+        for (int t = tb; t < te; t++) {
+            const uint64_t t0 = static_cast<uint64_t>(t) * kKeyTile;
+            const bool last = t + 1 == te;
+            if (!last) tile_gload<D, THREADS>(kg, t0 + kKeyTile, a.n, tid, kr);
+            __builtin_amdgcn_sched_barrier(0);
+            const uint16_t *kt = kb[(t - tb) & 1];
+            f32x16 acc = {};
+#pragma unroll
+            for (int s = 0; s < D / 16; s++) acc = mfma(load16(kt + arow + 16 * s), qb[s], acc);
+            if (t < nfull) {
+#pragma unroll
+                for (int r = 0; r < 16; r++) m = __builtin_fmaxf(m, POW2 ? acc[r] : acc[r] * a.scale);
+            } else {
+                const int vis = static_cast<int>(static_cast<int64_t>(lim) - static_cast<int64_t>(t0));
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const float s = POW2 ? acc[r] : acc[r] * a.scale;
+                    if (key_of(r, grp) <= vis) m = __builtin_fmaxf(m, s);
+                }
+            }
+            if (!last) tile_lstore_padded<D, THREADS>(kb[(t - tb + 1) & 1], SK, tid, kr);
+            __syncthreads();
+        }
+    }
+    m = __builtin_fmaxf(m, __shfl_xor(m, 32));
+    if (rowv && grp == 0) sp.smax[(static_cast<uint64_t>(blockIdx.z) * sp.heads + head) * a.rows + row] = m;
+}
+
+template <int D, int HPW, bool POW2, int NW>
+__global__ __launch_bounds__(64 * NW, 1) void prefill_split_pv(PrefillArgs a, SplitArgs sp)
+{
+    constexpr int RB = NW / HPW, THREADS = 64 * NW;
+    constexpr int SK = Pad<D>::K, SV = Pad<D>::V;
+    __shared__ __attribute__((aligned(16))) uint16_t kb[2][kKeyTile * SK];
+    __shared__ __attribute__((aligned(16))) uint16_t vb[2][kKeyTile * SV];
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6, l = tid & 63, col = l & 31, grp = l >> 5;
+    const int head = blockIdx.y * HPW + (wave % HPW);
+    const int kvh = head / a.gqa;
+    const uint64_t rgroup = gridDim.x - 1 - blockIdx.x;
+    const uint64_t wg_r0 = rgroup * (32 * RB);
+    const uint64_t w_r0 = wg_r0 + 32 * (wave / HPW);
+    const uint64_t row = w_r0 + col;
+    const bool rowv = row < a.rows;
+    const bool wact = w_r0 < a.rows;
+    const uint64_t wg_rend = wg_r0 + 32 * RB < a.rows ? wg_r0 + 32 * RB : a.rows;
+    const int ntiles = static_cast<int>((a.past + wg_rend + kKeyTile - 1) / kKeyTile);
+    const int nfull = wact ? static_cast<int>((a.past + w_r0 + 1) / kKeyTile) : 0;
+    const uint64_t lim = a.past + row;
+    const int nz = static_cast<int>(gridDim.z);
+    const int per = (ntiles + nz - 1) / nz;
+    const int tb = static_cast<int>(blockIdx.z) * per < ntiles ? static_cast<int>(blockIdx.z) * per : ntiles;
+    const int te = tb + per < ntiles ? tb + per : ntiles;
+
+    // the exact row maximum: the largest of the splits' partial maxima (rows
+    // past the chunk take 0: computed, never stored)
+    float m = rowv ? kNegInf : 0.0f;
+    if (rowv)
+        for (int z = 0; z < nz; z++) m = __builtin_fmaxf(m, sp.smax[(static_cast<uint64_t>(z) * sp.heads + head) * a.rows + row]);
+    ExpArgs ex;
+    ex.m = m;
+    ex.scale = a.scale;
+    ex.clamp = POW2 ? -87.33654f / a.scale : -87.33654f;
+    ex.mul = POW2 ? 1.442695f * a.scale : 1.442695f;
+
+    const uint16_t *kg = a.k + static_cast<uint64_t>(kvh) * a.kv_stride;
+    const uint16_t *vg = a.v + static_cast<uint64_t>(kvh) * a.kv_stride;
+    u32x4 kr[Tile<D, THREADS>::kPer], vr[Tile<D, THREADS>::kPer];
+    u32x4 qb[D / 16];
+    const uint16_t *qp = a.q + (rowv ? row : 0) * a.q_row + static_cast<uint64_t>(head) * a.q_head;
+#pragma unroll
+    for (int s = 0; s < D / 16; s++) {
+        const u32x4 v = load16(qp + 16 * s + 8 * grp);
+        qb[s] = rowv ? v : u32x4{0, 0, 0, 0};
+    }
+    const int arow = swap23(col) * SK + 8 * grp;
+    f32x16 o[D / 32];
+#pragma unroll
+    for (int dt = 0; dt < D / 32; dt++) o[dt] = f32x16{};
+    float lsum = 0.0f;
+    if (tb < te) {
+        tile_gload<D, THREADS>(kg, static_cast<uint64_t>(tb) * kKeyTile, a.n, tid, kr);
+        tile_gload<D, THREADS>(vg, static_cast<uint64_t>(tb) * kKeyTile, a.n, tid, vr);
+        tile_lstore_padded<D, THREADS>(kb[0], SK, tid, kr);
+        tile_mask<D, THREADS>(static_cast<uint64_t>(tb) * kKeyTile, a.n, tid, vr);
+        tile_lstore_padded<D, THREADS>(vb[0], SV, tid, vr);
+        __syncthreads();
+        for (int t = tb; t < te; t++) {
+            const uint64_t t0 = static_cast<uint64_t>(t) * kKeyTile;
+            const int b = (t - tb) & 1;
+            const bool last = t + 1 == te;
+            if (!last) tile_gload<D, THREADS>(kg, t0 + kKeyTile, a.n, tid, kr);
+            __builtin_amdgcn_sched_barrier(0);
+            f32x16 acc = {};
+#pragma unroll
+            for (int s = 0; s < D / 16; s++) acc = mfma(load16(kb[b] + arow + 16 * s), qb[s], acc);
+            const bool full = t < nfull;
+            const int vis = static_cast<int>(static_cast<int64_t>(lim) - static_cast<int64_t>(t0));
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                float ev[8];
+#pragma unroll
+                for (int r = 0; r < 8; r++) {
+                    const float e = exp_score<POW2>(acc[8 * h + r], ex);
+                    ev[r] = full || key_of(8 * h + r, grp) <= vis ? e : 0.0f;
+                    lsum += ev[r];
+                }
+                u32x4 hi, lo;
+                split_pack_hw(ev, hi, lo);
+                if (h == 0 && !last) tile_gload<D, THREADS>(vg, t0 + kKeyTile, a.n, tid, vr);
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int dt = 0; dt < D / 32; dt++) {
+                    const u32x4 av = vt_operand_padded<D>(vb[b], 16 * h, 32 * dt, l);
+                    o[dt] = mfma(av, hi, o[dt]);
+                    o[dt] = mfma(av, lo, o[dt]);
+                }
+            }
+            if (!last) {
+                tile_lstore_padded<D, THREADS>(kb[b ^ 1], SK, tid, kr);
+                tile_mask<D, THREADS>(t0 + kKeyTile, a.n, tid, vr);
+                tile_lstore_padded<D, THREADS>(vb[b ^ 1], SV, tid, vr);
+            }
+            __syncthreads();
+        }
+    }
+    lsum += __shfl_xor(lsum, 32);
+    if (rowv) {
+        const uint64_t cell = (static_cast<uint64_t>(blockIdx.z) * a.rows + row) * sp.heads + head;
+        float *op = sp.so + cell * D;
+#pragma unroll
+        for (int dt = 0; dt < D / 32; dt++)
+#pragma unroll
+            for (int c = 0; c < 4; c++)
+                *reinterpret_cast<f32x4 *>(op + 32 * dt + 8 * c + 4 * grp) =
+                    f32x4{o[dt][4 * c], o[dt][4 * c + 1], o[dt][4 * c + 2], o[dt][4 * c + 3]};
+        if (grp == 0) sp.sl[cell] = lsum;
+    }
+}
+
+// grid (rows, heads), D threads: one output element each.
+template <int D>
+__global__ __launch_bounds__(D) void prefill_split_combine(PrefillArgs a, SplitArgs sp, int splits);
+
+// A positive power of two in [2^-20, 2^20]: scaling by it is exact for the
+// scores and for the folded exponential constants.
+static bool scale_is_pow2(float s)
+{
+    const uint32_t b = __builtin_bit_cast(uint32_t, s);
+    const uint32_t e = (b >> 23) & 0xFF;
+    return (b & 0x807FFFFFu) == 0 && e >= 127 - 20 && e <= 127 + 20;
+}
+
+// The three split kernels on grid (row groups, head groups, splits). POW2:
+// whether a power-of-two scale takes the folded form (the general form rounds
+// identically).
+template <int D, int HPW, int NW, bool POW2_FORM = true>
+static void launch_prefill_split(const PrefillArgs &a, int heads, const PrefillSplit &ps, dim3 grid, int splits,
+                                 hipStream_t s)
+{
+    const SplitArgs sp{ps.smax, ps.so, ps.sl, heads};
+    const dim3 gs(grid.x, grid.y, static_cast<unsigned>(splits));
+    if (POW2_FORM && scale_is_pow2(a.scale)) {
+        hipLaunchKernelGGL((prefill_split_max<D, HPW, POW2_FORM, NW>), gs, dim3(64 * NW), 0, s, a, sp);
+        hipLaunchKernelGGL((prefill_split_pv<D, HPW, POW2_FORM, NW>), gs, dim3(64 * NW), 0, s, a, sp);
+    } else {
+        hipLaunchKernelGGL((prefill_split_max<D, HPW, false, NW>), gs, dim3(64 * NW), 0, s, a, sp);
+        hipLaunchKernelGGL((prefill_split_pv<D, HPW, false, NW>), gs, dim3(64 * NW), 0, s, a, sp);
+    }
+    hipLaunchKernelGGL(prefill_split_combine<D>, dim3(static_cast<unsigned>(a.rows), heads), dim3(D), 0, s, a, sp,
+                       splits);
+}
+
+template <int D>
+__global__ __launch_bounds__(D) void prefill_split_combine(PrefillArgs a, SplitArgs sp, int splits)
+{
+    const uint64_t row = blockIdx.x, head = blockIdx.y;
+    const int dim = threadIdx.x;
+    float o = 0.0f, ls = 0.0f;
+    for (int z = 0; z < splits; z++) {
+        const uint64_t cell = (static_cast<uint64_t>(z) * a.rows + row) * sp.heads + head;
+        o += sp.so[cell * D + dim];
+        ls += sp.sl[cell];
+    }
+    uint16_t ob = static_cast<uint16_t>(cvt_out(o / ls));
+    if (a.gate) ob = gate_bf16(ob, a.gate[row * a.gate_row + head * D + dim]);
+    a.out[row * a.out_row + head * D + dim] = ob;
+}
+
 }  // namespace hsdpa

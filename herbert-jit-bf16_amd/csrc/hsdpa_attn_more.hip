@@ -44,12 +44,14 @@ static hipError_t decode_more_d(const DecodeArgs &a, int kv_heads, hipStream_t s
 }
 
 template <int D>
-static hipError_t prefill_more_d(const PrefillArgs &a, int heads, hipStream_t s)
+static hipError_t prefill_more_d(const PrefillArgs &a, int heads, const PrefillSplit &ps, hipStream_t s)
 {
     constexpr int NW = D > 256 ? 4 : 8;
     constexpr int ROWS = 32 * NW;                                // HPW = 1: NW row blocks of one head
     const dim3 grid(static_cast<unsigned>((a.rows + ROWS - 1) / ROWS), heads);
-    hipLaunchKernelGGL((prefill_attn<D, 1, false, NW>), grid, dim3(64 * NW), 0, s, a);
+    const int splits = prefill_splits(a, static_cast<uint64_t>(grid.x) * grid.y, heads, ps);
+    if (splits > 1) launch_prefill_split<D, 1, NW, false>(a, heads, ps, grid, splits, s);
+    else hipLaunchKernelGGL((prefill_attn<D, 1, false, NW>), grid, dim3(64 * NW), 0, s, a);
     return hipGetLastError();
 }
 
@@ -67,11 +69,11 @@ hipError_t launch_decode_more(const DecodeArgs &a, int head_dim, int kv_heads, h
     }
 }
 
-hipError_t launch_prefill_more(const PrefillArgs &a, int head_dim, int heads, hipStream_t s)
+hipError_t launch_prefill_more(const PrefillArgs &a, int head_dim, int heads, const PrefillSplit &ps, hipStream_t s)
 {
     switch (head_dim) {
 #define HSDPA_CASE(D) \
-    case D: return prefill_more_d<D>(a, heads, s);
+    case D: return prefill_more_d<D>(a, heads, ps, s);
         HSDPA_MORE_DIMS(HSDPA_CASE)
 #undef HSDPA_CASE
     default: return hipErrorInvalidValue;

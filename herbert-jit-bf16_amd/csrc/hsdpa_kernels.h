@@ -43,11 +43,22 @@ struct PrefillArgs {
     uint64_t gate_row;
 };
 
+// The split form of the causal kernel (see prefill_split_max): workspace for
+// its partial maxima, outputs and sums, and what the launcher needs to choose
+// the number of splits. units: the most (split, 32-row group, head) cells the
+// workspace holds. No split when `so` is null.
+struct PrefillSplit {
+    float *smax, *so, *sl;
+    uint64_t units;
+    int cus;
+};
+
 // Constants of the kernels the host needs to size grids and workspaces.
 constexpr int kKeyTile = 32;          // keys per MFMA key block
 constexpr int kDecodeKeysQK = 128;    // keys per decode pass-1 workgroup (4 waves x 1 tile)
 constexpr int kDecodeKeysPV = 256;    // keys per decode pass-2 workgroup (8 waves x 1 tile; 4 x 1 on short caches)
 constexpr int kDecodeMaxGroup = 16;   // query heads per KV head the decode kernels take
+constexpr int kSplitUnits = 2048;     // (split, 32-row group, head) cells of the split prefill's workspace
 
 // KV append: token-major block rows into the head-major cache.
 struct KvAppendArgs {
@@ -112,9 +123,25 @@ hipError_t launch_norm_rope(const NormRopeArgs &a, hipStream_t s);
 hipError_t launch_gate(const GateArgs &a, hipStream_t s);
 hipError_t launch_kv_append(const KvAppendArgs &a, bool vec, hipStream_t s);
 hipError_t launch_decode(const DecodeArgs &a, int head_dim, int kv_heads, hipStream_t s);
-hipError_t launch_prefill(const PrefillArgs &a, int head_dim, int heads, hipStream_t s);
+hipError_t launch_prefill(const PrefillArgs &a, int head_dim, int heads, const PrefillSplit &ps, hipStream_t s);
 // the head dimensions other than 64, 128 and 256 (hsdpa_attn_more.hip)
 hipError_t launch_decode_more(const DecodeArgs &a, int head_dim, int kv_heads, hipStream_t s);
-hipError_t launch_prefill_more(const PrefillArgs &a, int head_dim, int heads, hipStream_t s);
+hipError_t launch_prefill_more(const PrefillArgs &a, int head_dim, int heads, const PrefillSplit &ps, hipStream_t s);
+
+// Splits for a causal call whose one-workgroup grid has `wgs` workgroups: enough
+// to fill the compute units once, at least 4 tiles of the longest row group
+// each, within the workspace; 1 when the grid fills half the units already or
+// the rows see fewer than 8 tiles.
+inline int prefill_splits(const PrefillArgs &a, uint64_t wgs, int heads, const PrefillSplit &ps)
+{
+    if (!ps.so || ps.cus <= 0 || wgs * 2 > static_cast<uint64_t>(ps.cus)) return 1;
+    const uint64_t ntiles = (a.past + a.rows + kKeyTile - 1) / kKeyTile;
+    if (ntiles < 8) return 1;
+    uint64_t s = static_cast<uint64_t>(ps.cus) / wgs;
+    if (s > ntiles / 4) s = ntiles / 4;
+    const uint64_t cells = (a.rows + 31) / 32 * static_cast<uint64_t>(heads);
+    if (s > ps.units / cells) s = ps.units / cells;
+    return s >= 2 ? static_cast<int>(s) : 1;
+}
 
 }  // namespace hsdpa

@@ -278,14 +278,6 @@ __global__ __launch_bounds__(256) void output_gate(GateArgs a)
 // ---------------------------------------------------------------------------
 bool head_dim_supported(int d) { return d >= 32 && d <= 512 && d % 32 == 0; }
 
-// A positive power of two in [2^-20, 2^20]: scaling by it is exact for the
-// scores and for the folded exponential constants.
-static bool scale_is_pow2(float s)
-{
-    const uint32_t b = __builtin_bit_cast(uint32_t, s);
-    const uint32_t e = (b >> 23) & 0xFF;
-    return (b & 0x807FFFFFu) == 0 && e >= 127 - 20 && e <= 127 + 20;
-}
 
 template <int D>
 static hipError_t decode_d(const DecodeArgs &a, int kv_heads, hipStream_t s)
@@ -315,21 +307,26 @@ hipError_t launch_decode(const DecodeArgs &a, int head_dim, int kv_heads, hipStr
 }
 
 template <int D, int HPW>
-static void prefill_dh(const PrefillArgs &a, int heads, hipStream_t s)
+static void prefill_dh(const PrefillArgs &a, int heads, const PrefillSplit &ps, hipStream_t s)
 {
     const int rows_per_wg = 32 * (8 / HPW);
     const dim3 grid(static_cast<unsigned>((a.rows + rows_per_wg - 1) / rows_per_wg), heads / HPW);
+    const int splits = prefill_splits(a, static_cast<uint64_t>(grid.x) * grid.y, heads, ps);
+    if (splits > 1) {
+        launch_prefill_split<D, HPW, 8>(a, heads, ps, grid, splits, s);
+        return;
+    }
     if (scale_is_pow2(a.scale)) hipLaunchKernelGGL((prefill_attn<D, HPW, true>), grid, dim3(512), 0, s, a);
     else hipLaunchKernelGGL((prefill_attn<D, HPW, false>), grid, dim3(512), 0, s, a);
 }
 
 template <int D>
-static void prefill_d(const PrefillArgs &a, int heads, hipStream_t s)
+static void prefill_d(const PrefillArgs &a, int heads, const PrefillSplit &ps, hipStream_t s)
 {
-    if (a.gqa % 8 == 0) prefill_dh<D, 8>(a, heads, s);
-    else if (a.gqa % 4 == 0) prefill_dh<D, 4>(a, heads, s);
-    else if (a.gqa % 2 == 0) prefill_dh<D, 2>(a, heads, s);
-    else prefill_dh<D, 1>(a, heads, s);
+    if (a.gqa % 8 == 0) prefill_dh<D, 8>(a, heads, ps, s);
+    else if (a.gqa % 4 == 0) prefill_dh<D, 4>(a, heads, ps, s);
+    else if (a.gqa % 2 == 0) prefill_dh<D, 2>(a, heads, ps, s);
+    else prefill_dh<D, 1>(a, heads, ps, s);
 }
 
 hipError_t launch_kv_append(const KvAppendArgs &a, bool vec, hipStream_t s)
@@ -363,13 +360,13 @@ hipError_t launch_gate(const GateArgs &a, hipStream_t s)
     return hipGetLastError();
 }
 
-hipError_t launch_prefill(const PrefillArgs &a, int head_dim, int heads, hipStream_t s)
+hipError_t launch_prefill(const PrefillArgs &a, int head_dim, int heads, const PrefillSplit &ps, hipStream_t s)
 {
     switch (head_dim) {
-    case 64: prefill_d<64>(a, heads, s); break;
-    case 128: prefill_d<128>(a, heads, s); break;
-    case 256: prefill_d<256>(a, heads, s); break;
-    default: return launch_prefill_more(a, head_dim, heads, s);
+    case 64: prefill_d<64>(a, heads, ps, s); break;
+    case 128: prefill_d<128>(a, heads, ps, s); break;
+    case 256: prefill_d<256>(a, heads, ps, s); break;
+    default: return launch_prefill_more(a, head_dim, heads, ps, s);
     }
     return hipGetLastError();
 }

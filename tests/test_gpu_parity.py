@@ -25,6 +25,14 @@ SMALL = [
     # pass 1 in several rounds per workgroup, the last workgroup partial
     ("decode_d256_n50001_two_rounds", 16, 2, 256, 1, 50000),
     ("decode_d128_n70001_five_rounds", 16, 4, 128, 1, 70000),
+    # short chunks after long caches: the causal kernel split over the keys
+    ("prefill_split_d256_r64_p3000", 16, 2, 256, 64, 3000),
+    ("prefill_split_d256_r300_p9000", 16, 2, 256, 300, 9000),
+    ("prefill_split_d128_r100_p5000_g4", 16, 4, 128, 100, 5000),
+    ("prefill_split_d64_r40_p2000_g2", 8, 4, 64, 40, 2000),
+    ("prefill_split_d96_r50_p4000", 8, 2, 96, 50, 4000),
+    ("prefill_split_d384_r33_p2500", 4, 2, 384, 33, 2500),
+    ("prefill_split_d256_r7_p257_uneven", 8, 2, 256, 7, 257),
 ]
 
 
@@ -76,6 +84,7 @@ GROUPS = [
     ("decode_g20_d256_loop", 40, 2, 256, 1, 70000),
     ("decode_g17_through_prefill", 17, 1, 128, 1, 900),
     ("decode_g80_through_prefill", 80, 1, 64, 1, 300),
+    ("decode_g80_through_split_prefill", 80, 1, 64, 1, 6000),
 ]
 
 
