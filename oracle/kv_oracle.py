@@ -1,8 +1,8 @@
 """CPU restatement of the reference's KV append and snapshot copies — TEST
 INFRASTRUCTURE ONLY.
 
-Only tests/ use it, as the checker of hsdpa_kv_append, hsdpa_kv_take and
-hsdpa_kv_restore; the product path never does. The snapshot copies
+Only tests/ use it: the oracle that hsdpa_kv_append, hsdpa_kv_take and
+hsdpa_kv_restore are compared with; the product path never does. The snapshot copies
 (snapshot_take / restore_from, below) restate model.rs:732-857 and are pinned
 by the tests against a hand-placed known-answer cache and by take-then-restore
 identity. It restates src/jit/target/x86/execution/kv.rs:15-69: one task per KV
