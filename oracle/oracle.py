@@ -1,7 +1,7 @@
 """ctypes wrapper of liboracle_sdpa.so — TEST INFRASTRUCTURE ONLY.
 
-The oracle is the parity checker (a CPU restatement of the reference's
-emitted SDPA, see sdpa_oracle.h). Only tests/, the smoke check and the
+The oracle is what the parity tests compare the GPU with (a CPU restatement
+of the reference's emitted SDPA, see sdpa_oracle.h). Only tests/, the smoke check and the
 CPU-baseline leg of bench.py load it; the product path never does.
 """
 from __future__ import annotations

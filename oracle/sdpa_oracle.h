@@ -1,7 +1,7 @@
 /*
  * sdpa_oracle.h — TEST INFRASTRUCTURE ONLY.
  *
- * The oracle is the parity checker for the HIP attention kernels: a CPU
+ * The oracle is what the HIP attention kernels are compared with: a CPU
  * restatement of the attention (SDPA) step that xigh/herbert-jit-bf16 emits at
  * run time as x86 AVX-512 BF16 machine code. Only tests/, the smoke check and
  * the CPU-baseline leg of bench.py may load it; the product library

@@ -1,5 +1,5 @@
 """CPU tests that pin the oracle (the CPU restatement of the reference's
-emitted SDPA) before it is trusted as the parity checker.
+emitted SDPA) before the parity tests compare the GPU with it.
 
 What pins what:
   * bf16 conversions   : closed forms over all 65 536 bf16 values, and an
