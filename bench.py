@@ -42,8 +42,8 @@ MFMA_BF16_PEAK_TFS = 2500.0  # MI355X dense bf16 MFMA, TFLOP/s
 # every L2 fill from the memory fabric, so Infinity Cache hits are included.
 # Summary and commands: profiles/pmc_traffic_decode32k_prefill4096.md
 TRAFFIC_BYTES = {
-    "decode_32k": (2 * (16451.5 + 17545.4 + 1091.5) + (2176.4 + 2056.0 + 8.0)) * 1024,
-    "prefill_4096_after_8192": (2 * 1204556.0 + 36352.0) * 1024,
+    "decode_32k": (2 * (16451.8 + 17543.4 + 1092.1) + (2176.2 + 2056.0 + 8.0)) * 1024,
+    "prefill_4096_after_8192": (2 * 1201422.1 + 36352.0) * 1024,
 }
 
 
