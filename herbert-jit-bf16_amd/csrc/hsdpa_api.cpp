@@ -332,11 +332,18 @@ static hsdpa_status run_attention(const hsdpa_plan *plan, const hsdpa_call *call
         a.sub = sub;
         const uint64_t groups = plan->kv_heads * static_cast<uint64_t>(sub);
         // pass 1: a tile per wave, or several in turn (the next one in flight)
-        // once one tile per wave would need more than one round of two
-        // workgroups per compute unit; this bounds the maxima pass 2 reads
+        // once one tile per wave would need more than one workgroup per
+        // compute unit: at least two, and as many as one round of two
+        // workgroups per compute unit needs; this bounds the maxima pass 2
+        // reads. Two tiles per wave from one workgroup per compute unit on
+        // measured 0.3-0.5 us faster than one tile per wave between 20K and
+        // 32K keys at 2 KV heads, and the same elsewhere.
         const uint64_t nqk1 = (n + hsdpa::kDecodeKeysQK - 1) / hsdpa::kDecodeKeysQK;
-        const uint64_t slots = 2 * static_cast<uint64_t>(cus > 0 ? cus : 1);
-        const uint64_t rq = hsdpa::decode_loop_ok(d) ? (groups * nqk1 + slots - 1) / slots : 1;
+        const uint64_t cu1 = static_cast<uint64_t>(cus > 0 ? cus : 1);
+        const uint64_t rounds = (groups * nqk1 + 2 * cu1 - 1) / (2 * cu1);
+        const uint64_t rq = !hsdpa::decode_loop_ok(d) ? 1
+                            : groups * nqk1 > cu1 && rounds < 2 ? 2
+                                                                 : rounds;
         a.keys_qk = hsdpa::kDecodeKeysQK * static_cast<int>(rq > 1 ? rq : 1);
         // pass 2 takes 8 tiles per workgroup, or 4 while the smaller
         // workgroups still fit the compute units in one round (short caches:
