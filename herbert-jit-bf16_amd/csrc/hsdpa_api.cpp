@@ -347,11 +347,24 @@ static hsdpa_status run_attention(const hsdpa_plan *plan, const hsdpa_call *call
         a.keys_qk = hsdpa::kDecodeKeysQK * static_cast<int>(rq > 1 ? rq : 1);
         // pass 2 takes 8 tiles per workgroup, or 4 while the smaller
         // workgroups still fit the compute units in one round (short caches:
-        // twice the workgroups, measured faster up to 16K keys at 2 KV heads)
+        // twice the workgroups, measured faster up to 16K keys at 2 KV heads);
+        // past one round of 8-wave workgroups, one round of chunked ones: the
+        // CUs shared among the groups, each workgroup a run of whole tiles
+        // (equal runs stream equal bytes, where rounds of fixed workgroups
+        // leave a partial last round)
         const uint64_t nwg4 = (n + 4 * hsdpa::kKeyTile - 1) / (4 * hsdpa::kKeyTile);
-        a.keys_pv = groups * nwg4 <= static_cast<uint64_t>(cus) || !hsdpa::decode_wide_ok(d)
-                        ? 4 * hsdpa::kKeyTile
-                        : hsdpa::kDecodeKeysPV;
+        const uint64_t ucus = static_cast<uint64_t>(cus > 0 ? cus : 1);
+        const uint64_t nch = (n + hsdpa::kDecodeKeysPV - 1) / hsdpa::kDecodeKeysPV;
+        if (groups * nwg4 <= ucus || !hsdpa::decode_wide_ok(d)) {
+            a.keys_pv = 4 * hsdpa::kKeyTile;
+        } else {
+            const uint64_t per = ucus / groups > 0 ? ucus / groups : 1;
+            const uint64_t tiles = (n + hsdpa::kKeyTile - 1) / hsdpa::kKeyTile;
+            const uint64_t run = hsdpa::kKeyTile * ((tiles + per - 1) / per);
+            a.keys_pv = groups * nch <= ucus || !hsdpa::decode_pv_loop_ok(d, a.g) || run > (1u << 30)
+                            ? hsdpa::kDecodeKeysPV
+                            : static_cast<int>(run);
+        }
         a.nwg_qk = static_cast<int>((n + a.keys_qk - 1) / a.keys_qk);
         a.nwg_pv = static_cast<int>((n + a.keys_pv - 1) / a.keys_pv);
         a.scale = call->scale;

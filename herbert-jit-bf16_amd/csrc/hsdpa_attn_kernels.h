@@ -469,8 +469,13 @@ __global__ __launch_bounds__(256) void decode_qk(DecodeArgs a)
 // ~2 600 bytes of LDS at D = 256, one workgroup per CU; W = 4 half of that, two
 // per CU, so that one workgroup's work after its last load overlaps another's
 // stream when the grid takes several rounds.
+// LOOP: the workgroup covers keys_pv keys (any multiple of 32) in chunks of
+// W tiles, one round of workgroups over the cache instead of several: steps
+// 3-5 per chunk, the next chunk's scores and V tiles loaded as soon as this
+// chunk's V is in LDS (its registers are free then), O accumulated over the
+// chunks in the MFMA registers.
 // ---------------------------------------------------------------------------
-template <int D, int W, int NCB>
+template <int D, int W, int NCB, bool LOOP = false>
 __global__ __launch_bounds__(64 * W, D > 256 ? 1 : 8 / W) void decode_pv(DecodeArgs a)
 {
     constexpr int THREADS = 64 * W;
@@ -493,22 +498,26 @@ __global__ __launch_bounds__(64 * W, D > 256 ? 1 : 8 / W) void decode_pv(DecodeA
     __shared__ __attribute__((aligned(16))) float ored[PARTS > 1 ? (PARTS - 1) * WPP * NCB * DBW * 4 * 64 : 1];
     const int kvh = blockIdx.y * gridDim.z + blockIdx.z, wg = blockIdx.x, tid = threadIdx.x;   // as in decode_qk
     const int wave = tid >> 6, l = tid & 63, j = l & 15, G = l >> 4;
-    const uint64_t j0 = static_cast<uint64_t>(wg) * KEYS;
-    const uint64_t j1 = j0 + KEYS < a.n ? j0 + KEYS : a.n;
+    const uint64_t span = LOOP ? static_cast<uint64_t>(a.keys_pv) : static_cast<uint64_t>(KEYS);
+    const uint64_t j0 = static_cast<uint64_t>(wg) * span;
+    const uint64_t j1 = j0 + span < a.n ? j0 + span : a.n;
     const uint16_t *vbase = a.v + static_cast<uint64_t>(blockIdx.y) * a.kv_stride;
     constexpr int nh = 8 * NCB;                                 // lo columns start here
     // The small loads go first: the vector-memory counter completes in order,
     // so anything issued after the V tile would wait for all of it.
     const int key_e = tid % KEYS;
-    const uint64_t gk_e = j0 + key_e;
-    const bool kv_e = gk_e < j1;
     float sv[kDecodeMaxGroup / 2];
+    // this thread's scores of the chunk starting at key c0
+    auto load_scores = [&](uint64_t c0) {
+        const uint64_t gk = c0 + key_e;
 #pragma unroll
-    for (int i = 0; i < kDecodeMaxGroup / 2; i++) {
-        const int h = tid / KEYS + 2 * i;
-        const int hc = h < a.g ? h : 0;
-        sv[i] = a.scores[static_cast<uint64_t>(kvh * a.g + hc) * a.npad + (kv_e ? gk_e : 0)];
-    }
+        for (int i = 0; i < kDecodeMaxGroup / 2; i++) {
+            const int h = tid / KEYS + 2 * i;
+            const int hc = h < a.g ? h : 0;
+            sv[i] = a.scores[static_cast<uint64_t>(kvh * a.g + hc) * a.npad + (gk < j1 ? gk : 0)];
+        }
+    };
+    load_scores(j0);
     // Pass-1 maxima: T lanes per head (THREADS / 8 for g <= 8, THREADS / 16
     // for g <= 16); lane u reads entries u, u + T, .. of head t / T. The first
     // batch is loaded before the V tile, later batches (more than 8 T
@@ -544,10 +553,15 @@ __global__ __launch_bounds__(64 * W, D > 256 ? 1 : 8 / W) void decode_pv(DecodeA
     if (u == T - 1 && jh < a.g) smax[jh] = m;
     __syncthreads();
 
-    // 3. dense exponentials: thread t owns key j0 + t % KEYS for heads
-    //    t / KEYS, t / KEYS + 2, ...; a wave covers 64 consecutive keys of one
-    //    head set
-    {
+    const int dgi = wave % WPP, part = wave / WPP;
+    f32x4 o[NCB][DBW] = {};
+    // steps 3-5 for the chunk of keys [c0, c1); one chunk unless LOOP
+    for (uint64_t c0 = j0;; c0 += KEYS) {
+        const uint64_t c1 = c0 + KEYS < j1 ? c0 + KEYS : j1;
+        const bool kv_e = c0 + key_e < c1;
+        // 3. dense exponentials: thread t owns key c0 + t % KEYS for heads
+        //    t / KEYS, t / KEYS + 2, ...; a wave covers 64 consecutive keys of
+        //    one head set
 #pragma unroll
         for (int i = 0; i < kDecodeMaxGroup / 2; i++) {
             const int h = tid / KEYS + 2 * i;
@@ -557,38 +571,52 @@ __global__ __launch_bounds__(64 * W, D > 256 ? 1 : 8 / W) void decode_pv(DecodeA
             pc[h * PS + key_e] = static_cast<uint16_t>(hb);
             pc[(nh + h) * PS + key_e] = static_cast<uint16_t>(bf16_rne(e - __uint_as_float(hb << 16)));
             const float sum = wave_sum_hi(e);
-            if (l == 63) lpart[wave][h] = sum;
+            if (l == 63) lpart[wave][h] = (LOOP && c0 != j0 ? lpart[wave][h] : 0.0f) + sum;
         }
-    }
-    // 4. V tile to LDS
-    tile_mask_lstore_v16<D, 64>(vt[wave], j0 + kKeyTile * wave, j1, l, vr);
-    __syncthreads();
+        // 4. V tile to LDS; with LOOP the next chunk's scores and V tiles are
+        //    requested right behind it
+        tile_mask_lstore_v16<D, 64>(vt[wave], c0 + kKeyTile * wave, c1, l, vr);
+        const bool more = LOOP && c1 < j1;
+        if (more) {
+            // the stores above read vr first: the loads below reuse its registers
+            __builtin_amdgcn_sched_barrier(0);
+            load_scores(c0 + KEYS);
+            tile_gload<D, 64>(vbase, c0 + KEYS + kKeyTile * wave, j1, l, vr);
+        }
+        __syncthreads();
 
-    // 5. P.V for this wave's dimension blocks. Columns that hold no head read
-    //    whatever the LDS holds; their outputs are never used. Every operand
-    //    read is issued before the first MFMA: reading each just before its
-    //    MFMA waits out the LDS latency once per MFMA.
-    const int dgi = wave % WPP, part = wave / WPP;
-    u32x4 bp[TPP][NCB], av[TPP][DBW];
+        // 5. P.V for this wave's dimension blocks. Columns that hold no head
+        //    read whatever the LDS holds; their outputs are never used. Every
+        //    operand read is issued before the first MFMA: reading each just
+        //    before its MFMA waits out the LDS latency once per MFMA. With
+        //    LOOP the next chunk's V registers are live here, so the operands
+        //    come in two halves of the tiles.
+        constexpr int PH = LOOP && TPP % 2 == 0 ? 2 : 1, TPH = TPP / PH;
 #pragma unroll
-    for (int tt = 0; tt < TPP; tt++) {
-        const int t = part * TPP + tt;
+        for (int ph = 0; ph < PH; ph++) {
+            u32x4 bp[TPH][NCB], av[TPH][DBW];
 #pragma unroll
-        for (int c = 0; c < NCB; c++) bp[tt][c] = load16(pc + (16 * c + j) * PS + kKeyTile * t + 8 * G);
+            for (int tt = 0; tt < TPH; tt++) {
+                const int t = part * TPP + ph * TPH + tt;
 #pragma unroll
-        for (int db = 0; db < DBW; db++) {
-            const int blk = dgi * DBW + db;
-            av[tt][db] = vt16_operand<D>(vt[t], 16 * (ALL || blk < DB ? blk : 0), l);
+                for (int c = 0; c < NCB; c++) bp[tt][c] = load16(pc + (16 * c + j) * PS + kKeyTile * t + 8 * G);
+#pragma unroll
+                for (int db = 0; db < DBW; db++) {
+                    const int blk = dgi * DBW + db;
+                    av[tt][db] = vt16_operand<D>(vt[t], 16 * (ALL || blk < DB ? blk : 0), l);
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int tt = 0; tt < TPH; tt++)
+#pragma unroll
+                for (int db = 0; db < DBW; db++)
+#pragma unroll
+                    for (int c = 0; c < NCB; c++) o[c][db] = mfma16(av[tt][db], bp[tt][c], o[c][db]);
         }
+        if (!more) break;
+        __syncthreads();                        // pc and vt are rewritten by the next chunk
     }
-    __builtin_amdgcn_sched_barrier(0);
-    f32x4 o[NCB][DBW] = {};
-#pragma unroll
-    for (int tt = 0; tt < TPP; tt++)
-#pragma unroll
-        for (int db = 0; db < DBW; db++)
-#pragma unroll
-            for (int c = 0; c < NCB; c++) o[c][db] = mfma16(av[tt][db], bp[tt][c], o[c][db]);
     if (PARTS > 1) {
         if (part > 0) {
             float *dst = ored + ((part - 1) * WPP + dgi) * (NCB * DBW * 4 * 64);

@@ -118,6 +118,10 @@ inline int decode_groups(int g)
     return 0;
 }
 inline bool decode_wide_ok(int d) { return d <= 256 && (d / 16 >= 8 || 8 % (d / 16) == 0); }
+// Pass 2 in chunks (one round of workgroups over a long cache) is built for
+// the tuned head dimensions, at D = 256 for groups of up to 8 heads (with 16
+// the P columns' operands no longer fit beside the next chunk's V tile).
+inline bool decode_pv_loop_ok(int d, int g) { return d == 64 || d == 128 || (d == 256 && g <= 8); }
 hipError_t launch_layer_prep(const LayerPrepArgs &a, hipStream_t s);
 hipError_t launch_norm_rope(const NormRopeArgs &a, hipStream_t s);
 hipError_t launch_gate(const GateArgs &a, hipStream_t s);

@@ -287,10 +287,17 @@ static hipError_t decode_d(const DecodeArgs &a, int kv_heads, hipStream_t s)
     else hipLaunchKernelGGL((decode_qk<D, false>), gqk, dim3(256), 0, s, a);
     if (a.g <= 8) {
         if (a.keys_pv == 4 * kKeyTile) hipLaunchKernelGGL((decode_pv<D, 4, 1>), gpv, dim3(256), 0, s, a);
+        else if (a.keys_pv > kDecodeKeysPV) hipLaunchKernelGGL((decode_pv<D, 8, 1, true>), gpv, dim3(512), 0, s, a);
         else hipLaunchKernelGGL((decode_pv<D, 8, 1>), gpv, dim3(512), 0, s, a);
     } else {
-        if (a.keys_pv == 4 * kKeyTile) hipLaunchKernelGGL((decode_pv<D, 4, 2>), gpv, dim3(256), 0, s, a);
-        else hipLaunchKernelGGL((decode_pv<D, 8, 2>), gpv, dim3(512), 0, s, a);
+        if (a.keys_pv == 4 * kKeyTile) {
+            hipLaunchKernelGGL((decode_pv<D, 4, 2>), gpv, dim3(256), 0, s, a);
+        } else if (a.keys_pv > kDecodeKeysPV) {
+            if constexpr (D < 256) hipLaunchKernelGGL((decode_pv<D, 8, 2, true>), gpv, dim3(512), 0, s, a);
+            else return hipErrorInvalidValue;               // decode_pv_loop_ok
+        } else {
+            hipLaunchKernelGGL((decode_pv<D, 8, 2>), gpv, dim3(512), 0, s, a);
+        }
     }
     hipLaunchKernelGGL(decode_combine<D>, dim3(kv_heads * a.sub * a.g, (D + 63) / 64), dim3(64 * kCombineSubs), 0, s, a);
     return hipGetLastError();

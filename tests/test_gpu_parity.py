@@ -28,6 +28,9 @@ SMALL = [
     # two tiles per wave once one tile per wave needs more than a workgroup per CU
     ("decode_d256_n20001_two_tiles", 16, 2, 256, 1, 20000),
     ("decode_d128_n9000_kv4_two_tiles", 16, 4, 128, 1, 8999),
+    # pass 2 in chunks, one round of workgroups, the last chunk of each run partial
+    ("decode_d256_n40001_chunked", 16, 2, 256, 1, 40000),
+    ("decode_d128_kv8_n9000_chunked", 64, 8, 128, 1, 8999),
     # short chunks after long caches: the causal kernel split over the keys
     ("prefill_split_d256_r64_p3000", 16, 2, 256, 64, 3000),
     ("prefill_split_d256_r300_p9000", 16, 2, 256, 300, 9000),
