@@ -337,13 +337,30 @@ static hsdpa_status run_attention(const hsdpa_plan *plan, const hsdpa_call *call
         // workgroups per compute unit needs; this bounds the maxima pass 2
         // reads. Two tiles per wave from one workgroup per compute unit on
         // measured 0.3-0.5 us faster than one tile per wave between 20K and
-        // 32K keys at 2 KV heads, and the same elsewhere.
+        // 32K keys at 2 KV heads, and the same elsewhere. From there up to
+        // twice as many tiles per wave, the count that leaves the fewest
+        // tiles on the busiest compute unit (the looped kernel runs one
+        // workgroup per CU at a time; the smaller count on a tie): a partial
+        // last round costs a whole one (40K keys: 3 tiles in one round, 27.8
+        // us, against 2 tiles in two rounds, 29.2 us).
         const uint64_t nqk1 = (n + hsdpa::kDecodeKeysQK - 1) / hsdpa::kDecodeKeysQK;
         const uint64_t cu1 = static_cast<uint64_t>(cus > 0 ? cus : 1);
         const uint64_t rounds = (groups * nqk1 + 2 * cu1 - 1) / (2 * cu1);
-        const uint64_t rq = !hsdpa::decode_loop_ok(d) ? 1
-                            : groups * nqk1 > cu1 && rounds < 2 ? 2
-                                                                 : rounds;
+        uint64_t rq = !hsdpa::decode_loop_ok(d) ? 1
+                      : groups * nqk1 > cu1 && rounds < 2 ? 2
+                                                           : rounds;
+        if (rq > 1) {
+            uint64_t best = rq, cost = ~0ull;
+            for (uint64_t r = rq; r <= 2 * rq; r++) {
+                const uint64_t wgs = groups * ((nqk1 + r - 1) / r);
+                const uint64_t c = (wgs + cu1 - 1) / cu1 * r;
+                if (c < cost) {
+                    cost = c;
+                    best = r;
+                }
+            }
+            rq = best;
+        }
         a.keys_qk = hsdpa::kDecodeKeysQK * static_cast<int>(rq > 1 ? rq : 1);
         // pass 2 takes 8 tiles per workgroup, or 4 while the smaller
         // workgroups still fit the compute units in one round (short caches:
