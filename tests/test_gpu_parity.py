@@ -31,6 +31,7 @@ SMALL = [
     # pass 2 in chunks, one round of workgroups, the last chunk of each run partial
     ("decode_d256_n40001_chunked", 16, 2, 256, 1, 40000),
     ("decode_d128_kv8_n9000_chunked", 64, 8, 128, 1, 8999),
+    ("decode_d128_g16_n20001_chunked", 64, 4, 128, 1, 20000),   # two P column blocks
     # short chunks after long caches: the causal kernel split over the keys
     ("prefill_split_d256_r64_p3000", 16, 2, 256, 64, 3000),
     ("prefill_split_d256_r300_p9000", 16, 2, 256, 300, 9000),
