@@ -4,6 +4,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 #include <mutex>
@@ -18,6 +19,7 @@ struct hsdpa_plan {
     // decode workspace (floats): scores, per-workgroup maxima, partials
     uint64_t dec_npad;        // scores row length for a full cache
     uint64_t dec_nwg;         // workgroups per KV head for a full cache
+    uint64_t dec_cols;        // columns per KV head: query heads, or (row, head) pairs
     uint64_t off_scores, off_wgmax, off_part_o, off_part_l, dec_bytes;
     // split causal workspace (floats), after the decode's: partial row maxima,
     // outputs and sums of kSplitUnits (split, 32-row group, head) cells
@@ -273,15 +275,22 @@ hsdpa_status hsdpa_plan_create(const hsdpa_spec *spec, hsdpa_plan **out)
     p->kv_heads = kvh;
     p->dec_nwg = (cap + hsdpa::kDecodeKeysQK - 1) / hsdpa::kDecodeKeysQK;  // the larger of the two counts
     p->dec_npad = align_up(cap, hsdpa::kDecodeKeysPV);
+    // room for a few rows after a cache on the decode kernels
+    uint64_t cols = g;
+    if (hsdpa::decode_rows_ok(static_cast<int>(d))) {
+        const uint64_t mr = std::min<uint64_t>(hsdpa::kDecodeMaxCols, hsdpa::kDecodeMaxRows * g);
+        cols = std::max(cols, mr);
+    }
+    p->dec_cols = cols;
     uint64_t off = 0;
     p->off_scores = off;
-    off = align_up(off + kvh * g * p->dec_npad * 4, kAlign);
+    off = align_up(off + kvh * cols * p->dec_npad * 4, kAlign);
     p->off_wgmax = off;
-    off = align_up(off + kvh * p->dec_nwg * g * 4, kAlign);
+    off = align_up(off + kvh * p->dec_nwg * cols * 4, kAlign);
     p->off_part_o = off;
-    off = align_up(off + kvh * p->dec_nwg * g * d * 4, kAlign);
+    off = align_up(off + kvh * p->dec_nwg * cols * d * 4, kAlign);
     p->off_part_l = off;
-    off = align_up(off + kvh * p->dec_nwg * g * 4, kAlign);
+    off = align_up(off + kvh * p->dec_nwg * cols * 4, kAlign);
     p->dec_bytes = off;
     const uint64_t cells = static_cast<uint64_t>(hsdpa::kSplitUnits) * 32;
     p->off_smax = off;
@@ -309,12 +318,16 @@ static hsdpa_status run_attention(const hsdpa_plan *plan, const hsdpa_call *call
     char *ws = static_cast<char *>(call->workspace);
     const uint64_t n = call->past + call->rows;
     const int d = static_cast<int>(s.head_dim);
-    // decode kernels: one query row, the query heads of a KV head in `sub`
-    // equal groups of at most kDecodeMaxGroup (their LDS holds a group's
-    // exponentials; each group streams the KV head's cache); otherwise the
-    // causal kernel serves the row.
-    const int sub = hsdpa::decode_groups(static_cast<int>(s.gqa));
-    if (call->rows == 1 && sub > 0) {
+    // decode kernels: one query row, or up to kDecodeMaxRows rows (one column
+    // per (row, head) pair, each with its own causal limit), the columns of a
+    // KV head in `sub` equal groups of at most kDecodeMaxGroup (their LDS
+    // holds a group's exponentials; each group streams the KV head's cache);
+    // otherwise the causal kernel serves the rows.
+    const uint64_t cols = call->rows * s.gqa;
+    const bool few = call->rows > 1 && call->rows <= hsdpa::kDecodeMaxRows && hsdpa::decode_rows_ok(d) &&
+                     cols <= plan->dec_cols;
+    const int sub = call->rows == 1 || few ? hsdpa::decode_groups(static_cast<int>(cols)) : 0;
+    if (sub > 0) {
         hsdpa::DecodeArgs a{};
         a.q = call->q;
         a.k = call->keys;
@@ -328,8 +341,14 @@ static hsdpa_status run_attention(const hsdpa_plan *plan, const hsdpa_call *call
         a.npad = plan->dec_npad;
         a.kv_stride = s.kv_stride;
         a.q_head = s.q_head;
-        a.g = static_cast<int>(s.gqa) / sub;
+        a.g = static_cast<int>(cols) / sub;
         a.sub = sub;
+        a.rows = static_cast<int>(call->rows);
+        a.G = static_cast<int>(s.gqa);
+        a.past = call->past;
+        a.q_row = s.q_row;
+        a.out_row = s.out_row;
+        a.gate_row = gate_row;
         const uint64_t groups = plan->kv_heads * static_cast<uint64_t>(sub);
         // pass 1: a tile per wave, or several in turn (the next one in flight)
         // once one tile per wave would need more than one workgroup per
@@ -378,7 +397,7 @@ static hsdpa_status run_attention(const hsdpa_plan *plan, const hsdpa_call *call
             const uint64_t per = ucus / groups > 0 ? ucus / groups : 1;
             const uint64_t tiles = (n + hsdpa::kKeyTile - 1) / hsdpa::kKeyTile;
             const uint64_t run = hsdpa::kKeyTile * ((tiles + per - 1) / per);
-            a.keys_pv = groups * nch <= ucus || !hsdpa::decode_pv_loop_ok(d, a.g) || run > (1u << 30)
+            a.keys_pv = groups * nch <= ucus || !hsdpa::decode_pv_loop_ok(d, a.g, a.rows) || run > (1u << 30)
                             ? hsdpa::kDecodeKeysPV
                             : static_cast<int>(run);
         }

@@ -345,7 +345,7 @@ __device__ __forceinline__ u32x4 vt_operand_padded(const uint16_t *vtile, int kb
 // straight from HBM would request 64 bytes of 16 rows per instruction, which
 // streams measurably slower than whole rows.
 // ---------------------------------------------------------------------------
-template <int D, bool LOOP>
+template <int D, bool LOOP, bool MR = false>
 __global__ __launch_bounds__(256) void decode_qk(DecodeArgs a)
 {
     constexpr int KS = D / 32;
@@ -362,7 +362,16 @@ __global__ __launch_bounds__(256) void decode_qk(DecodeArgs a)
     // Rows past the visible keys (loaded from row 0) and columns past g are
     // computed and discarded: an MFMA output element depends only on its own
     // A row and B column.
-    const uint16_t *qp = a.q + static_cast<uint64_t>(kvh * a.g + (colv ? i : 0)) * a.q_head + 8 * G;
+    const uint16_t *qp;
+    uint64_t lim = a.n;                 // keys below lim are visible to this lane's column
+    if constexpr (MR) {
+        const int c = static_cast<int>(blockIdx.z) * a.g + (colv ? i : 0), row = c / a.G;
+        qp = a.q + static_cast<uint64_t>(row) * a.q_row +
+             static_cast<uint64_t>(static_cast<int>(blockIdx.y) * a.G + c - row * a.G) * a.q_head + 8 * G;
+        lim = a.past + static_cast<uint64_t>(row) + 1;
+    } else {
+        qp = a.q + static_cast<uint64_t>(kvh * a.g + (colv ? i : 0)) * a.q_head + 8 * G;
+    }
     u32x4 qb[KS];
 #pragma unroll
     for (int s = 0; s < KS; s++) qb[s] = load16(qp + 32 * s);
@@ -402,7 +411,8 @@ __global__ __launch_bounds__(256) void decode_qk(DecodeArgs a)
                 float *v = reinterpret_cast<float *>(&v4);
 #pragma unroll
                 for (int r = 0; r < 4; r++) {
-                    const bool valid = t0 + 16 * b + 4 * G + r < j1;
+                    const uint64_t key = t0 + 16 * b + 4 * G + r;
+                    const bool valid = key < j1 && (!MR || key < lim);
                     const float s = acc[b][r] * a.scale;
                     v[r] = valid ? s : kNegInf;
                     if (valid) m = s > m ? s : m;
@@ -475,7 +485,7 @@ __global__ __launch_bounds__(256) void decode_qk(DecodeArgs a)
 // chunk's V is in LDS (its registers are free then), O accumulated over the
 // chunks in the MFMA registers.
 // ---------------------------------------------------------------------------
-template <int D, int W, int NCB, bool LOOP = false>
+template <int D, int W, int NCB, bool LOOP = false, bool MR = false>
 __global__ __launch_bounds__(64 * W, D > 256 ? 1 : 8 / W) void decode_pv(DecodeArgs a)
 {
     constexpr int THREADS = 64 * W;
@@ -566,7 +576,13 @@ __global__ __launch_bounds__(64 * W, D > 256 ? 1 : 8 / W) void decode_pv(DecodeA
         for (int i = 0; i < kDecodeMaxGroup / 2; i++) {
             const int h = tid / KEYS + 2 * i;
             if (h >= a.g) break;
-            const float e = kv_e ? exp_poly(sv[i] - smax[h]) : 0.0f;
+            bool vis = kv_e;
+            if constexpr (MR) {
+                // column h's row sees keys [0, past + row]
+                const int row = (static_cast<int>(blockIdx.z) * a.g + h) / a.G;
+                vis = vis && c0 + key_e <= a.past + static_cast<uint64_t>(row);
+            }
+            const float e = vis ? exp_poly(sv[i] - smax[h]) : 0.0f;
             const uint32_t hb = bf16_rne(e);
             pc[h * PS + key_e] = static_cast<uint16_t>(hb);
             pc[(nh + h) * PS + key_e] = static_cast<uint16_t>(bf16_rne(e - __uint_as_float(hb << 16)));
@@ -672,7 +688,7 @@ __global__ __launch_bounds__(64 * W, D > 256 ? 1 : 8 / W) void decode_pv(DecodeA
 // ---------------------------------------------------------------------------
 constexpr int kCombineSubs = 8;
 
-template <int D>
+template <int D, bool MR = false>
 __global__ __launch_bounds__(512) void decode_combine(DecodeArgs a)
 {
     __shared__ float ored[kCombineSubs][64];
@@ -713,8 +729,16 @@ __global__ __launch_bounds__(512) void decode_combine(DecodeArgs a)
             ls += lred[i];
         }
         uint16_t ob = static_cast<uint16_t>(cvt_out(os / ls));
-        if (a.gate) ob = gate_bf16(ob, a.gate[static_cast<uint64_t>(h) * D + dim]);
-        a.out[static_cast<uint64_t>(h) * D + dim] = ob;
+        uint64_t oat = static_cast<uint64_t>(h) * D + dim, gat = oat;
+        if constexpr (MR) {
+            // group kvh = y sub + z; its column jh is column z g + jh of KV head y
+            const int y = kvh / a.sub, c = (kvh - y * a.sub) * a.g + jh, row = c / a.G;
+            const uint64_t head = static_cast<uint64_t>(y * a.G + c - row * a.G);
+            oat = static_cast<uint64_t>(row) * a.out_row + head * D + dim;
+            gat = static_cast<uint64_t>(row) * a.gate_row + head * D + dim;
+        }
+        if (a.gate) ob = gate_bf16(ob, a.gate[gat]);
+        a.out[oat] = ob;
     }
 }
 

@@ -19,6 +19,7 @@ namespace hsdpa {
 template <int D>
 static hipError_t decode_more_d(const DecodeArgs &a, int kv_heads, hipStream_t s)
 {
+    if (a.rows != 1) return hipErrorInvalidValue;           // decode_rows_ok
     const dim3 gqk(a.nwg_qk, kv_heads, a.sub), gpv(a.nwg_pv, kv_heads, a.sub);
     if constexpr (D <= 256) {
         if (a.keys_qk > 4 * kKeyTile) hipLaunchKernelGGL((decode_qk<D, true>), gqk, dim3(256), 0, s, a);

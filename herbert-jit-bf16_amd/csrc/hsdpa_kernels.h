@@ -21,12 +21,19 @@ struct DecodeArgs {
     uint64_t npad;          // scores row length, a multiple of the key tile
     uint64_t kv_stride;
     uint64_t q_head;
-    int g;                  // query heads per group (<= kDecodeMaxGroup)
-    int sub;                // groups per KV head: g * sub query heads share one (the grid's z)
+    int g;                  // columns per group (<= kDecodeMaxGroup)
+    int sub;                // groups per KV head: g * sub columns share one (the grid's z)
     int nwg_qk, nwg_pv;     // workgroups per KV head of the two passes
     int keys_qk, keys_pv;   // keys per workgroup of the two passes
     float scale;
     const uint16_t *gate;   // null, or the output gate: head h at gate + h*head_dim
+    // A few query rows after a cache (the MR kernels): the columns of KV head
+    // y are (row, head) pairs, column c serving row c / G and query head
+    // y G + c % G, whose visible keys are [0, past + row].
+    int rows;               // 1 for a decode step
+    int G;                  // query heads per KV head
+    uint64_t past;
+    uint64_t q_row, out_row, gate_row;
 };
 
 // Causal prefill: `rows` query rows after `past` cached positions.
@@ -118,10 +125,22 @@ inline int decode_groups(int g)
     return 0;
 }
 inline bool decode_wide_ok(int d) { return d <= 256 && (d / 16 >= 8 || 8 % (d / 16) == 0); }
+// A few rows after a cache run on the decode kernels (one column per (row,
+// head) pair, up to 4 groups of 16 columns per KV head) for the tuned head
+// dimensions; the causal kernel computes 32-row tiles, most of them wasted on
+// so few rows.
+constexpr int kDecodeMaxRows = 8;
+constexpr int kDecodeMaxCols = 4 * kDecodeMaxGroup;     // columns per KV head
+inline bool decode_rows_ok(int d) { return d == 64 || d == 128 || d == 256; }
+
 // Pass 2 in chunks (one round of workgroups over a long cache) is built for
-// the tuned head dimensions, at D = 256 for groups of up to 8 heads (with 16
-// the P columns' operands no longer fit beside the next chunk's V tile).
-inline bool decode_pv_loop_ok(int d, int g) { return d == 64 || d == 128 || (d == 256 && g <= 8); }
+// one query row at the tuned head dimensions, at D = 256 for groups of up to 8
+// heads (with 16 the P columns' operands no longer fit beside the next chunk's
+// V tile; with several rows the column limits no longer fit either).
+inline bool decode_pv_loop_ok(int d, int g, int rows)
+{
+    return rows == 1 && (d == 64 || d == 128 || (d == 256 && g <= 8));
+}
 hipError_t launch_layer_prep(const LayerPrepArgs &a, hipStream_t s);
 hipError_t launch_norm_rope(const NormRopeArgs &a, hipStream_t s);
 hipError_t launch_gate(const GateArgs &a, hipStream_t s);

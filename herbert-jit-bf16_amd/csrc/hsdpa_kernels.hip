@@ -279,28 +279,36 @@ __global__ __launch_bounds__(256) void output_gate(GateArgs a)
 bool head_dim_supported(int d) { return d >= 32 && d <= 512 && d % 32 == 0; }
 
 
+// MR: a few rows after a cache, one column per (row, head) pair.
+template <int D, bool MR>
+static hipError_t decode_dm(const DecodeArgs &a, int kv_heads, hipStream_t s)
+{
+    const dim3 gqk(a.nwg_qk, kv_heads, a.sub), gpv(a.nwg_pv, kv_heads, a.sub);
+    if (a.keys_qk > 4 * kKeyTile) hipLaunchKernelGGL((decode_qk<D, true, MR>), gqk, dim3(256), 0, s, a);
+    else hipLaunchKernelGGL((decode_qk<D, false, MR>), gqk, dim3(256), 0, s, a);
+    if (a.g <= 8) {
+        if (a.keys_pv == 4 * kKeyTile) hipLaunchKernelGGL((decode_pv<D, 4, 1, false, MR>), gpv, dim3(256), 0, s, a);
+        else if (a.keys_pv <= kDecodeKeysPV) hipLaunchKernelGGL((decode_pv<D, 8, 1, false, MR>), gpv, dim3(512), 0, s, a);
+        else if constexpr (!MR) hipLaunchKernelGGL((decode_pv<D, 8, 1, true>), gpv, dim3(512), 0, s, a);
+        else return hipErrorInvalidValue;                   // decode_pv_loop_ok
+    } else {
+        if (a.keys_pv == 4 * kKeyTile) {
+            hipLaunchKernelGGL((decode_pv<D, 4, 2, false, MR>), gpv, dim3(256), 0, s, a);
+        } else if (a.keys_pv > kDecodeKeysPV) {
+            if constexpr (D < 256 && !MR) hipLaunchKernelGGL((decode_pv<D, 8, 2, true>), gpv, dim3(512), 0, s, a);
+            else return hipErrorInvalidValue;               // decode_pv_loop_ok
+        } else {
+            hipLaunchKernelGGL((decode_pv<D, 8, 2, false, MR>), gpv, dim3(512), 0, s, a);
+        }
+    }
+    hipLaunchKernelGGL((decode_combine<D, MR>), dim3(kv_heads * a.sub * a.g, (D + 63) / 64), dim3(64 * kCombineSubs), 0, s, a);
+    return hipGetLastError();
+}
+
 template <int D>
 static hipError_t decode_d(const DecodeArgs &a, int kv_heads, hipStream_t s)
 {
-    const dim3 gqk(a.nwg_qk, kv_heads, a.sub), gpv(a.nwg_pv, kv_heads, a.sub);
-    if (a.keys_qk > 4 * kKeyTile) hipLaunchKernelGGL((decode_qk<D, true>), gqk, dim3(256), 0, s, a);
-    else hipLaunchKernelGGL((decode_qk<D, false>), gqk, dim3(256), 0, s, a);
-    if (a.g <= 8) {
-        if (a.keys_pv == 4 * kKeyTile) hipLaunchKernelGGL((decode_pv<D, 4, 1>), gpv, dim3(256), 0, s, a);
-        else if (a.keys_pv > kDecodeKeysPV) hipLaunchKernelGGL((decode_pv<D, 8, 1, true>), gpv, dim3(512), 0, s, a);
-        else hipLaunchKernelGGL((decode_pv<D, 8, 1>), gpv, dim3(512), 0, s, a);
-    } else {
-        if (a.keys_pv == 4 * kKeyTile) {
-            hipLaunchKernelGGL((decode_pv<D, 4, 2>), gpv, dim3(256), 0, s, a);
-        } else if (a.keys_pv > kDecodeKeysPV) {
-            if constexpr (D < 256) hipLaunchKernelGGL((decode_pv<D, 8, 2, true>), gpv, dim3(512), 0, s, a);
-            else return hipErrorInvalidValue;               // decode_pv_loop_ok
-        } else {
-            hipLaunchKernelGGL((decode_pv<D, 8, 2>), gpv, dim3(512), 0, s, a);
-        }
-    }
-    hipLaunchKernelGGL(decode_combine<D>, dim3(kv_heads * a.sub * a.g, (D + 63) / 64), dim3(64 * kCombineSubs), 0, s, a);
-    return hipGetLastError();
+    return a.rows > 1 ? decode_dm<D, true>(a, kv_heads, s) : decode_dm<D, false>(a, kv_heads, s);
 }
 
 hipError_t launch_decode(const DecodeArgs &a, int head_dim, int kv_heads, hipStream_t s)

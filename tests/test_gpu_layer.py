@@ -106,6 +106,9 @@ CASES = [
     ("decode_g16_no_rope", 16, 1, 256, 1, 5000, 5100, True, 0),
     ("decode_g32_two_groups", 32, 1, 128, 1, 700, 800, True, 64),
     ("decode_g17_through_prefill", 17, 1, 128, 1, 700, 800, True, 64),
+    # a few rows after a cache: the decode kernels, gate rows gate_row apart
+    ("few_rows_qwen_4_after_3000", 16, 2, 256, 4, 3000, 3100, True, 64),
+    ("few_rows_d128_3_after_50", 8, 2, 128, 3, 50, 80, True, 128),
     # k and v 2 bytes off: the decode takes the separate element launch
     ("decode_unaligned_kv", 16, 2, 256, 1, 1000, 1100, True, 64, 1),
     # head dimensions outside 64/128/256: the generic norm path and the other

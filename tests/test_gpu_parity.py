@@ -54,6 +54,35 @@ def test_small_shapes(torch_cuda, case):
     print(name, r, flush=True)
 
 
+# A few rows after a cache run on the decode kernels: one column per (row,
+# head) pair, each row with its own causal limit, up to 4 groups of 16 columns
+# per KV head; more columns take the causal kernel.
+FEW = [
+    # name, heads, kv_heads, head_dim, rows, past
+    ("few_r2_d256_g8_p5000", 16, 2, 256, 2, 5000),
+    ("few_r3_d256_g8_p37", 16, 2, 256, 3, 37),             # 24 columns: two groups of 12
+    ("few_r4_d256_g8_p40000", 16, 2, 256, 4, 40000),       # two groups of 16, long cache
+    ("few_r8_d128_g8_p3000", 16, 2, 128, 8, 3000),         # four groups of 16
+    ("few_r5_d128_g8_p900", 16, 2, 128, 5, 900),           # four groups of 10
+    ("few_r8_d64_g1_p100", 8, 8, 64, 8, 100),
+    ("few_r2_d256_g16_p2000", 32, 2, 256, 2, 2000),
+    ("few_r4_d128_g4_p0", 8, 2, 128, 4, 0),                # row r sees keys 0..r only
+    ("few_r7_d256_g8_p0", 16, 2, 256, 7, 0),
+    ("few_r8_d128_g16_causal_kernel", 32, 2, 128, 8, 500),  # 128 columns
+]
+
+
+@pytest.mark.parametrize("case", FEW, ids=[c[0] for c in FEW])
+def test_few_rows(torch_cuda, case):
+    name, h, kvh, d, rows, past = case
+    w = W.make(name, heads=h, kv_heads=kvh, head_dim=d, rows=rows, past=past, seed=17)
+    print(f"case {name}", flush=True)
+    out = run_hsdpa(w)
+    ref = oracle.attention(w)
+    r = assert_parity(out, ref, w, name)
+    print(name, r, flush=True)
+
+
 @pytest.mark.parametrize("name", ["decode_1k", "prefill_512"])
 def test_configs_small(torch_cuda, name):
     w = W.config(name, seed=1)
