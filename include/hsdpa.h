@@ -122,8 +122,9 @@ void hsdpa_plan_destroy(hsdpa_plan *plan);
  * kv_capacity. Calls that may run concurrently need distinct workspaces. */
 uint64_t hsdpa_workspace_bytes(const hsdpa_plan *plan);
 
-/* The whole attention node: every query head of every row, decode when
- * rows == 1, causal prefill otherwise, enqueued on `stream` (a hipStream_t;
+/* The whole attention node: every query head of every row, the decode kernels
+ * when rows == 1 (and for up to 8 rows at head_dim 64, 128 and 256 while
+ * rows * gqa <= 64), causal prefill otherwise, enqueued on `stream` (a hipStream_t;
  * NULL is the default stream). Validation happens on the host before any
  * launch; nothing is allocated. */
 hsdpa_status hsdpa_attention(const hsdpa_plan *plan, const hsdpa_call *call, void *stream);
