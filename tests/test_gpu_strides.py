@@ -21,6 +21,7 @@ CASES = [
     ("prefill_d256", 16, 2, 256, 80, 200),
     ("prefill_d128_split", 16, 4, 128, 40, 3000),      # the split causal kernel
     ("prefill_d96_more", 8, 2, 96, 70, 100),           # the other head dims' unit
+    ("few_rows_d256_r3", 16, 2, 256, 3, 900),          # (row, head) columns on the decode kernels
 ]
 
 SENTINEL = np.uint16(0x7E5A)
