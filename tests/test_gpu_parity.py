@@ -69,6 +69,8 @@ FEW = [
     ("few_r4_d128_g4_p0", 8, 2, 128, 4, 0),                # row r sees keys 0..r only
     ("few_r7_d256_g8_p0", 16, 2, 256, 7, 0),
     ("few_r8_d128_g16_causal_kernel", 32, 2, 128, 8, 500),  # 128 columns
+    ("few_r2_d128_g32_p700", 32, 1, 128, 2, 700),          # 64 columns: four groups of 16
+    ("few_r5_d256_g3_p333", 6, 2, 256, 5, 333),            # 15 columns: one group, two P blocks
 ]
 
 
