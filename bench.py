@@ -19,7 +19,8 @@ not Python launch time; the replay's output is checked against an eager call.
 
 Also timed: the whole attention chain of a gated Qwen3.5 layer (q/k norm and
 RoPE, KV append, attention, output gate) fused into one call against the same
-nodes called one by one.
+nodes called one by one; the decode at 1K, 8K, 32K and 128K keys; and 2, 4 and
+8 rows after the 32K cache (`--no-sweep` skips these two).
 """
 from __future__ import annotations
 
@@ -262,7 +263,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-layer", action="store_true", help="skip the fused layer chain timing")
-    ap.add_argument("--no-sweep", action="store_true", help="skip the decode length sweep")
+    ap.add_argument("--no-sweep", action="store_true", help="skip the decode length sweep and the few-rows timings")
     ap.add_argument("--prefill-steps", type=int, default=0, help="timed prefill steps (default: --steps, max 20)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -369,6 +370,24 @@ def main():
             torch.cuda.empty_cache()
         result["decode_sweep"] = {"keys": sweep, "config": "16 query heads on 2 KV heads, head_dim 256, 1 row; "
                                                            "caches rotated over at least 1 GiB; 20 graph steps"}
+        # a few rows after the 32K cache (speculative verification): (row, head)
+        # columns on the decode kernels
+        few = {}
+        for rows in (2, 4, 8):
+            wf = W.make(f"few_{rows}", heads=16, kv_heads=2, head_dim=256, rows=rows, past=32768 - rows, seed=3)
+            q, ks, vs, out = device_buffers(torch, wf, copies=16)
+            plan_f = hsdpa.Plan(wf.heads, wf.gqa, wf.head_dim, wf.capacity)
+            ws_f = torch.empty(plan_f.workspace_bytes, dtype=torch.uint8, device="cuda")
+            f_ms, _, eager, replay = time_steps(torch, plan_f, wf, q, ks, vs, out, ws_f, 20, 3)
+            if not torch.equal(eager, replay):
+                print(f"{rows} rows: graph replay differs from the eager call", file=sys.stderr)
+                sys.exit(3)
+            few[str(rows)] = {"us": round(f_ms * 1e3, 2)}
+            log(f"{rows} rows after {32768 - rows} keys: {f_ms*1e3:7.2f} us")
+            del q, ks, vs, out, ws_f
+            torch.cuda.empty_cache()
+        result["few_rows"] = {"rows": few, "config": "16 query heads on 2 KV heads, head_dim 256, rows after "
+                                                     "32768 - rows cached keys; 16 rotating caches; 20 graph steps"}
 
     # ---- the layer chain: norms, append, attention, gate -------------------------
     if not args.no_layer:
