@@ -345,16 +345,44 @@ __device__ __forceinline__ u32x4 vt_operand_padded(const uint16_t *vtile, int kb
 // straight from HBM would request 64 bytes of 16 rows per instruction, which
 // streams measurably slower than whole rows.
 // ---------------------------------------------------------------------------
-template <int D, bool LOOP, bool MR = false>
+// The decode passes' workgroup: key range wg of group z (of a.sub) of KV head
+// blockIdx.y. MR = 0 (one row) or 1 (a few rows in one group): wg = blockIdx.x,
+// z = blockIdx.z. MR = 2 (a few rows in several groups): x = (wg / 8 * sub +
+// z) * 8 + wg % 8, the groups of a key range
+// eight workgroups apart, so on one XCD (workgroup i runs on XCD i % 8) and
+// close in time: the later ones find the range's tiles in its L2 (3 to 8 rows
+// after 32K 11-14 % faster, 4 rows after 128K 16 %). x runs over the key
+// ranges padded to a multiple of 8; the padding exits at once.
+template <int MR> struct DecodeIds {
+    int wg, z;
+    __device__ __forceinline__ explicit DecodeIds(const DecodeArgs &a)
+    {
+        if constexpr (MR == 2) {
+            const int x = static_cast<int>(blockIdx.x), lo = x & 7, t = x >> 3;
+            const int hi = t / a.sub;
+            z = t - hi * a.sub;
+            wg = hi * 8 + lo;
+        } else {
+            wg = static_cast<int>(blockIdx.x);
+            z = static_cast<int>(blockIdx.z);
+        }
+    }
+};
+
+template <int D, bool LOOP, int MR = 0>
 __global__ __launch_bounds__(256) void decode_qk(DecodeArgs a)
 {
     constexpr int KS = D / 32;
     constexpr int C = D / 8, KM = swz_group<D>() - 1;          // chunks per row, swizzle mask
     __shared__ __attribute__((aligned(16))) uint16_t kt[4][kKeyTile * D];
     __shared__ float red[4][16];
-    // blockIdx.y: the KV head; blockIdx.z: which of its gridDim.z groups of g
-    // query heads (one unless a KV head has more than 16)
-    const int kvh = blockIdx.y * gridDim.z + blockIdx.z, wg = blockIdx.x;
+    // blockIdx.y: the KV head; id.z: which of its a.sub groups of g columns
+    // (one unless a KV head has more than 16)
+    const DecodeIds<MR> id(a);
+    if (MR == 2 && id.wg >= a.nwg_qk) return;              // grid padding
+    const int kvh = MR == 2 ? static_cast<int>(blockIdx.y) * a.sub + id.z
+                            : static_cast<int>(blockIdx.y * gridDim.z + blockIdx.z);
+    const int wg = id.wg;
     const int wave = threadIdx.x >> 6, l = threadIdx.x & 63, i = l & 15, G = l >> 4;
     const uint64_t j0 = static_cast<uint64_t>(wg) * a.keys_qk;
     const uint64_t j1 = j0 + a.keys_qk < a.n ? j0 + a.keys_qk : a.n;
@@ -365,7 +393,7 @@ __global__ __launch_bounds__(256) void decode_qk(DecodeArgs a)
     const uint16_t *qp;
     uint64_t lim = a.n;                 // keys below lim are visible to this lane's column
     if constexpr (MR) {
-        const int c = static_cast<int>(blockIdx.z) * a.g + (colv ? i : 0), row = c / a.G;
+        const int c = id.z * a.g + (colv ? i : 0), row = c / a.G;
         qp = a.q + static_cast<uint64_t>(row) * a.q_row +
              static_cast<uint64_t>(static_cast<int>(blockIdx.y) * a.G + c - row * a.G) * a.q_head + 8 * G;
         lim = a.past + static_cast<uint64_t>(row) + 1;
@@ -485,7 +513,7 @@ __global__ __launch_bounds__(256) void decode_qk(DecodeArgs a)
 // chunk's V is in LDS (its registers are free then), O accumulated over the
 // chunks in the MFMA registers.
 // ---------------------------------------------------------------------------
-template <int D, int W, int NCB, bool LOOP = false, bool MR = false>
+template <int D, int W, int NCB, bool LOOP = false, int MR = 0>
 __global__ __launch_bounds__(64 * W, D > 256 ? 1 : 8 / W) void decode_pv(DecodeArgs a)
 {
     constexpr int THREADS = 64 * W;
@@ -506,7 +534,11 @@ __global__ __launch_bounds__(64 * W, D > 256 ? 1 : 8 / W) void decode_pv(DecodeA
     __shared__ float smax[kDecodeMaxGroup];
     __shared__ float lpart[W][kDecodeMaxGroup];
     __shared__ __attribute__((aligned(16))) float ored[PARTS > 1 ? (PARTS - 1) * WPP * NCB * DBW * 4 * 64 : 1];
-    const int kvh = blockIdx.y * gridDim.z + blockIdx.z, wg = blockIdx.x, tid = threadIdx.x;   // as in decode_qk
+    const DecodeIds<MR> id(a);
+    if (MR == 2 && id.wg >= a.nwg_pv) return;              // grid padding
+    const int kvh = MR == 2 ? static_cast<int>(blockIdx.y) * a.sub + id.z       // as in decode_qk
+                            : static_cast<int>(blockIdx.y * gridDim.z + blockIdx.z);
+    const int wg = id.wg, tid = threadIdx.x;
     const int wave = tid >> 6, l = tid & 63, j = l & 15, G = l >> 4;
     const uint64_t span = LOOP ? static_cast<uint64_t>(a.keys_pv) : static_cast<uint64_t>(KEYS);
     const uint64_t j0 = static_cast<uint64_t>(wg) * span;
@@ -579,7 +611,7 @@ __global__ __launch_bounds__(64 * W, D > 256 ? 1 : 8 / W) void decode_pv(DecodeA
             bool vis = kv_e;
             if constexpr (MR) {
                 // column h's row sees keys [0, past + row]
-                const int row = (static_cast<int>(blockIdx.z) * a.g + h) / a.G;
+                const int row = (id.z * a.g + h) / a.G;
                 vis = vis && c0 + key_e <= a.past + static_cast<uint64_t>(row);
             }
             const float e = vis ? exp_poly(sv[i] - smax[h]) : 0.0f;

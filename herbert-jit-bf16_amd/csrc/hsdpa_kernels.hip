@@ -279,11 +279,16 @@ __global__ __launch_bounds__(256) void output_gate(GateArgs a)
 bool head_dim_supported(int d) { return d >= 32 && d <= 512 && d % 32 == 0; }
 
 
-// MR: a few rows after a cache, one column per (row, head) pair.
-template <int D, bool MR>
+// MR: a few rows after a cache, one column per (row, head) pair; 2 when
+// they make several groups (DecodeIds).
+template <int D, int MR>
 static hipError_t decode_dm(const DecodeArgs &a, int kv_heads, hipStream_t s)
 {
-    const dim3 gqk(a.nwg_qk, kv_heads, a.sub), gpv(a.nwg_pv, kv_heads, a.sub);
+    // MR = 2: the groups of a key range on one XCD (DecodeIds)
+    constexpr bool xcd = MR == 2;
+    const auto pad8 = [](int n) { return static_cast<unsigned>((n + 7) / 8 * 8); };
+    const dim3 gqk = xcd ? dim3(pad8(a.nwg_qk) * a.sub, kv_heads, 1) : dim3(a.nwg_qk, kv_heads, a.sub);
+    const dim3 gpv = xcd ? dim3(pad8(a.nwg_pv) * a.sub, kv_heads, 1) : dim3(a.nwg_pv, kv_heads, a.sub);
     if (a.keys_qk > 4 * kKeyTile) hipLaunchKernelGGL((decode_qk<D, true, MR>), gqk, dim3(256), 0, s, a);
     else hipLaunchKernelGGL((decode_qk<D, false, MR>), gqk, dim3(256), 0, s, a);
     if (a.g <= 8) {
@@ -301,14 +306,15 @@ static hipError_t decode_dm(const DecodeArgs &a, int kv_heads, hipStream_t s)
             hipLaunchKernelGGL((decode_pv<D, 8, 2, false, MR>), gpv, dim3(512), 0, s, a);
         }
     }
-    hipLaunchKernelGGL((decode_combine<D, MR>), dim3(kv_heads * a.sub * a.g, (D + 63) / 64), dim3(64 * kCombineSubs), 0, s, a);
+    hipLaunchKernelGGL((decode_combine<D, MR != 0>), dim3(kv_heads * a.sub * a.g, (D + 63) / 64), dim3(64 * kCombineSubs), 0, s, a);
     return hipGetLastError();
 }
 
 template <int D>
 static hipError_t decode_d(const DecodeArgs &a, int kv_heads, hipStream_t s)
 {
-    return a.rows > 1 ? decode_dm<D, true>(a, kv_heads, s) : decode_dm<D, false>(a, kv_heads, s);
+    if (a.rows == 1) return decode_dm<D, 0>(a, kv_heads, s);
+    return a.sub > 1 ? decode_dm<D, 2>(a, kv_heads, s) : decode_dm<D, 1>(a, kv_heads, s);
 }
 
 hipError_t launch_decode(const DecodeArgs &a, int head_dim, int kv_heads, hipStream_t s)
