@@ -403,6 +403,12 @@ static hsdpa_status run_attention(const hsdpa_plan *plan, const hsdpa_call *call
         }
         a.nwg_qk = static_cast<int>((n + a.keys_qk - 1) / a.keys_qk);
         a.nwg_pv = static_cast<int>((n + a.keys_pv - 1) / a.keys_pv);
+        // several groups: a key range's groups on one XCD, whose L2 then serves
+        // the later ones (a few rows: 3-8 rows after 32K 11-14 % faster; one
+        // row where pass 2 takes several rounds of workgroups, not chunks: 48
+        // heads on 2 KV heads at 128K, 126 -> 109 us; with chunks, or in one
+        // round, the plain grid is faster)
+        a.xcd = sub > 1 && (call->rows > 1 || (a.keys_pv <= hsdpa::kDecodeKeysPV && groups * nch > ucus)) ? 1 : 0;
         a.scale = call->scale;
         a.gate = gate;
         const hipError_t e = hsdpa::launch_decode(a, d, static_cast<int>(plan->kv_heads), st);

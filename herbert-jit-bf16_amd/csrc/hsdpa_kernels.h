@@ -30,6 +30,7 @@ struct DecodeArgs {
     // A few query rows after a cache (the MR kernels): the columns of KV head
     // y are (row, head) pairs, column c serving row c / G and query head
     // y G + c % G, whose visible keys are [0, past + row].
+    int xcd;                // 1: the groups of a key range numbered onto one XCD (several groups)
     int rows;               // 1 for a decode step
     int G;                  // query heads per KV head
     uint64_t past;

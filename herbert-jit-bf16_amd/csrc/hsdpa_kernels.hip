@@ -279,8 +279,9 @@ __global__ __launch_bounds__(256) void output_gate(GateArgs a)
 bool head_dim_supported(int d) { return d >= 32 && d <= 512 && d % 32 == 0; }
 
 
-// MR: a few rows after a cache, one column per (row, head) pair; 2 when
-// they make several groups (DecodeIds).
+// MR: 1 for a few rows after a cache, one column per (row, head) pair; 2 for
+// several groups numbered onto one XCD per key range (DecodeIds), a few rows or
+// one row (row 0 of every column).
 template <int D, int MR>
 static hipError_t decode_dm(const DecodeArgs &a, int kv_heads, hipStream_t s)
 {
@@ -313,8 +314,8 @@ static hipError_t decode_dm(const DecodeArgs &a, int kv_heads, hipStream_t s)
 template <int D>
 static hipError_t decode_d(const DecodeArgs &a, int kv_heads, hipStream_t s)
 {
-    if (a.rows == 1) return decode_dm<D, 0>(a, kv_heads, s);
-    return a.sub > 1 ? decode_dm<D, 2>(a, kv_heads, s) : decode_dm<D, 1>(a, kv_heads, s);
+    if (a.xcd) return decode_dm<D, 2>(a, kv_heads, s);
+    return a.rows == 1 ? decode_dm<D, 0>(a, kv_heads, s) : decode_dm<D, 1>(a, kv_heads, s);
 }
 
 hipError_t launch_decode(const DecodeArgs &a, int head_dim, int kv_heads, hipStream_t s)
