@@ -43,8 +43,8 @@ MFMA_BF16_PEAK_TFS = 2500.0  # MI355X dense bf16 MFMA, TFLOP/s
 # every L2 fill from the memory fabric, so Infinity Cache hits are included.
 # Summary and commands: profiles/pmc_traffic_decode32k_prefill4096.md
 TRAFFIC_BYTES = {
-    "decode_32k": (2 * (16472.8 + 17511.4 + 1092.1) + (2112.0 + 2056.0 + 8.0)) * 1024,
-    "prefill_4096_after_8192": (2 * 1205671.9 + 36352.0) * 1024,
+    "decode_32k": (2 * (16472.8 + 17512.5 + 1092.1) + (2112.0 + 2056.0 + 8.0)) * 1024,
+    "prefill_4096_after_8192": (2 * 171094.3 + 36352.9) * 1024,
 }
 
 
