@@ -213,7 +213,8 @@ template <int D, int THREADS> struct Tile {
 // NT: non-temporal loads, for the decode streams that no other workgroup
 // reads again. The causal kernels load ordinary ones: the workgroups of a KV
 // head on one XCD walk the same tiles at about the same time, and the L2 then
-// serves all but the first (4096 rows after 8192: 1.50 -> 1.40 ms).
+// serves all but the first (4096 rows after 8192: 1.50 -> 1.40 ms); so do the
+// decode passes whose column groups share an XCD (MR = 2).
 template <int D, int THREADS, bool NT = true>
 __device__ __forceinline__ void tile_gload(const uint16_t *base, uint64_t t0, uint64_t lim, int tid,
                                            u32x4 (&r)[Tile<D, THREADS>::kPer])
@@ -456,7 +457,7 @@ __global__ __launch_bounds__(256) void decode_qk(DecodeArgs a)
     };
     if constexpr (!LOOP) {
         u32x4 kr[Tile<D, 64>::kPer];
-        tile_gload<D, 64>(kbase, j0 + kKeyTile * wave, j1, l, kr);
+        tile_gload<D, 64, MR != 2>(kbase, j0 + kKeyTile * wave, j1, l, kr);
         // Every load is in flight before the first use waits on one: left to
         // itself the scheduler interleaves them and keeps only a few outstanding.
         __builtin_amdgcn_sched_barrier(0);
@@ -467,14 +468,14 @@ __global__ __launch_bounds__(256) void decode_qk(DecodeArgs a)
         // falls past j1 and reads row 0 (clamped, unused)
         const int rounds = a.keys_qk / (4 * kKeyTile);
         u32x4 kr0[Tile<D, 64>::kPer], kr1[Tile<D, 64>::kPer];
-        tile_gload<D, 64>(kbase, j0 + kKeyTile * wave, j1, l, kr0);
+        tile_gload<D, 64, MR != 2>(kbase, j0 + kKeyTile * wave, j1, l, kr0);
         for (int it = 0; it < rounds; it += 2) {
             const uint64_t t0 = j0 + 4 * kKeyTile * it + kKeyTile * wave;
-            tile_gload<D, 64>(kbase, t0 + 4 * kKeyTile, j1, l, kr1);
+            tile_gload<D, 64, MR != 2>(kbase, t0 + 4 * kKeyTile, j1, l, kr1);
             __builtin_amdgcn_sched_barrier(0);
             tile(t0, kr0);
             if (it + 1 < rounds) {
-                tile_gload<D, 64>(kbase, t0 + 8 * kKeyTile, j1, l, kr0);
+                tile_gload<D, 64, MR != 2>(kbase, t0 + 8 * kKeyTile, j1, l, kr0);
                 __builtin_amdgcn_sched_barrier(0);
                 tile(t0 + 4 * kKeyTile, kr1);
             }
@@ -580,7 +581,7 @@ __global__ __launch_bounds__(64 * W, D > 256 ? 1 : 8 / W) void decode_pv(DecodeA
         mx[b] = msrc[w < a.nwg_qk ? w : 0];
     }
     u32x4 vr[Tile<D, 64>::kPer];
-    tile_gload<D, 64>(vbase, j0 + kKeyTile * wave, j1, l, vr);
+    tile_gload<D, 64, MR != 2>(vbase, j0 + kKeyTile * wave, j1, l, vr);
     __builtin_amdgcn_sched_barrier(0);                          // all loads issued first
     float m = kNegInf;
 #pragma unroll
@@ -634,7 +635,7 @@ __global__ __launch_bounds__(64 * W, D > 256 ? 1 : 8 / W) void decode_pv(DecodeA
             // the stores above read vr first: the loads below reuse its registers
             __builtin_amdgcn_sched_barrier(0);
             load_scores(c0 + KEYS);
-            tile_gload<D, 64>(vbase, c0 + KEYS + kKeyTile * wave, j1, l, vr);
+            tile_gload<D, 64, MR != 2>(vbase, c0 + KEYS + kKeyTile * wave, j1, l, vr);
         }
         __syncthreads();
 
