@@ -135,12 +135,12 @@ constexpr int kDecodeMaxCols = 4 * kDecodeMaxGroup;     // columns per KV head
 inline bool decode_rows_ok(int d) { return d == 64 || d == 128 || d == 256; }
 
 // Pass 2 in chunks (one round of workgroups over a long cache) is built for
-// one query row at the tuned head dimensions, at D = 256 for groups of up to 8
-// heads (with 16 the P columns' operands no longer fit beside the next chunk's
-// V tile; with several rows the column limits no longer fit either).
+// the tuned head dimensions, at D = 256 for one row in groups of up to 8
+// columns (with 16 the P columns' operands no longer fit beside the next
+// chunk's V tile; with several rows the column limits no longer fit either).
 inline bool decode_pv_loop_ok(int d, int g, int rows)
 {
-    return rows == 1 && (d == 64 || d == 128 || (d == 256 && g <= 8));
+    return d == 64 || d == 128 || (d == 256 && g <= 8 && rows == 1);
 }
 hipError_t launch_layer_prep(const LayerPrepArgs &a, hipStream_t s);
 hipError_t launch_norm_rope(const NormRopeArgs &a, hipStream_t s);

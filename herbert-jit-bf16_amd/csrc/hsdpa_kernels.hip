@@ -295,13 +295,13 @@ static hipError_t decode_dm(const DecodeArgs &a, int kv_heads, hipStream_t s)
     if (a.g <= 8) {
         if (a.keys_pv == 4 * kKeyTile) hipLaunchKernelGGL((decode_pv<D, 4, 1, false, MR>), gpv, dim3(256), 0, s, a);
         else if (a.keys_pv <= kDecodeKeysPV) hipLaunchKernelGGL((decode_pv<D, 8, 1, false, MR>), gpv, dim3(512), 0, s, a);
-        else if constexpr (!MR) hipLaunchKernelGGL((decode_pv<D, 8, 1, true>), gpv, dim3(512), 0, s, a);
+        else if constexpr (!MR || D < 256) hipLaunchKernelGGL((decode_pv<D, 8, 1, true, MR>), gpv, dim3(512), 0, s, a);
         else return hipErrorInvalidValue;                   // decode_pv_loop_ok
     } else {
         if (a.keys_pv == 4 * kKeyTile) {
             hipLaunchKernelGGL((decode_pv<D, 4, 2, false, MR>), gpv, dim3(256), 0, s, a);
         } else if (a.keys_pv > kDecodeKeysPV) {
-            if constexpr (D < 256 && !MR) hipLaunchKernelGGL((decode_pv<D, 8, 2, true>), gpv, dim3(512), 0, s, a);
+            if constexpr (D < 256) hipLaunchKernelGGL((decode_pv<D, 8, 2, true, MR>), gpv, dim3(512), 0, s, a);
             else return hipErrorInvalidValue;               // decode_pv_loop_ok
         } else {
             hipLaunchKernelGGL((decode_pv<D, 8, 2, false, MR>), gpv, dim3(512), 0, s, a);

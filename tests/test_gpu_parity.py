@@ -71,6 +71,10 @@ FEW = [
     ("few_r8_d128_g16_causal_kernel", 32, 2, 128, 8, 500),  # 128 columns
     ("few_r2_d128_g32_p700", 32, 1, 128, 2, 700),          # 64 columns: four groups of 16
     ("few_r5_d256_g3_p333", 6, 2, 256, 5, 333),            # 15 columns: one group, two P blocks
+    # long caches at D 64 and 128: pass 2 in chunks
+    ("few_r4_d128_g8_p40000_chunked", 16, 2, 128, 4, 40000),
+    ("few_r2_d128_g8_p70000_chunked", 16, 2, 128, 2, 70000),
+    ("few_r3_d64_g4_p50000_chunked", 8, 2, 64, 3, 50000),
 ]
 
 
