@@ -389,15 +389,14 @@ static hsdpa_status run_attention(const hsdpa_plan *plan, const hsdpa_call *call
         // (equal runs stream equal bytes, where rounds of fixed workgroups
         // leave a partial last round)
         const uint64_t nwg4 = (n + 4 * hsdpa::kKeyTile - 1) / (4 * hsdpa::kKeyTile);
-        const uint64_t ucus = static_cast<uint64_t>(cus > 0 ? cus : 1);
         const uint64_t nch = (n + hsdpa::kDecodeKeysPV - 1) / hsdpa::kDecodeKeysPV;
-        if (groups * nwg4 <= ucus || !hsdpa::decode_wide_ok(d)) {
+        if (groups * nwg4 <= cu1 || !hsdpa::decode_wide_ok(d)) {
             a.keys_pv = 4 * hsdpa::kKeyTile;
         } else {
-            const uint64_t per = ucus / groups > 0 ? ucus / groups : 1;
+            const uint64_t per = cu1 / groups > 0 ? cu1 / groups : 1;
             const uint64_t tiles = (n + hsdpa::kKeyTile - 1) / hsdpa::kKeyTile;
             const uint64_t run = hsdpa::kKeyTile * ((tiles + per - 1) / per);
-            a.keys_pv = groups * nch <= ucus || !hsdpa::decode_pv_loop_ok(d, a.g, a.rows) || run > (1u << 30)
+            a.keys_pv = groups * nch <= cu1 || !hsdpa::decode_pv_loop_ok(d, a.g, a.rows) || run > (1u << 30)
                             ? hsdpa::kDecodeKeysPV
                             : static_cast<int>(run);
         }
@@ -408,7 +407,7 @@ static hsdpa_status run_attention(const hsdpa_plan *plan, const hsdpa_call *call
         // row where pass 2 takes several rounds of workgroups, not chunks: 48
         // heads on 2 KV heads at 128K, 126 -> 109 us; with chunks, or in one
         // round, the plain grid is faster)
-        a.xcd = sub > 1 && (call->rows > 1 || (a.keys_pv <= hsdpa::kDecodeKeysPV && groups * nch > ucus)) ? 1 : 0;
+        a.xcd = sub > 1 && (call->rows > 1 || (a.keys_pv <= hsdpa::kDecodeKeysPV && groups * nch > cu1)) ? 1 : 0;
         a.scale = call->scale;
         a.gate = gate;
         const hipError_t e = hsdpa::launch_decode(a, d, static_cast<int>(plan->kv_heads), st);
