@@ -1025,6 +1025,23 @@ struct SplitArgs {
     int heads;
 };
 
+// The split kernels' workgroup (row group x, head group y, split z). When the
+// (head group, split) pairs are a multiple of 8, the row groups of one pair go
+// to one XCD (workgroup i runs on XCD i % 8), where they walk the same key
+// tiles and its L2 serves all but the first (256 rows after 32K: 5 % faster).
+struct SplitIds {
+    int x, y, z;
+    __device__ __forceinline__ SplitIds()
+    {
+        const int gx = gridDim.x, gy = gridDim.y, gz = gridDim.z, C = gy * gz;
+        x = blockIdx.x; y = blockIdx.y; z = blockIdx.z;
+        if (C % 8 == 0) {
+            const int L = x + gx * (y + gy * z), xcd = L & 7, k = L >> 3, c = xcd + 8 * (k / gx);
+            x = k % gx; y = c % gy; z = c / gy;
+        }
+    }
+};
+
 template <int D, int HPW, bool POW2, int NW>
 __global__ __launch_bounds__(64 * NW, 1) void prefill_split_max(PrefillArgs a, SplitArgs sp)
 {
@@ -1033,9 +1050,10 @@ __global__ __launch_bounds__(64 * NW, 1) void prefill_split_max(PrefillArgs a, S
     __shared__ __attribute__((aligned(16))) uint16_t kb[2][kKeyTile * SK];
     const int tid = threadIdx.x;
     const int wave = tid >> 6, l = tid & 63, col = l & 31, grp = l >> 5;
-    const int head = blockIdx.y * HPW + (wave % HPW);
+    const SplitIds sid;
+    const int head = sid.y * HPW + (wave % HPW);
     const int kvh = head / a.gqa;
-    const uint64_t rgroup = gridDim.x - 1 - blockIdx.x;
+    const uint64_t rgroup = gridDim.x - 1 - sid.x;
     const uint64_t wg_r0 = rgroup * (32 * RB);
     const uint64_t w_r0 = wg_r0 + 32 * (wave / HPW);
     const uint64_t row = w_r0 + col;
@@ -1046,7 +1064,7 @@ __global__ __launch_bounds__(64 * NW, 1) void prefill_split_max(PrefillArgs a, S
     const int nfull = wact ? static_cast<int>((a.past + w_r0 + 1) / kKeyTile) : 0;
     const uint64_t lim = a.past + row;
     const int per = (ntiles + static_cast<int>(gridDim.z) - 1) / static_cast<int>(gridDim.z);
-    const int tb = static_cast<int>(blockIdx.z) * per < ntiles ? static_cast<int>(blockIdx.z) * per : ntiles;
+    const int tb = sid.z * per < ntiles ? sid.z * per : ntiles;
     const int te = tb + per < ntiles ? tb + per : ntiles;
 
     const uint16_t *kg = a.k + static_cast<uint64_t>(kvh) * a.kv_stride;
@@ -1089,7 +1107,7 @@ __global__ __launch_bounds__(64 * NW, 1) void prefill_split_max(PrefillArgs a, S
         }
     }
     m = __builtin_fmaxf(m, __shfl_xor(m, 32));
-    if (rowv && grp == 0) sp.smax[(static_cast<uint64_t>(blockIdx.z) * sp.heads + head) * a.rows + row] = m;
+    if (rowv && grp == 0) sp.smax[(static_cast<uint64_t>(sid.z) * sp.heads + head) * a.rows + row] = m;
 }
 
 template <int D, int HPW, bool POW2, int NW>
@@ -1101,9 +1119,10 @@ __global__ __launch_bounds__(64 * NW, 1) void prefill_split_pv(PrefillArgs a, Sp
     __shared__ __attribute__((aligned(16))) uint16_t vb[2][kKeyTile * SV];
     const int tid = threadIdx.x;
     const int wave = tid >> 6, l = tid & 63, col = l & 31, grp = l >> 5;
-    const int head = blockIdx.y * HPW + (wave % HPW);
+    const SplitIds sid;
+    const int head = sid.y * HPW + (wave % HPW);
     const int kvh = head / a.gqa;
-    const uint64_t rgroup = gridDim.x - 1 - blockIdx.x;
+    const uint64_t rgroup = gridDim.x - 1 - sid.x;
     const uint64_t wg_r0 = rgroup * (32 * RB);
     const uint64_t w_r0 = wg_r0 + 32 * (wave / HPW);
     const uint64_t row = w_r0 + col;
@@ -1115,7 +1134,7 @@ __global__ __launch_bounds__(64 * NW, 1) void prefill_split_pv(PrefillArgs a, Sp
     const uint64_t lim = a.past + row;
     const int nz = static_cast<int>(gridDim.z);
     const int per = (ntiles + nz - 1) / nz;
-    const int tb = static_cast<int>(blockIdx.z) * per < ntiles ? static_cast<int>(blockIdx.z) * per : ntiles;
+    const int tb = sid.z * per < ntiles ? sid.z * per : ntiles;
     const int te = tb + per < ntiles ? tb + per : ntiles;
 
     // the exact row maximum: the largest of the splits' partial maxima (rows
@@ -1192,7 +1211,7 @@ __global__ __launch_bounds__(64 * NW, 1) void prefill_split_pv(PrefillArgs a, Sp
     }
     lsum += __shfl_xor(lsum, 32);
     if (rowv) {
-        const uint64_t cell = (static_cast<uint64_t>(blockIdx.z) * a.rows + row) * sp.heads + head;
+        const uint64_t cell = (static_cast<uint64_t>(sid.z) * a.rows + row) * sp.heads + head;
         float *op = sp.so + cell * D;
 #pragma unroll
         for (int dt = 0; dt < D / 32; dt++)
