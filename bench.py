@@ -16,6 +16,13 @@ are captured once into a HIP graph and replayed, so the figure is GPU time,
 not Python launch time; the replay's output is checked against an eager call.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-prefill] [--no-layer] [--no-sweep]
+                    [--only CONFIG ...]
+
+Every configuration of the benchmark is timed and reported under "configs"
+with its own value, time and roofline fraction: decode at 1K keys (8/2
+heads), decode at 32K (the headline), the 512-row causal chunk into an empty
+cache (16/4 heads), the 4096-row chunk after 8192 keys, and decode at 128K
+keys with outlier keys and values.
 
 Also timed: the whole attention chain of a gated Qwen3.5 layer (q/k norm and
 RoPE, KV append, attention, output gate) fused into one call against the same
@@ -215,7 +222,63 @@ def time_layer(torch, hsdpa, w, copies, steps, warmup):
     return results["fused"], results["nodes"], same
 
 
-def cpu_baseline(w_decode, decode_gbs_gpu):
+CONFIG_ORDER = ["decode_1k", "decode_32k", "prefill_512", "prefill_4096_after_8192", "decode_128k_outliers"]
+CONFIG_TEXT = {
+    "decode_1k": "1 query row, 8 query heads on 2 KV heads (GQA 4:1), head_dim 256, 1024 cached keys",
+    "decode_32k": "1 query row, 16 query heads on 2 KV heads (GQA 8:1), head_dim 256, 32768 cached keys",
+    "prefill_512": "causal chunk of 512 rows into an empty cache, 16 query heads on 4 KV heads, head_dim 256",
+    "prefill_4096_after_8192": "causal chunk of 4096 rows after 8192 cached keys, 16 query heads on 2 KV heads, "
+                               "head_dim 256",
+    "decode_128k_outliers": "1 query row, 16 query heads on 2 KV heads, head_dim 256, 131072 cached keys; 4 key "
+                            "channels per KV head x20, 1% of value rows x8",
+}
+DECODE_KERNELS = "decode step (decode_qk + decode_pv + decode_combine)"
+
+
+def bench_config(torch, hsdpa, W, name, kind, steps, warmup, form="chained"):
+    """Time one configuration as a HIP graph of `steps` calls. Decode rotates
+    distinct caches totalling at least 1 GiB (the Infinity Cache is 256 MB);
+    a prefill reads a 24 MiB or smaller cache and runs long enough per call
+    that one copy is representative. Returns the configuration's record."""
+    w = W.config(name, seed=0)
+    per_cache = 2 * w.kv_heads * w.capacity * w.head_dim * 2
+    copies = max(4, -(-(1 << 30) // per_cache)) if kind == "decode" else 1
+    q, ks, vs, out = device_buffers(torch, w, copies=copies)
+    plan = hsdpa.Plan(w.heads, w.gqa, w.head_dim, w.capacity, **({"form": form} if form != "chained" else {}))
+    ws = torch.empty(plan.workspace_bytes, dtype=torch.uint8, device="cuda")
+    ms, wall, eager, replay = time_steps(torch, plan, w, q, ks, vs, out, ws, steps, warmup)
+    if not torch.equal(eager, replay):
+        print(f"{name}: graph replay differs from the eager call", file=sys.stderr)
+        sys.exit(3)
+    del q, ks, vs, out, ws
+    torch.cuda.empty_cache()
+    text = f"{name}: {CONFIG_TEXT[name]}, bf16 q/K/V/out, f32 accumulation, scale 1/16"
+    if form != "chained":
+        text += f", decode form {form}"
+    if kind == "decode":
+        nbytes = w.decode_bytes()
+        val = nbytes / (ms * 1e-3) / 1e9
+        log(f"{name} ({form}): {ms*1e3:.2f} us/step, {val:.1f} GB/s ({val/HBM_PEAK_GBS:.1%} of HBM peak), "
+            f"wall {wall*1e3:.2f} ms")
+        tr = TRAFFIC_BYTES.get(name) if form == "chained" else None
+        return {"value": round(val, 2), "unit": "GB/s", "ms_per_step": round(ms, 5), "steps": steps,
+                "config": {"workload": text, "algorithmic_bytes": nbytes, "kv_caches_rotated": copies},
+                "roofline": {"bound": "hbm", "achieved": round(val, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                             "frac": round(val / HBM_PEAK_GBS, 4), "traffic": round(tr) if tr else None,
+                             "kernel": DECODE_KERNELS}}
+    flops = w.prefill_flops()
+    val = flops / (ms * 1e-3) / 1e12
+    log(f"{name}: {ms*1e3:.2f} us/step, {val:.1f} TFLOP/s ({val/MFMA_BF16_PEAK_TFS:.1%} of MFMA peak)")
+    tr = TRAFFIC_BYTES.get(name)
+    return {"value": round(val, 2), "unit": "TFLOP/s", "ms_per_step": round(ms, 5), "steps": steps,
+            "config": {"workload": text, "algorithmic_flops": flops},
+            "roofline": {"bound": "mfma", "achieved": round(val, 2), "peak": MFMA_BF16_PEAK_TFS, "unit": "TFLOP/s",
+                         "frac": round(val / MFMA_BF16_PEAK_TFS, 4), "traffic": round(tr) if tr else None,
+                         "kernel": "prefill_attn" if name == "prefill_4096_after_8192" else
+                                   "prefill_split_max + prefill_split_pv + prefill_split_combine"}}
+
+
+def cpu_baseline(w_decode):
     """Time the AVX-512 BF16 restatement of the reference on this host: the
     reference's decode node has Hq tasks, so it uses min(cores, Hq) threads;
     a 1-thread figure is reported beside it."""
@@ -265,6 +328,8 @@ def main():
     ap.add_argument("--no-layer", action="store_true", help="skip the fused layer chain timing")
     ap.add_argument("--no-sweep", action="store_true", help="skip the decode length sweep and the few-rows timings")
     ap.add_argument("--prefill-steps", type=int, default=0, help="timed prefill steps (default: --steps, max 20)")
+    ap.add_argument("--only", nargs="*", default=None, choices=CONFIG_ORDER,
+                    help="time only these configurations (the headline line then lacks the others)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: the attention step here is built and timed on a single MI355X; "
@@ -284,29 +349,29 @@ def main():
     props = torch.cuda.get_device_properties(0)
     log(f"device {props.name} gcn {getattr(props, 'gcnArchName', '?')} CUs {props.multi_processor_count}")
 
-    # ---- decode, 32K context ------------------------------------------------
-    wd = W.config("decode_32k", seed=0)
-    q, ks, vs, out = device_buffers(torch, wd, copies=16)
-    plan = hsdpa.Plan(wd.heads, wd.gqa, wd.head_dim, wd.capacity)
-    ws = torch.empty(plan.workspace_bytes, dtype=torch.uint8, device="cuda")
-    ms, wall, eager, replay = time_steps(torch, plan, wd, q, ks, vs, out, ws, args.steps, args.warmup)
-    if not torch.equal(eager, replay):
-        print("graph replay differs from the eager call", file=sys.stderr)
-        sys.exit(3)
-    dec_bytes = wd.decode_bytes()
-    gbs = dec_bytes / (ms * 1e-3) / 1e9
-    log(f"decode_32k: {ms*1e3:.2f} us/step, {gbs:.1f} GB/s ({gbs/HBM_PEAK_GBS:.1%} of HBM peak), wall {wall*1e3:.2f} ms")
-    del ks, vs
-    torch.cuda.empty_cache()
-
+    # ---- the five configurations -------------------------------------------------
+    # decode_32k is the headline (`value`); prefill_4096_after_8192 is also
+    # repeated as `prefill`. Each configuration carries its own time, value and
+    # roofline fraction under "configs".
+    psteps = args.prefill_steps or min(args.steps, 20)
+    configs = {}
+    for name in CONFIG_ORDER:
+        if args.only and name not in args.only:
+            continue
+        kind = "prefill" if name.startswith("prefill") else "decode"
+        if kind == "prefill" and args.no_prefill:
+            continue
+        configs[name] = bench_config(torch, hsdpa, W, name, kind, psteps if kind == "prefill" else args.steps,
+                                     min(args.warmup, 3) if kind == "prefill" else args.warmup)
+    head = configs.get("decode_32k")
     result = {
         "metric": "decode SDPA GB/s (% HBM peak) @32K ctx; prefill TFLOP/s (% MFMA peak)",
-        "value": round(gbs, 2),
+        "value": head["value"] if head else None,
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(ms, 5),
+        "ms_per_step": head["ms_per_step"] if head else None,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -314,41 +379,16 @@ def main():
         "data": "synthetic",
         "config": {"workload": "decode_32k: 1 query row, 16 query heads on 2 KV heads (GQA 8:1), head_dim 256, "
                                "32768 cached keys, bf16 q/K/V/out, f32 accumulation, scale 1/16",
-                   "algorithmic_bytes": dec_bytes, "kv_caches_rotated": 16, "timing": "HIP graph of the timed steps"},
-        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": round(TRAFFIC_BYTES["decode_32k"]),
-                     "kernel": "decode step (decode_qk + decode_pv + decode_combine)"},
+                   "algorithmic_bytes": head["config"]["algorithmic_bytes"] if head else None,
+                   "kv_caches_rotated": head["config"]["kv_caches_rotated"] if head else None,
+                   "timing": "HIP graph of the timed steps"},
+        "roofline": head["roofline"] if head else None,
     }
-
-    # ---- prefill, 4096 rows after 8192 ------------------------------------------
-    if not args.no_prefill:
-        wp = W.config("prefill_4096_after_8192", seed=0)
-        q, ks, vs, out = device_buffers(torch, wp, copies=1)
-        plan_p = hsdpa.Plan(wp.heads, wp.gqa, wp.head_dim, wp.capacity)
-        ws_p = torch.empty(plan_p.workspace_bytes, dtype=torch.uint8, device="cuda")
-        psteps = args.prefill_steps or min(args.steps, 20)
-        pms, pwall, eager, replay = time_steps(torch, plan_p, wp, q, ks, vs, out, ws_p, psteps, min(args.warmup, 3))
-        if not torch.equal(eager, replay):
-            print("prefill graph replay differs from the eager call", file=sys.stderr)
-            sys.exit(3)
-        flops = wp.prefill_flops()
-        tfs = flops / (pms * 1e-3) / 1e12
-        log(f"prefill_4096_after_8192: {pms:.3f} ms/step, {tfs:.1f} TFLOP/s ({tfs/MFMA_BF16_PEAK_TFS:.1%} of MFMA peak)")
-        result["prefill"] = {
-            "value": round(tfs, 2), "unit": "TFLOP/s", "ms_per_step": round(pms, 4), "steps": psteps,
-            "config": {"workload": "prefill_4096_after_8192: causal chunk of 4096 rows after 8192 cached keys, "
-                                   "16 query heads on 2 KV heads, head_dim 256, scale 1/16",
-                       "algorithmic_flops": flops},
-            "roofline": {"bound": "mfma", "achieved": round(tfs, 2), "peak": MFMA_BF16_PEAK_TFS, "unit": "TFLOP/s",
-                         "frac": round(tfs / MFMA_BF16_PEAK_TFS, 4),
-                         "traffic": round(TRAFFIC_BYTES["prefill_4096_after_8192"]),
-                         "kernel": "prefill_attn"},
-        }
-        del ks, vs, q, out
-        torch.cuda.empty_cache()
-        wp_cpu = wp
-    else:
-        wp_cpu = None
+    if "prefill_4096_after_8192" in configs:
+        result["prefill"] = configs["prefill_4096_after_8192"]
+    result["configs"] = configs
+    wd = W.config("decode_32k", seed=0) if not args.no_cpu else None
+    wp_cpu = W.config("prefill_4096_after_8192", seed=0) if ("prefill" in result and not args.no_cpu) else None
 
     # ---- decode at other lengths (same heads): fixed latency vs stream ---------
     if not args.no_sweep:
@@ -419,7 +459,7 @@ def main():
 
     # ---- CPU baseline ------------------------------------------------------------
     if not args.no_cpu:
-        cb, why = cpu_baseline(wd, gbs)
+        cb, why = cpu_baseline(wd)
         if cb is None:
             result["cpu_baseline"] = {"value": None, "unit": "GB/s", "cores": 0, "kind": "port", "sample": why}
         else:

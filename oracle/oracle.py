@@ -81,6 +81,22 @@ def lib():
         L.oracle_dpbf16_selfcheck.restype = ctypes.c_long
         L.oracle_cvt_exp_selfcheck.argtypes = [ctypes.c_uint64, ctypes.c_long]
         L.oracle_cvt_exp_selfcheck.restype = ctypes.c_long
+        L.oracle_fused_qk_dot.argtypes = [u16p, u16p, ctypes.c_int]
+        L.oracle_fused_qk_dot.restype = ctypes.c_float
+        L.oracle_fused_head.argtypes = [u16p, u16p, u16p, u16p, ctypes.c_uint64, ctypes.c_float, ctypes.c_int,
+                                        ctypes.c_void_p]
+        L.oracle_fused_head.restype = ctypes.c_int
+        L.oracle_avx2_qk_dot.argtypes = [u16p, u16p, ctypes.c_int]
+        L.oracle_avx2_qk_dot.restype = ctypes.c_float
+        L.oracle_avx2_head.argtypes = [u16p, u16p, u16p, ctypes.c_void_p, u16p, ctypes.c_uint64, ctypes.c_float,
+                                       ctypes.c_int]
+        L.oracle_avx2_head.restype = ctypes.c_int
+        L.oracle_avx2_cvt_bf16.argtypes = [ctypes.c_float]
+        L.oracle_avx2_cvt_bf16.restype = ctypes.c_uint16
+        L.oracle_exp_poly_n.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint64]
+        L.oracle_exp_poly_n.restype = None
+        L.oracle_attention_form.argtypes = [ctypes.POINTER(Spec), ctypes.POINTER(Call), ctypes.c_int, ctypes.c_int]
+        L.oracle_attention_form.restype = ctypes.c_int
         _lib = L
     return _lib
 
@@ -94,11 +110,29 @@ def avx512_available() -> bool:
     return bool(lib().oracle_avx512_available())
 
 
-def attention(w, impl: str = "auto", threads: int = 0) -> np.ndarray:
+FORMS = {"chained": 0, "fused": 1, "avx2": 2}
+
+
+def attention(w, impl: str = "auto", threads: int = 0, form: str = "chained") -> np.ndarray:
     """Run the reference attention node on workload `w`; returns out bf16 bits
     [rows][heads][head_dim]. impl: 'scalar', 'avx512' or 'auto' (AVX-512
-    when the host has it, which is bit-identical to the scalar one)."""
+    when the host has it, which is bit-identical to the scalar one).
+    form: 'chained' (the engine's default), 'fused' (the knob's online
+    softmax) or 'avx2' (a host without AVX-512 BF16); the last two run the
+    scalar emulation on `threads` threads (0: all cores)."""
     L = lib()
+    if form != "chained":
+        out = np.zeros((w.rows, w.heads, w.head_dim), dtype=np.uint16)
+        q = np.ascontiguousarray(w.q)
+        k = np.ascontiguousarray(w.k)
+        v = np.ascontiguousarray(w.v)
+        spec = Spec(w.heads, w.gqa, w.head_dim, w.q_row, w.head_dim, w.out_row)
+        call = Call(_ptr(q), _ptr(k), _ptr(v), _ptr(out), w.rows, w.past, w.kv_stride, w.scale, 0.0)
+        rc = L.oracle_attention_form(ctypes.byref(spec), ctypes.byref(call), FORMS[form],
+                                     threads or (os.cpu_count() or 1))
+        if rc != 0:
+            raise RuntimeError(f"oracle attention ({form}) failed rc={rc}")
+        return out
     out = np.zeros((w.rows, w.heads, w.head_dim), dtype=np.uint16)
     q = np.ascontiguousarray(w.q)
     k = np.ascontiguousarray(w.k)
@@ -125,6 +159,41 @@ def head(q: np.ndarray, k: np.ndarray, v: np.ndarray, n: int, scale: float) -> n
     sc = np.zeros(((n + 15) // 16) * 16, dtype=np.float32)
     out = np.zeros(d, dtype=np.uint16)
     lib().oracle_sdpa_head(_ptr(q), _ptr(k), _ptr(v), _ptr(sc), _ptr(out), n, scale, d)
+    return out
+
+
+def exp_poly(x: np.ndarray) -> np.ndarray:
+    """The reference's exponential on every element of a float32 array."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty_like(x)
+    lib().oracle_exp_poly_n(_ptr(x), _ptr(y), x.size)
+    return y
+
+
+def fused_head(q: np.ndarray, k: np.ndarray, v: np.ndarray, n: int, scale: float, acc: bool = False):
+    """One Fused-form decode head: out [d] bf16 bits, and the f32 accumulators
+    before the conversion when `acc`."""
+    d = q.shape[-1]
+    q = np.ascontiguousarray(q, dtype=np.uint16)
+    k = np.ascontiguousarray(k, dtype=np.uint16)
+    v = np.ascontiguousarray(v, dtype=np.uint16)
+    out = np.zeros(d, dtype=np.uint16)
+    a = np.zeros(d, dtype=np.float32)
+    if lib().oracle_fused_head(_ptr(q), _ptr(k), _ptr(v), _ptr(out), n, scale, d, _ptr(a)) != 0:
+        raise ValueError("the Fused form declines this head_dim")
+    return (out, a) if acc else out
+
+
+def avx2_head(q: np.ndarray, k: np.ndarray, v: np.ndarray, n: int, scale: float) -> np.ndarray:
+    """One AVX2-arm decode head: out [d] bf16 bits."""
+    d = q.shape[-1]
+    q = np.ascontiguousarray(q, dtype=np.uint16)
+    k = np.ascontiguousarray(k, dtype=np.uint16)
+    v = np.ascontiguousarray(v, dtype=np.uint16)
+    sc = np.zeros(((n + 7) // 8) * 8 + 8, dtype=np.float32)
+    out = np.zeros(d, dtype=np.uint16)
+    if lib().oracle_avx2_head(_ptr(q), _ptr(k), _ptr(v), _ptr(sc), _ptr(out), n, scale, d) != 0:
+        raise ValueError("the AVX2 arm declines this head_dim")
     return out
 
 

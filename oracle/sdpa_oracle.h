@@ -113,6 +113,38 @@ int oracle_attention_scalar(const oracle_attention_spec *spec,
 int oracle_check_geometry(const oracle_attention_spec *spec,
                           const oracle_attention_call *call);
 
+/* ---- the other decode forms (sdpa_forms.c) -------------------------------- */
+
+/* The score of one position in the Fused form, before the scale: four
+ * vdpbf16ps chains over the 32-element chunks, (w0 + w1) + (w2 + w3), hsum
+ * (src/jit/target/x86/emit_sdpa/x86/decode.rs:551-580). */
+float oracle_fused_qk_dot(const uint16_t *q, const uint16_t *k, int head_dim);
+/* The Fused decode head (emit_fused, decode.rs:501-669): online softmax over
+ * blocks of 16 positions. n = 0 writes zeros. acc_out (may be null) receives
+ * the head_dim f32 accumulators before the bf16 conversion. Returns -1 above
+ * head_dim 256 (the form declines, src/jit/ir.rs:146-148). */
+int oracle_fused_head(const uint16_t *q, const uint16_t *k, const uint16_t *v, uint16_t *out, uint64_t n,
+                      float scale, int head_dim, float *acc_out);
+/* The AVX2 arm's QK score before the scale (even element then odd, four
+ * chains over 16-element blocks, an 8-lane tree; emit_sdpa_avx2.rs:262-305). */
+float oracle_avx2_qk_dot(const uint16_t *q, const uint16_t *k, int head_dim);
+/* The AVX2 decode head (src/jit/target/x86/emit_sdpa_avx2.rs:231-470).
+ * scores: at least roundup8(n) f32. Returns -1 when head_dim is not a
+ * multiple of 16 (check_avx2). */
+int oracle_avx2_head(const uint16_t *q, const uint16_t *k, const uint16_t *v, float *scores, uint16_t *out,
+                     uint64_t n, float scale, int head_dim);
+/* oracle_exp_poly element by element over n floats. */
+void oracle_exp_poly_n(const float *x, float *y, uint64_t n);
+/* The AVX2 arm's integer round to nearest even (emit_sdpa_avx2.rs:208-217). */
+uint16_t oracle_avx2_cvt_bf16(float x);
+/* The attention node under a decode form: 0 Chained (as
+ * oracle_attention_scalar), 1 Fused (full 8-row chunks still take the block
+ * kernel; other rows the Fused head, or the Chained one above head_dim 256),
+ * 2 AVX2 (every row the AVX2 head). `threads` workers over (q head, row
+ * group) tasks. Returns 0 or -1. */
+int oracle_attention_form(const oracle_attention_spec *spec, const oracle_attention_call *call, int form,
+                          int threads);
+
 /* ---- AVX-512 BF16 restatement (the CPU baseline) ------------------------ */
 
 /* 1 if this host can run the AVX-512 BF16 path. */
