@@ -22,7 +22,8 @@ Every configuration of the benchmark is timed and reported under "configs"
 with its own value, time and roofline fraction: decode at 1K keys (8/2
 heads), decode at 32K (the headline), the 512-row causal chunk into an empty
 cache (16/4 heads), the 4096-row chunk after 8192 keys, and decode at 128K
-keys with outlier keys and values.
+keys with outlier keys and values. The three decode configurations are also
+timed under the reference's Fused form ("configs_fused").
 
 Also timed: the whole attention chain of a gated Qwen3.5 layer (q/k norm and
 RoPE, KV append, attention, output gate) fused into one call against the same
@@ -328,6 +329,7 @@ def main():
     ap.add_argument("--no-layer", action="store_true", help="skip the fused layer chain timing")
     ap.add_argument("--no-sweep", action="store_true", help="skip the decode length sweep and the few-rows timings")
     ap.add_argument("--prefill-steps", type=int, default=0, help="timed prefill steps (default: --steps, max 20)")
+    ap.add_argument("--no-fused", action="store_true", help="skip the decode timings under the Fused form")
     ap.add_argument("--only", nargs="*", default=None, choices=CONFIG_ORDER,
                     help="time only these configurations (the headline line then lacks the others)")
     args = ap.parse_args()
@@ -387,6 +389,16 @@ def main():
     if "prefill_4096_after_8192" in configs:
         result["prefill"] = configs["prefill_4096_after_8192"]
     result["configs"] = configs
+    # the decode configurations under the reference's Fused form (plan form =
+    # HSDPA_FORM_FUSED), beside the Chained default above
+    if not args.no_fused:
+        fused = {}
+        for name in ("decode_1k", "decode_32k", "decode_128k_outliers"):
+            if args.only and name not in args.only:
+                continue
+            fused[name] = bench_config(torch, hsdpa, W, name, "decode", args.steps, args.warmup, form="fused")
+        if fused:
+            result["configs_fused"] = fused
     wd = W.config("decode_32k", seed=0) if not args.no_cpu else None
     wp_cpu = W.config("prefill_4096_after_8192", seed=0) if ("prefill" in result and not args.no_cpu) else None
 

@@ -16,13 +16,19 @@
 struct hsdpa_plan {
     hsdpa_spec spec;
     uint64_t kv_heads;
-    // decode workspace (floats): scores, per-workgroup maxima, partials
+    uint32_t form;            // the effective form: Fused only up to head_dim 256
+    int cus;                  // compute units the grids are chosen (and the workspace sized) for
+    uint64_t max_rows;        // spec.max_rows, or kv_capacity when 0
+    // decode workspace (floats): scores, per-workgroup maxima, partials; with
+    // the Fused form also the 16-key block maxima and the partials' products
     uint64_t dec_npad;        // scores row length for a full cache
-    uint64_t dec_nwg;         // workgroups per KV head for a full cache
-    uint64_t dec_cols;        // columns per KV head: query heads, or (row, head) pairs
-    uint64_t off_scores, off_wgmax, off_part_o, off_part_l, dec_bytes;
+    uint64_t dec_nwg_qk;      // pass-1 workgroups per group, at most
+    uint64_t dec_cols;        // columns per KV head: query heads, or (row, head) pairs (0: no decode)
+    uint64_t dec_part;        // (pass-2 workgroup, column) partials per KV head, at most
+    uint64_t off_scores, off_wgmax, off_part_o, off_part_l, off_bmax, off_part_x, dec_bytes;
     // split causal workspace (floats), after the decode's: partial row maxima,
-    // outputs and sums of kSplitUnits (split, 32-row group, head) cells
+    // outputs and sums of split_units (split, 32-row group, head) cells
+    uint64_t split_units;
     uint64_t off_smax, off_so, off_sl;
     uint64_t ws_bytes;
 };
@@ -51,6 +57,8 @@ hsdpa_status check_spec(const hsdpa_spec &s)
     if (s.kv_capacity == 0) return HSDPA_ERR_CAPACITY;
     if (s.kv_capacity > (static_cast<uint64_t>(1) << 40) / s.head_dim) return HSDPA_ERR_CAPACITY;
     if (s.kv_stride < s.kv_capacity * s.head_dim) return HSDPA_ERR_STRIDE;
+    if (s.form > HSDPA_FORM_FUSED || s.reserved != 0) return HSDPA_ERR_FORM;
+    if (s.max_rows > s.kv_capacity) return HSDPA_ERR_CAPACITY;
     // the kernels move 16-byte vectors
     if (s.q_row % 8 || s.q_head % 8 || s.out_row % 8 || s.kv_stride % 8) return HSDPA_ERR_ALIGNMENT;
     return HSDPA_OK;
@@ -261,6 +269,133 @@ hsdpa_status hsdpa_kv_append(const hsdpa_kv_spec *spec, const hsdpa_kv_call *cal
 }
 
 
+// ---- decode configuration --------------------------------------------------
+
+namespace {
+
+// How the decode passes cover a call: `sub` groups of `g` columns per KV
+// head, keys per workgroup and workgroups per group of each pass.
+struct DecodeCfg {
+    int sub, g, keys_qk, keys_pv, nwg_qk, nwg_pv, xcd;
+};
+
+// Whether `rows` rows run on the decode kernels: one row whose g query heads
+// split into at most 4 groups of at most 16, or up to 8 rows as (row, head)
+// columns at head dimensions 64, 128 and 256 within the plan's columns.
+int decode_sub(const hsdpa_plan *p, uint64_t rows)
+{
+    const uint64_t cols = rows * p->spec.gqa;
+    const int d = static_cast<int>(p->spec.head_dim);
+    if (rows == 1) return cols <= static_cast<uint64_t>(4 * hsdpa::kDecodeMaxGroup) ? hsdpa::decode_groups(static_cast<int>(cols)) : 0;
+    if (rows > hsdpa::kDecodeMaxRows || !hsdpa::decode_rows_ok(d) || cols > p->dec_cols) return 0;
+    return hsdpa::decode_groups(static_cast<int>(cols));
+}
+
+// The decode passes' grids for `rows` rows over n visible keys (decode_sub
+// already > 0).
+DecodeCfg decode_cfg(const hsdpa_plan *p, uint64_t rows, uint64_t n, int sub)
+{
+    DecodeCfg c{};
+    const int d = static_cast<int>(p->spec.head_dim);
+    const uint64_t cols = rows * p->spec.gqa;
+    c.sub = sub;
+    c.g = static_cast<int>(cols) / sub;
+    const uint64_t groups = p->kv_heads * static_cast<uint64_t>(sub);
+    // pass 1: a tile per wave, or several in turn (the next one in flight)
+    // once one tile per wave would need more than one workgroup per compute
+    // unit: at least two, and as many as one round of two workgroups per
+    // compute unit needs; this bounds the maxima pass 2 reads. Two tiles per
+    // wave from one workgroup per compute unit on measured 0.3-0.5 us faster
+    // than one tile per wave between 20K and 32K keys at 2 KV heads, and the
+    // same elsewhere. From there up to twice as many tiles per wave, the
+    // count that leaves the fewest tiles on the busiest compute unit (the
+    // looped kernel runs one workgroup per CU at a time; the smaller count on
+    // a tie): a partial last round costs a whole one (40K keys: 3 tiles in
+    // one round, 27.8 us, against 2 tiles in two rounds, 29.2 us).
+    const uint64_t nqk1 = (n + hsdpa::kDecodeKeysQK - 1) / hsdpa::kDecodeKeysQK;
+    const uint64_t cu1 = static_cast<uint64_t>(p->cus);
+    const uint64_t rounds = (groups * nqk1 + 2 * cu1 - 1) / (2 * cu1);
+    uint64_t rq = !hsdpa::decode_loop_ok(d) ? 1 : groups * nqk1 > cu1 && rounds < 2 ? 2 : rounds;
+    if (rq > 1) {
+        uint64_t best = rq, cost = ~0ull;
+        for (uint64_t r = rq; r <= 2 * rq; r++) {
+            const uint64_t wgs = groups * ((nqk1 + r - 1) / r);
+            const uint64_t cc = (wgs + cu1 - 1) / cu1 * r;
+            if (cc < cost) {
+                cost = cc;
+                best = r;
+            }
+        }
+        rq = best;
+    }
+    c.keys_qk = hsdpa::kDecodeKeysQK * static_cast<int>(rq > 1 ? rq : 1);
+    // pass 2 takes 8 tiles per workgroup, or 4 while the smaller workgroups
+    // still fit the compute units in one round (short caches: twice the
+    // workgroups, measured faster up to 16K keys at 2 KV heads); past one
+    // round of 8-wave workgroups, one round of chunked ones: the CUs shared
+    // among the groups, each workgroup a run of whole tiles (equal runs stream
+    // equal bytes, where rounds of fixed workgroups leave a partial last round)
+    const uint64_t nwg4 = (n + 4 * hsdpa::kKeyTile - 1) / (4 * hsdpa::kKeyTile);
+    const uint64_t nch = (n + hsdpa::kDecodeKeysPV - 1) / hsdpa::kDecodeKeysPV;
+    if (groups * nwg4 <= cu1 || !hsdpa::decode_wide_ok(d)) {
+        c.keys_pv = 4 * hsdpa::kKeyTile;
+    } else {
+        const uint64_t per = cu1 / groups > 0 ? cu1 / groups : 1;
+        const uint64_t tiles = (n + hsdpa::kKeyTile - 1) / hsdpa::kKeyTile;
+        const uint64_t run = hsdpa::kKeyTile * ((tiles + per - 1) / per);
+        c.keys_pv = groups * nch <= cu1 || !hsdpa::decode_pv_loop_ok(d, c.g, static_cast<int>(rows)) ||
+                            run > (1u << 30)
+                        ? hsdpa::kDecodeKeysPV
+                        : static_cast<int>(run);
+    }
+    c.nwg_qk = static_cast<int>((n + c.keys_qk - 1) / c.keys_qk);
+    c.nwg_pv = static_cast<int>((n + c.keys_pv - 1) / c.keys_pv);
+    // several groups: a key range's groups on one XCD, whose L2 then serves
+    // the later ones (a few rows: 3-8 rows after 32K 11-14 % faster; one row
+    // where pass 2 takes several rounds of workgroups, not chunks: 48 heads on
+    // 2 KV heads at 128K, 126 -> 109 us; with chunks, or in one round, the
+    // plain grid is faster)
+    c.xcd = sub > 1 && (rows > 1 || (c.keys_pv <= hsdpa::kDecodeKeysPV && groups * nch > cu1)) ? 1 : 0;
+    return c;
+}
+
+// The most pass-2 workgroups per group over any n <= cap: one round of CUs
+// shared among the groups wherever the chunked pass 2 applies, otherwise a
+// workgroup per 256 (or 128) keys.
+uint64_t decode_nwg_pv_max(const hsdpa_plan *p, uint64_t rows, int sub)
+{
+    const int d = static_cast<int>(p->spec.head_dim);
+    const uint64_t cap = p->spec.kv_capacity, groups = p->kv_heads * static_cast<uint64_t>(sub);
+    const uint64_t per = static_cast<uint64_t>(p->cus) / groups > 0 ? static_cast<uint64_t>(p->cus) / groups : 1;
+    const uint64_t by128 = (cap + 127) / 128, by256 = (cap + 255) / 256;
+    const int g = static_cast<int>(rows * p->spec.gqa) / sub;
+    if (!hsdpa::decode_wide_ok(d)) return by128;
+    const uint64_t one_round = std::min(by128, per);
+    // the chunked pass 2 gives way to 256-key workgroups where it cannot run
+    // (decode_pv_loop_ok) or a run would exceed 2^30 keys
+    const uint64_t run_max = 32 * (((cap + 31) / 32 + per - 1) / per);
+    if (!hsdpa::decode_pv_loop_ok(d, g, static_cast<int>(rows)) || run_max > (uint64_t{1} << 30))
+        return std::max(one_round, by256);
+    return one_round;
+}
+
+// Whether a call of `rows` rows can reach the causal kernels.
+bool reaches_causal(const hsdpa_plan *p, uint64_t rows) { return decode_sub(p, rows) == 0; }
+
+// The Fused form's rows outside full chunks of 8: the last rows % 8 (the
+// reference's passes of 256 rows are multiples of 8, so only the last pass
+// ends on a partial chunk), all rows of a call shorter than 8.
+uint64_t fused_tail(uint64_t rows) { return rows < 8 ? rows : rows % 8; }
+
+// One sub-call of the node: rows [row0, row0 + rows) of the call, their
+// numerics (Fused or Chained) and their kernels.
+struct Part {
+    uint64_t row0, rows;
+    bool fused;
+};
+
+}  // namespace
+
 hsdpa_status hsdpa_plan_create(const hsdpa_spec *spec, hsdpa_plan **out)
 {
     if (!spec || !out) return HSDPA_ERR_NULL;
@@ -273,26 +408,55 @@ hsdpa_status hsdpa_plan_create(const hsdpa_spec *spec, hsdpa_plan **out)
     const uint64_t d = spec->head_dim, g = spec->gqa, kvh = spec->heads / spec->gqa;
     const uint64_t cap = spec->kv_capacity;
     p->kv_heads = kvh;
-    p->dec_nwg = (cap + hsdpa::kDecodeKeysQK - 1) / hsdpa::kDecodeKeysQK;  // the larger of the two counts
-    p->dec_npad = align_up(cap, hsdpa::kDecodeKeysPV);
-    // room for a few rows after a cache on the decode kernels
-    uint64_t cols = g;
-    if (hsdpa::decode_rows_ok(static_cast<int>(d))) {
-        const uint64_t mr = std::min<uint64_t>(hsdpa::kDecodeMaxCols, hsdpa::kDecodeMaxRows * g);
-        cols = std::max(cols, mr);
+    p->form = spec->form == HSDPA_FORM_FUSED && d <= 256 ? HSDPA_FORM_FUSED : HSDPA_FORM_CHAINED;
+    p->max_rows = spec->max_rows ? spec->max_rows : cap;
+    // the grids (and so the workspace) follow the device's compute units; with
+    // no device current, the MI355X's 256
+    int cus = 0;
+    p->cus = check_device(&cus) == HSDPA_OK && cus > 0 ? cus : 256;
+    // decode columns: the query heads of one row, or up to 8 rows of them
+    uint64_t cols = hsdpa::decode_groups(static_cast<int>(std::min<uint64_t>(g, 1u << 20))) ? g : 0;
+    if (hsdpa::decode_rows_ok(static_cast<int>(d)) && p->max_rows > 1) {
+        const uint64_t mr = std::min<uint64_t>(hsdpa::kDecodeMaxRows, p->max_rows);
+        cols = std::max(cols, std::min<uint64_t>(hsdpa::kDecodeMaxCols, mr * g));
     }
     p->dec_cols = cols;
+    p->dec_npad = align_up(cap, hsdpa::kDecodeKeysPV);
+    p->dec_nwg_qk = (cap + hsdpa::kDecodeKeysQK - 1) / hsdpa::kDecodeKeysQK;
+    // the largest (pass-2 workgroup, column) count of any call the plan serves
+    uint64_t part = 0, cols_used = 0;
+    for (uint64_t r = 1; r <= std::min<uint64_t>(hsdpa::kDecodeMaxRows, p->max_rows); r++) {
+        const int sub = decode_sub(p, r);
+        if (sub == 0) continue;
+        cols_used = std::max(cols_used, r * g);
+        part = std::max(part, decode_nwg_pv_max(p, r, sub) * r * g);
+    }
+    p->dec_cols = cols_used;
+    p->dec_part = part;
     uint64_t off = 0;
     p->off_scores = off;
-    off = align_up(off + kvh * cols * p->dec_npad * 4, kAlign);
+    off = align_up(off + kvh * cols_used * p->dec_npad * 4, kAlign);
     p->off_wgmax = off;
-    off = align_up(off + kvh * p->dec_nwg * cols * 4, kAlign);
+    off = align_up(off + kvh * p->dec_nwg_qk * cols_used * 4, kAlign);
     p->off_part_o = off;
-    off = align_up(off + kvh * p->dec_nwg * cols * d * 4, kAlign);
+    off = align_up(off + kvh * part * d * 4, kAlign);
     p->off_part_l = off;
-    off = align_up(off + kvh * p->dec_nwg * cols * 4, kAlign);
+    off = align_up(off + kvh * part * 4, kAlign);
+    p->off_bmax = p->off_part_x = off;
+    if (p->form == HSDPA_FORM_FUSED) {
+        off = align_up(off + kvh * cols_used * (p->dec_npad / 16) * 4, kAlign);
+        p->off_part_x = off;
+        off = align_up(off + kvh * part * 4, kAlign);
+    }
     p->dec_bytes = off;
-    const uint64_t cells = static_cast<uint64_t>(hsdpa::kSplitUnits) * 32;
+    // the split causal kernel: (split, 32-row group, head) cells, enough for
+    // one round of the compute units (8 row blocks of 32 per workgroup), when
+    // some call of the plan reaches the causal kernels
+    bool causal = false;
+    for (uint64_t r = 1; r <= std::min<uint64_t>(hsdpa::kDecodeMaxRows + 1, p->max_rows) && !causal; r++)
+        causal = reaches_causal(p, r);
+    p->split_units = causal ? std::min<uint64_t>(hsdpa::kSplitUnits, 8 * static_cast<uint64_t>(p->cus)) : 0;
+    const uint64_t cells = p->split_units * 32;
     p->off_smax = off;
     off = align_up(off + cells * 4, kAlign);
     p->off_so = off;
@@ -308,118 +472,72 @@ void hsdpa_plan_destroy(hsdpa_plan *plan) { delete plan; }
 
 uint64_t hsdpa_workspace_bytes(const hsdpa_plan *plan) { return plan ? plan->ws_bytes : 0; }
 
-// The attention node on validated arguments; `gate`, when not null, is
+// Rows [part.row0, part.row0 + part.rows) of a validated call: the decode
+// kernels or the causal ones. `route` (optional) receives the kernels, and
+// nothing is launched when `launch` is false. `gate`, when not null, is
 // applied to the output as it is written (row r, head h at gate +
 // r*gate_row + h*head_dim).
-static hsdpa_status run_attention(const hsdpa_plan *plan, const hsdpa_call *call, const uint16_t *gate,
-                                  uint64_t gate_row, hipStream_t st, int cus)
+static hsdpa_status run_part(const hsdpa_plan *plan, const hsdpa_call *call, const Part &part, const uint16_t *gate,
+                             uint64_t gate_row, hipStream_t st, bool launch, uint32_t *kernels, uint32_t *splits,
+                             uint32_t *launches)
 {
     const hsdpa_spec &s = plan->spec;
     char *ws = static_cast<char *>(call->workspace);
-    const uint64_t n = call->past + call->rows;
+    const uint64_t rows = part.rows, past = call->past + part.row0;
+    const uint64_t n = past + rows;
     const int d = static_cast<int>(s.head_dim);
-    // decode kernels: one query row, or up to kDecodeMaxRows rows (one column
-    // per (row, head) pair, each with its own causal limit), the columns of a
-    // KV head in `sub` equal groups of at most kDecodeMaxGroup (their LDS
-    // holds a group's exponentials; each group streams the KV head's cache);
-    // otherwise the causal kernel serves the rows.
-    const uint64_t cols = call->rows * s.gqa;
-    const bool few = call->rows > 1 && call->rows <= hsdpa::kDecodeMaxRows && hsdpa::decode_rows_ok(d) &&
-                     cols <= plan->dec_cols;
-    const int sub = call->rows == 1 || few ? hsdpa::decode_groups(static_cast<int>(cols)) : 0;
+    const uint16_t *q = call->q ? call->q + part.row0 * s.q_row : nullptr;
+    uint16_t *outp = call->output ? call->output + part.row0 * s.out_row : nullptr;
+    const uint16_t *gp = gate ? gate + part.row0 * gate_row : nullptr;
+    const int sub = decode_sub(plan, rows);
     if (sub > 0) {
+        const DecodeCfg c = decode_cfg(plan, rows, n, sub);
+        if (kernels) *kernels = rows == 1 ? HSDPA_KERNELS_DECODE : HSDPA_KERNELS_FEW_ROWS;
+        if (splits) *splits = 1;
+        if (launches) *launches += 3;
+        if (!launch) return HSDPA_OK;
         hsdpa::DecodeArgs a{};
-        a.q = call->q;
+        a.q = q;
         a.k = call->keys;
         a.v = call->values;
-        a.out = call->output;
+        a.out = outp;
         a.scores = reinterpret_cast<float *>(ws + plan->off_scores);
         a.wgmax = reinterpret_cast<float *>(ws + plan->off_wgmax);
         a.part_o = reinterpret_cast<float *>(ws + plan->off_part_o);
         a.part_l = reinterpret_cast<float *>(ws + plan->off_part_l);
+        a.bmax = reinterpret_cast<float *>(ws + plan->off_bmax);
+        a.part_x = reinterpret_cast<float *>(ws + plan->off_part_x);
+        a.nblk = plan->dec_npad / 16;
         a.n = n;
         a.npad = plan->dec_npad;
         a.kv_stride = s.kv_stride;
         a.q_head = s.q_head;
-        a.g = static_cast<int>(cols) / sub;
-        a.sub = sub;
-        a.rows = static_cast<int>(call->rows);
+        a.g = c.g;
+        a.sub = c.sub;
+        a.rows = static_cast<int>(rows);
         a.G = static_cast<int>(s.gqa);
-        a.past = call->past;
+        a.past = past;
         a.q_row = s.q_row;
         a.out_row = s.out_row;
         a.gate_row = gate_row;
-        const uint64_t groups = plan->kv_heads * static_cast<uint64_t>(sub);
-        // pass 1: a tile per wave, or several in turn (the next one in flight)
-        // once one tile per wave would need more than one workgroup per
-        // compute unit: at least two, and as many as one round of two
-        // workgroups per compute unit needs; this bounds the maxima pass 2
-        // reads. Two tiles per wave from one workgroup per compute unit on
-        // measured 0.3-0.5 us faster than one tile per wave between 20K and
-        // 32K keys at 2 KV heads, and the same elsewhere. From there up to
-        // twice as many tiles per wave, the count that leaves the fewest
-        // tiles on the busiest compute unit (the looped kernel runs one
-        // workgroup per CU at a time; the smaller count on a tie): a partial
-        // last round costs a whole one (40K keys: 3 tiles in one round, 27.8
-        // us, against 2 tiles in two rounds, 29.2 us).
-        const uint64_t nqk1 = (n + hsdpa::kDecodeKeysQK - 1) / hsdpa::kDecodeKeysQK;
-        const uint64_t cu1 = static_cast<uint64_t>(cus > 0 ? cus : 1);
-        const uint64_t rounds = (groups * nqk1 + 2 * cu1 - 1) / (2 * cu1);
-        uint64_t rq = !hsdpa::decode_loop_ok(d) ? 1
-                      : groups * nqk1 > cu1 && rounds < 2 ? 2
-                                                           : rounds;
-        if (rq > 1) {
-            uint64_t best = rq, cost = ~0ull;
-            for (uint64_t r = rq; r <= 2 * rq; r++) {
-                const uint64_t wgs = groups * ((nqk1 + r - 1) / r);
-                const uint64_t c = (wgs + cu1 - 1) / cu1 * r;
-                if (c < cost) {
-                    cost = c;
-                    best = r;
-                }
-            }
-            rq = best;
-        }
-        a.keys_qk = hsdpa::kDecodeKeysQK * static_cast<int>(rq > 1 ? rq : 1);
-        // pass 2 takes 8 tiles per workgroup, or 4 while the smaller
-        // workgroups still fit the compute units in one round (short caches:
-        // twice the workgroups, measured faster up to 16K keys at 2 KV heads);
-        // past one round of 8-wave workgroups, one round of chunked ones: the
-        // CUs shared among the groups, each workgroup a run of whole tiles
-        // (equal runs stream equal bytes, where rounds of fixed workgroups
-        // leave a partial last round)
-        const uint64_t nwg4 = (n + 4 * hsdpa::kKeyTile - 1) / (4 * hsdpa::kKeyTile);
-        const uint64_t nch = (n + hsdpa::kDecodeKeysPV - 1) / hsdpa::kDecodeKeysPV;
-        if (groups * nwg4 <= cu1 || !hsdpa::decode_wide_ok(d)) {
-            a.keys_pv = 4 * hsdpa::kKeyTile;
-        } else {
-            const uint64_t per = cu1 / groups > 0 ? cu1 / groups : 1;
-            const uint64_t tiles = (n + hsdpa::kKeyTile - 1) / hsdpa::kKeyTile;
-            const uint64_t run = hsdpa::kKeyTile * ((tiles + per - 1) / per);
-            a.keys_pv = groups * nch <= cu1 || !hsdpa::decode_pv_loop_ok(d, a.g, a.rows) || run > (1u << 30)
-                            ? hsdpa::kDecodeKeysPV
-                            : static_cast<int>(run);
-        }
-        a.nwg_qk = static_cast<int>((n + a.keys_qk - 1) / a.keys_qk);
-        a.nwg_pv = static_cast<int>((n + a.keys_pv - 1) / a.keys_pv);
-        // several groups: a key range's groups on one XCD, whose L2 then serves
-        // the later ones (a few rows: 3-8 rows after 32K 11-14 % faster; one
-        // row where pass 2 takes several rounds of workgroups, not chunks: 48
-        // heads on 2 KV heads at 128K, 126 -> 109 us; with chunks, or in one
-        // round, the plain grid is faster)
-        a.xcd = sub > 1 && (call->rows > 1 || (a.keys_pv <= hsdpa::kDecodeKeysPV && groups * nch > cu1)) ? 1 : 0;
+        a.keys_qk = c.keys_qk;
+        a.keys_pv = c.keys_pv;
+        a.nwg_qk = c.nwg_qk;
+        a.nwg_pv = c.nwg_pv;
+        a.xcd = c.xcd;
         a.scale = call->scale;
-        a.gate = gate;
-        const hipError_t e = hsdpa::launch_decode(a, d, static_cast<int>(plan->kv_heads), st);
+        a.gate = gp;
+        const hipError_t e = part.fused ? hsdpa::launch_decode_fused(a, d, static_cast<int>(plan->kv_heads), st)
+                                        : hsdpa::launch_decode(a, d, static_cast<int>(plan->kv_heads), st);
         return e == hipSuccess ? HSDPA_OK : HSDPA_ERR_HIP;
     }
     hsdpa::PrefillArgs a{};
-    a.q = call->q;
+    a.q = q;
     a.k = call->keys;
     a.v = call->values;
-    a.out = call->output;
-    a.rows = call->rows;
-    a.past = call->past;
+    a.out = outp;
+    a.rows = rows;
+    a.past = past;
     a.n = n;
     a.q_row = s.q_row;
     a.q_head = s.q_head;
@@ -427,16 +545,73 @@ static hsdpa_status run_attention(const hsdpa_plan *plan, const hsdpa_call *call
     a.kv_stride = s.kv_stride;
     a.gqa = static_cast<int>(s.gqa);
     a.scale = call->scale;
-    a.gate = gate;
+    a.gate = gp;
     a.gate_row = gate_row;
     hsdpa::PrefillSplit ps{};
-    ps.smax = reinterpret_cast<float *>(ws + plan->off_smax);
-    ps.so = reinterpret_cast<float *>(ws + plan->off_so);
-    ps.sl = reinterpret_cast<float *>(ws + plan->off_sl);
-    ps.units = hsdpa::kSplitUnits;
-    ps.cus = cus;
+    if (plan->split_units) {
+        ps.smax = reinterpret_cast<float *>(ws + plan->off_smax);
+        ps.so = reinterpret_cast<float *>(ws + plan->off_so);
+        ps.sl = reinterpret_cast<float *>(ws + plan->off_sl);
+    }
+    ps.units = plan->split_units;
+    ps.cus = plan->cus;
+    const int sp = hsdpa::prefill_split_count(a, d, static_cast<int>(s.heads), ps);
+    if (kernels) *kernels = sp > 1 ? HSDPA_KERNELS_CAUSAL_SPLIT : HSDPA_KERNELS_CAUSAL;
+    if (splits) *splits = static_cast<uint32_t>(sp);
+    if (launches) *launches += sp > 1 ? 3 : 1;
+    if (!launch) return HSDPA_OK;
     const hipError_t e = hsdpa::launch_prefill(a, d, static_cast<int>(s.heads), ps, st);
     return e == hipSuccess ? HSDPA_OK : HSDPA_ERR_HIP;
+}
+
+// The attention node on validated arguments: under the Fused form the rows
+// outside full chunks of 8 take the Fused numerics on the decode kernels (as
+// one few-rows call where the decode kernels take them together, else one
+// decode per row), the others the Chained ones; a route that ends on the
+// causal kernels keeps the Chained numerics.
+static hsdpa_status run_attention(const hsdpa_plan *plan, const hsdpa_call *call, const uint16_t *gate,
+                                  uint64_t gate_row, hipStream_t st, bool launch, hsdpa_route *route)
+{
+    hsdpa_route r{};
+    const uint64_t rows = call->rows;
+    const uint64_t tail = plan->form == HSDPA_FORM_FUSED ? fused_tail(rows) : 0;
+    const uint64_t main = rows - tail;
+    uint32_t splits = 1;
+    hsdpa_status stt = HSDPA_OK;
+    if (main) {
+        stt = run_part(plan, call, Part{0, main, false}, gate, gate_row, st, launch, &r.main, &splits, &r.launches);
+        r.main_rows = main;
+        r.main_form = HSDPA_FORM_CHAINED;
+    }
+    if (stt == HSDPA_OK && tail) {
+        // the tail's kernels decide its numerics: the decode kernels compute the
+        // Fused weights, the causal ones the Chained
+        const bool together = decode_sub(plan, tail) > 0;
+        uint32_t kern = HSDPA_KERNELS_NONE, sp = 1;
+        if (together) {
+            stt = run_part(plan, call, Part{main, tail, true}, gate, gate_row, st, launch, &kern, &sp, &r.launches);
+        } else {
+            for (uint64_t i = 0; i < tail && stt == HSDPA_OK; i++)
+                stt = run_part(plan, call, Part{main + i, 1, true}, gate, gate_row, st, launch, &kern, &sp,
+                               &r.launches);
+            if (tail > 1 && kern == HSDPA_KERNELS_DECODE) kern = HSDPA_KERNELS_DECODE_ROWS;
+        }
+        const bool on_decode = kern == HSDPA_KERNELS_DECODE || kern == HSDPA_KERNELS_FEW_ROWS ||
+                               kern == HSDPA_KERNELS_DECODE_ROWS;
+        if (main) {
+            r.tail = kern;
+            r.tail_rows = tail;
+            r.tail_form = on_decode ? HSDPA_FORM_FUSED : HSDPA_FORM_CHAINED;
+        } else {
+            r.main = kern;
+            r.main_rows = tail;
+            r.main_form = on_decode ? HSDPA_FORM_FUSED : HSDPA_FORM_CHAINED;
+            splits = sp;
+        }
+    }
+    r.splits = splits;
+    if (route) *route = r;
+    return stt;
 }
 
 // The host checks of the attention node (rows > 0 already established).
@@ -444,6 +619,7 @@ static hsdpa_status check_attention_call(const hsdpa_plan *plan, const hsdpa_cal
 {
     const hsdpa_spec &s = plan->spec;
     if (call->rows > s.kv_capacity || call->past > s.kv_capacity - call->rows) return HSDPA_ERR_CAPACITY;
+    if (call->rows > plan->max_rows) return HSDPA_ERR_BATCH;
     if (!call->q || !call->keys || !call->values || !call->output || !call->workspace) return HSDPA_ERR_NULL;
     if (!aligned16(call->q) || !aligned16(call->keys) || !aligned16(call->values) || !aligned16(call->output) ||
         !aligned16(call->workspace))
@@ -462,7 +638,22 @@ hsdpa_status hsdpa_attention(const hsdpa_plan *plan, const hsdpa_call *call, voi
     int cus = 0;
     const hsdpa_status dev = check_device(&cus);
     if (dev != HSDPA_OK) return dev;
-    return run_attention(plan, call, nullptr, 0, static_cast<hipStream_t>(stream), cus);
+    (void)cus;
+    return run_attention(plan, call, nullptr, 0, static_cast<hipStream_t>(stream), true, nullptr);
+}
+
+hsdpa_status hsdpa_attention_route(const hsdpa_plan *plan, uint64_t rows, uint64_t past, hsdpa_route *out)
+{
+    if (!plan || !out) return HSDPA_ERR_NULL;
+    *out = hsdpa_route{};
+    if (rows == 0) return HSDPA_OK;
+    const hsdpa_spec &s = plan->spec;
+    if (rows > s.kv_capacity || past > s.kv_capacity - rows) return HSDPA_ERR_CAPACITY;
+    if (rows > plan->max_rows) return HSDPA_ERR_BATCH;
+    hsdpa_call c{};
+    c.rows = rows;
+    c.past = past;
+    return run_attention(plan, &c, nullptr, 0, nullptr, false, out);
 }
 
 hsdpa_status hsdpa_attention_layer(const hsdpa_plan *plan, const hsdpa_layer_call *call, void *stream)
@@ -522,7 +713,8 @@ hsdpa_status hsdpa_attention_layer(const hsdpa_plan *plan, const hsdpa_layer_cal
     p.plus_one = call->plus_one ? 1 : 0;
     p.eps = call->eps;
     if (hsdpa::launch_layer_prep(p, stream_h) != hipSuccess) return HSDPA_ERR_HIP;
-    return run_attention(plan, &ac, call->gate, call->gate_row, stream_h, cus);
+    (void)cus;
+    return run_attention(plan, &ac, call->gate, call->gate_row, stream_h, true, nullptr);
 }
 
 const char *hsdpa_status_string(hsdpa_status status)
@@ -540,12 +732,13 @@ const char *hsdpa_status_string(hsdpa_status status)
     case HSDPA_ERR_NULL: return "null pointer";
     case HSDPA_ERR_HIP: return "HIP launch or runtime error";
     case HSDPA_ERR_NO_DEVICE: return "no gfx950 device is current";
-    case HSDPA_ERR_BATCH: return "more rows than the reserve's max_batch";
+    case HSDPA_ERR_BATCH: return "more rows than the reserve's max_batch or the plan's max_rows";
     case HSDPA_ERR_LAYOUT: return "the R16 copies of the KV cache are an AArch64 layout";
+    case HSDPA_ERR_FORM: return "unknown decode form";
     }
     return "unknown status";
 }
 
-uint32_t hsdpa_version(void) { return 100; }
+uint32_t hsdpa_version(void) { return 200; }
 
 }  // extern "C"

@@ -375,7 +375,10 @@ template <int MR> struct DecodeIds {
     }
 };
 
-template <int D, bool LOOP, int MR = 0>
+// FUSED: also store the maximum of every 16-key block of each column (bmax):
+// the Fused form evaluates a block's exponentials at the running maximum of
+// the blocks up to it.
+template <int D, bool LOOP, int MR = 0, bool FUSED = false>
 __global__ __launch_bounds__(256) void decode_qk(DecodeArgs a)
 {
     constexpr int KS = D / 32;
@@ -454,6 +457,26 @@ __global__ __launch_bounds__(256) void decode_qk(DecodeArgs a)
                 *reinterpret_cast<float4 *>(sp + 16 * b) = v4;
             }
         }
+        if constexpr (FUSED) {
+            // block b of the tile: keys t0 + 16 b + 4 G + r over the four lane
+            // groups G of column i (the same scaled values as stored above)
+#pragma unroll
+            for (int b = 0; b < 2; b++) {
+                float bm = kNegInf;
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const uint64_t key = t0 + 16 * b + 4 * G + r;
+                    const float s = acc[b][r] * a.scale;
+                    if (key < j1 && (!MR || key < lim)) bm = s > bm ? s : bm;
+                }
+                const float o16 = __shfl_xor(bm, 16);
+                bm = o16 > bm ? o16 : bm;
+                const float o32 = __shfl_xor(bm, 32);
+                bm = o32 > bm ? o32 : bm;
+                if (colv && G == 0 && t0 + 16 * b < j1)
+                    a.bmax[static_cast<uint64_t>(kvh * a.g + i) * a.nblk + (t0 + 16 * b) / 16] = bm;
+            }
+        }
     };
     if constexpr (!LOOP) {
         u32x4 kr[Tile<D, 64>::kPer];
@@ -518,8 +541,16 @@ __global__ __launch_bounds__(256) void decode_qk(DecodeArgs a)
 // 3-5 per chunk, the next chunk's scores and V tiles loaded as soon as this
 // chunk's V is in LDS (its registers are free then), O accumulated over the
 // chunks in the MFMA registers.
+// FUSED (the reference's Fused form, src/jit/target/x86/emit_sdpa/x86/decode.rs:
+// 501-669): the keys are blocks of 16, each evaluated at the running maximum
+// M_b of the blocks up to it instead of the row maximum, and weighted by the
+// product C_b of the corrections P(M_{b'-1} - M_b') of the later blocks b' of
+// the chunk: e = fl(P(s - M_b) * C_b). The running maximum entering the
+// workgroup comes from the pass-1 maxima of the keys before it; a chunk
+// rescales what came before it by its corrections' product X (O and l, in
+// LOOP), and part_x receives the workgroup's product for the combine.
 // ---------------------------------------------------------------------------
-template <int D, int W, int NCB, bool LOOP = false, int MR = 0>
+template <int D, int W, int NCB, bool LOOP = false, int MR = 0, bool FUSED = false>
 __global__ __launch_bounds__(64 * W, D > 256 ? 1 : 8 / W) void decode_pv(DecodeArgs a)
 {
     constexpr int THREADS = 64 * W;
@@ -540,6 +571,12 @@ __global__ __launch_bounds__(64 * W, D > 256 ? 1 : 8 / W) void decode_pv(DecodeA
     __shared__ float smax[kDecodeMaxGroup];
     __shared__ float lpart[W][kDecodeMaxGroup];
     __shared__ __attribute__((aligned(16))) float ored[PARTS > 1 ? (PARTS - 1) * WPP * NCB * DBW * 4 * 64 : 1];
+    // FUSED: per (column, block of the chunk): block maximum, running maximum,
+    // correction, suffix product of the later corrections; per column: the
+    // chunk's and the workgroup's products
+    constexpr int NB = KEYS / 16;
+    constexpr int FN = FUSED ? kDecodeMaxGroup * NB : 1, FH = FUSED ? kDecodeMaxGroup : 1;
+    __shared__ float fbm[FN], fmb[FN], fcor[FN], fcf[FN], fx[FH], fxw[FH];
     const DecodeIds<MR> id(a);
     if (MR == 2 && id.wg >= a.nwg_pv) return;              // grid padding
     const int kvh = MR == 2 ? static_cast<int>(blockIdx.y) * a.sub + id.z       // as in decode_qk
@@ -574,6 +611,8 @@ __global__ __launch_bounds__(64 * W, D > 256 ? 1 : 8 / W) void decode_pv(DecodeA
     const int jh = tid / T, u = tid % T;
     const float *msrc = a.wgmax + (static_cast<uint64_t>(kvh) * a.g + (jh < a.g ? jh : 0)) * a.nwg_qk;
     constexpr int BATCH = 8;
+    // FUSED: only the pass-1 workgroups wholly before this workgroup's keys
+    const int wlim = FUSED ? static_cast<int>(j0 / static_cast<uint64_t>(a.keys_qk)) : a.nwg_qk;
     float mx[BATCH];
 #pragma unroll
     for (int b = 0; b < BATCH; b++) {
@@ -585,18 +624,28 @@ __global__ __launch_bounds__(64 * W, D > 256 ? 1 : 8 / W) void decode_pv(DecodeA
     __builtin_amdgcn_sched_barrier(0);                          // all loads issued first
     float m = kNegInf;
 #pragma unroll
-    for (int b = 0; b < BATCH; b++) m = (u + b * T < a.nwg_qk && mx[b] > m) ? mx[b] : m;
-    for (int w0 = u + BATCH * T; w0 < a.nwg_qk; w0 += BATCH * T) {
+    for (int b = 0; b < BATCH; b++) m = (u + b * T < wlim && mx[b] > m) ? mx[b] : m;
+    for (int w0 = u + BATCH * T; w0 < wlim; w0 += BATCH * T) {
 #pragma unroll
         for (int b = 0; b < BATCH; b++) {
             const int w = w0 + b * T;
             mx[b] = msrc[w < a.nwg_qk ? w : 0];
         }
 #pragma unroll
-        for (int b = 0; b < BATCH; b++) m = (w0 + b * T < a.nwg_qk && mx[b] > m) ? mx[b] : m;
+        for (int b = 0; b < BATCH; b++) m = (w0 + b * T < wlim && mx[b] > m) ? mx[b] : m;
+    }
+    if constexpr (FUSED) {
+        // the blocks between the last whole pass-1 workgroup and j0
+        const uint64_t b1 = j0 / 16;
+        const float *bsrc = a.bmax + (static_cast<uint64_t>(kvh) * a.g + (jh < a.g ? jh : 0)) * a.nblk;
+        for (uint64_t b = static_cast<uint64_t>(wlim) * (a.keys_qk / 16) + u; b < b1; b += T) {
+            const float x = bsrc[b];
+            m = x > m ? x : m;
+        }
     }
 
-    // 2. exact maximum per query head: a DPP reduction over the head's lanes
+    // 2. exact maximum per query head (FUSED: the running maximum entering the
+    //    workgroup): a DPP reduction over the head's lanes
     m = group_max_hi(m, T);
     if (u == T - 1 && jh < a.g) smax[jh] = m;
     __syncthreads();
@@ -607,6 +656,55 @@ __global__ __launch_bounds__(64 * W, D > 256 ? 1 : 8 / W) void decode_pv(DecodeA
     for (uint64_t c0 = j0;; c0 += KEYS) {
         const uint64_t c1 = c0 + KEYS < j1 ? c0 + KEYS : j1;
         const bool kv_e = c0 + key_e < c1;
+        // whether key c0 + key_e is visible to column h
+        auto visible = [&](int h) {
+            bool vis = kv_e;
+            if constexpr (MR) {
+                // column h's row sees keys [0, past + row]
+                const int row = (id.z * a.g + h) / a.G;
+                vis = vis && c0 + key_e <= a.past + static_cast<uint64_t>(row);
+            }
+            return vis;
+        };
+        if constexpr (FUSED) {
+            // (a) the maxima of the chunk's 16-key blocks: a row of 16 lanes
+            //     holds one block of one column
+#pragma unroll
+            for (int i = 0; i < kDecodeMaxGroup / 2; i++) {
+                const int h = tid / KEYS + 2 * i;
+                if (h >= a.g) break;
+                float x = visible(h) ? sv[i] : kNegInf;
+                x = group_max_hi(x, 16);
+                if ((l & 15) == 0) fbm[h * NB + key_e / 16] = x;
+            }
+            __syncthreads();
+            // (b) per (column, block): the running maximum M_b and the
+            //     correction P(M_{b-1} - M_b), M_{-1} the maximum entering the chunk
+            if (tid < a.g * NB) {
+                const int h = tid / NB, b = tid - h * NB;
+                float mp = smax[h];
+                for (int k = 0; k < b; k++) mp = fbm[h * NB + k] > mp ? fbm[h * NB + k] : mp;
+                const float mb = fbm[h * NB + b] > mp ? fbm[h * NB + b] : mp;
+                fmb[tid] = mb;
+                fcor[tid] = exp_poly(mp - mb);
+            }
+            __syncthreads();
+            // (c) C_b = the product of the later blocks' corrections; the
+            //     chunk's product X rescales what came before it
+            if (tid < a.g * NB) {
+                const int h = tid / NB, b = tid - h * NB;
+                float c = 1.0f;
+                for (int k = b + 1; k < NB; k++) c = c * fcor[h * NB + k];
+                fcf[tid] = c;
+                if (b == 0) {
+                    const float x = fcor[h * NB] * c;
+                    fx[h] = x;
+                    fxw[h] = c0 == j0 ? x : fxw[h] * x;
+                    smax[h] = fmb[h * NB + NB - 1];
+                }
+            }
+            __syncthreads();
+        }
         // 3. dense exponentials: thread t owns key c0 + t % KEYS for heads
         //    t / KEYS, t / KEYS + 2, ...; a wave covers 64 consecutive keys of
         //    one head set
@@ -614,18 +712,23 @@ __global__ __launch_bounds__(64 * W, D > 256 ? 1 : 8 / W) void decode_pv(DecodeA
         for (int i = 0; i < kDecodeMaxGroup / 2; i++) {
             const int h = tid / KEYS + 2 * i;
             if (h >= a.g) break;
-            bool vis = kv_e;
-            if constexpr (MR) {
-                // column h's row sees keys [0, past + row]
-                const int row = (id.z * a.g + h) / a.G;
-                vis = vis && c0 + key_e <= a.past + static_cast<uint64_t>(row);
+            const bool vis = visible(h);
+            float e;
+            if constexpr (FUSED) {
+                const int fb = h * NB + key_e / 16;
+                e = vis ? exp_poly(sv[i] - fmb[fb]) * fcf[fb] : 0.0f;
+            } else {
+                e = vis ? exp_poly(sv[i] - smax[h]) : 0.0f;
             }
-            const float e = vis ? exp_poly(sv[i] - smax[h]) : 0.0f;
             const uint32_t hb = bf16_rne(e);
             pc[h * PS + key_e] = static_cast<uint16_t>(hb);
             pc[(nh + h) * PS + key_e] = static_cast<uint16_t>(bf16_rne(e - __uint_as_float(hb << 16)));
             const float sum = wave_sum_hi(e);
-            if (l == 63) lpart[wave][h] = (LOOP && c0 != j0 ? lpart[wave][h] : 0.0f) + sum;
+            if constexpr (FUSED) {
+                if (l == 63) lpart[wave][h] = (LOOP && c0 != j0 ? lpart[wave][h] * fx[h] : 0.0f) + sum;
+            } else {
+                if (l == 63) lpart[wave][h] = (LOOP && c0 != j0 ? lpart[wave][h] : 0.0f) + sum;
+            }
         }
         // 4. V tile to LDS; with LOOP the next chunk's scores and V tiles are
         //    requested right behind it
@@ -638,6 +741,20 @@ __global__ __launch_bounds__(64 * W, D > 256 ? 1 : 8 / W) void decode_pv(DecodeA
             tile_gload<D, 64, MR != 2>(vbase, c0 + KEYS + kKeyTile * wave, j1, l, vr);
         }
         __syncthreads();
+        if constexpr (FUSED && LOOP) {
+            // what the earlier chunks accumulated, rescaled by this chunk's
+            // corrections; lane j holds column j (j % 8 with g <= 8: hi and lo)
+            if (c0 != j0) {
+                const int hc = NCB == 1 ? (j & 7) : j;
+                const float x = fx[hc < a.g ? hc : 0];
+#pragma unroll
+                for (int c = 0; c < NCB; c++)
+#pragma unroll
+                    for (int db = 0; db < DBW; db++)
+#pragma unroll
+                        for (int r = 0; r < 4; r++) o[c][db][r] = o[c][db][r] * x;
+            }
+        }
 
         // 5. P.V for this wave's dimension blocks. Columns that hold no head
         //    read whatever the LDS holds; their outputs are never used. Every
@@ -715,6 +832,7 @@ __global__ __launch_bounds__(64 * W, D > 256 ? 1 : 8 / W) void decode_pv(DecodeA
         float L = 0.0f;
         for (int w = 0; w < KEYS / 64; w++) L += lpart[p0 + w][tid];
         a.part_l[pbase + tid] = L;
+        if constexpr (FUSED) a.part_x[pbase + tid] = fxw[tid];
     }
 }
 
@@ -723,14 +841,21 @@ __global__ __launch_bounds__(64 * W, D > 256 ? 1 : 8 / W) void decode_pv(DecodeA
 // grid (heads, D/64), 512 threads: 64 dimensions x 8 interleaved partial
 // subsets; every thread issues all its loads before adding (one round trip
 // for up to 8 * 16 partials), and the subsets are summed in a fixed order.
+// FUSED: the partials of workgroup w are relative to the running maximum at
+// its end; the product S_w of the later workgroups' correction products
+// brings them to the last one's (out = sum S_w O_w / sum S_w l_w). S_w comes
+// from a doubling scan in LDS over segments of kFusedMaxSeg workgroups, the
+// last segment first. The output is the sum times its reciprocal, as the
+// Fused form normalises (decode.rs:653-659).
 // ---------------------------------------------------------------------------
 constexpr int kCombineSubs = 8;
 
-template <int D, bool MR = false>
+template <int D, bool MR = false, bool FUSED = false>
 __global__ __launch_bounds__(512) void decode_combine(DecodeArgs a)
 {
     __shared__ float ored[kCombineSubs][64];
     __shared__ float lred[kCombineSubs];
+    __shared__ float xs[FUSED ? kFusedMaxSeg : 1];
     const int h = blockIdx.x, kvh = h / a.g, jh = h % a.g;
     const int t = threadIdx.x & 63, sub = threadIdx.x >> 6;
     // D not a multiple of 64: lanes past D in the last block read dimension 0
@@ -740,7 +865,44 @@ __global__ __launch_bounds__(512) void decode_combine(DecodeArgs a)
     float o = 0.0f, L = 0.0f;
     const uint64_t base = static_cast<uint64_t>(kvh) * a.nwg_pv * a.g + jh;
     constexpr int BATCH = 16;
-    for (int w0 = sub; w0 < a.nwg_pv; w0 += kCombineSubs * BATCH) {
+    if constexpr (FUSED) {
+        const int tid = threadIdx.x;
+        float carry = 1.0f;                 // product over the workgroups after the segment
+        for (int s1 = a.nwg_pv; s1 > 0; s1 -= kFusedMaxSeg) {
+            const int s0 = s1 > kFusedMaxSeg ? s1 - kFusedMaxSeg : 0, cnt = s1 - s0;
+            __syncthreads();                // the previous segment's xs is read
+            if (tid < cnt) xs[tid] = a.part_x[base + static_cast<uint64_t>(s0 + tid) * a.g];
+            __syncthreads();
+            // xs[i] <- the product of xs[i .. cnt-1]
+            for (int off = 1; off < cnt; off *= 2) {
+                const float y = tid + off < cnt ? xs[tid + off] : 1.0f;
+                __syncthreads();
+                if (tid < cnt) xs[tid] = xs[tid] * y;
+                __syncthreads();
+            }
+            for (int w0 = s0 + sub; w0 < s1; w0 += kCombineSubs * BATCH) {
+                float xo[BATCH], xl[BATCH];
+#pragma unroll
+                for (int b = 0; b < BATCH; b++) {
+                    const int w = w0 + kCombineSubs * b;
+                    const uint64_t part = base + static_cast<uint64_t>(w < s1 ? w : s0) * a.g;
+                    xo[b] = a.part_o[part * D + dim];
+                    xl[b] = a.part_l[part];
+                }
+#pragma unroll
+                for (int b = 0; b < BATCH; b++) {
+                    const int i = w0 + kCombineSubs * b - s0;
+                    if (i < cnt) {
+                        const float S = (i + 1 < cnt ? xs[i + 1] : 1.0f) * carry;
+                        o += S * xo[b];
+                        L += S * xl[b];
+                    }
+                }
+            }
+            carry = carry * xs[0];
+        }
+    }
+    for (int w0 = sub; !FUSED && w0 < a.nwg_pv; w0 += kCombineSubs * BATCH) {
         float xo[BATCH], xl[BATCH];
 #pragma unroll
         for (int b = 0; b < BATCH; b++) {
@@ -766,7 +928,7 @@ __global__ __launch_bounds__(512) void decode_combine(DecodeArgs a)
             os += ored[i][t];
             ls += lred[i];
         }
-        uint16_t ob = static_cast<uint16_t>(cvt_out(os / ls));
+        uint16_t ob = static_cast<uint16_t>(cvt_out(FUSED ? os * (1.0f / ls) : os / ls));
         uint64_t oat = static_cast<uint64_t>(h) * D + dim, gat = oat;
         if constexpr (MR) {
             // group kvh = y sub + z; its column jh is column z g + jh of KV head y
@@ -1240,20 +1402,21 @@ static bool scale_is_pow2(float s)
 // whether a power-of-two scale takes the folded form (the general form rounds
 // identically).
 template <int D, int HPW, int NW, bool POW2_FORM = true>
-static void launch_prefill_split(const PrefillArgs &a, int heads, const PrefillSplit &ps, dim3 grid, int splits,
-                                 hipStream_t s)
+static hipError_t launch_prefill_split(const PrefillArgs &a, int heads, const PrefillSplit &ps, dim3 grid, int splits,
+                                       hipStream_t s)
 {
     const SplitArgs sp{ps.smax, ps.so, ps.sl, heads};
     const dim3 gs(grid.x, grid.y, static_cast<unsigned>(splits));
+    hipError_t e;
     if (POW2_FORM && scale_is_pow2(a.scale)) {
-        hipLaunchKernelGGL((prefill_split_max<D, HPW, POW2_FORM, NW>), gs, dim3(64 * NW), 0, s, a, sp);
-        hipLaunchKernelGGL((prefill_split_pv<D, HPW, POW2_FORM, NW>), gs, dim3(64 * NW), 0, s, a, sp);
+        e = launch(prefill_split_max<D, HPW, POW2_FORM, NW>, gs, dim3(64 * NW), s, a, sp);
+        if (e == hipSuccess) e = launch(prefill_split_pv<D, HPW, POW2_FORM, NW>, gs, dim3(64 * NW), s, a, sp);
     } else {
-        hipLaunchKernelGGL((prefill_split_max<D, HPW, false, NW>), gs, dim3(64 * NW), 0, s, a, sp);
-        hipLaunchKernelGGL((prefill_split_pv<D, HPW, false, NW>), gs, dim3(64 * NW), 0, s, a, sp);
+        e = launch(prefill_split_max<D, HPW, false, NW>, gs, dim3(64 * NW), s, a, sp);
+        if (e == hipSuccess) e = launch(prefill_split_pv<D, HPW, false, NW>, gs, dim3(64 * NW), s, a, sp);
     }
-    hipLaunchKernelGGL(prefill_split_combine<D>, dim3(static_cast<unsigned>(a.rows), heads), dim3(D), 0, s, a, sp,
-                       splits);
+    if (e != hipSuccess) return e;
+    return launch(prefill_split_combine<D>, dim3(static_cast<unsigned>(a.rows), heads), dim3(D), s, a, sp, splits);
 }
 
 template <int D>

@@ -21,27 +21,28 @@ static hipError_t decode_more_d(const DecodeArgs &a, int kv_heads, hipStream_t s
 {
     if (a.rows != 1) return hipErrorInvalidValue;           // decode_rows_ok
     const dim3 gqk(a.nwg_qk, kv_heads, a.sub), gpv(a.nwg_pv, kv_heads, a.sub);
+    hipError_t e;
     if constexpr (D <= 256) {
-        if (a.keys_qk > 4 * kKeyTile) hipLaunchKernelGGL((decode_qk<D, true>), gqk, dim3(256), 0, s, a);
-        else hipLaunchKernelGGL((decode_qk<D, false>), gqk, dim3(256), 0, s, a);
+        e = a.keys_qk > 4 * kKeyTile ? launch(decode_qk<D, true>, gqk, dim3(256), s, a)
+                                     : launch(decode_qk<D, false>, gqk, dim3(256), s, a);
     } else {
         if (a.keys_qk != 4 * kKeyTile) return hipErrorInvalidValue;
-        hipLaunchKernelGGL((decode_qk<D, false>), gqk, dim3(256), 0, s, a);
+        e = launch(decode_qk<D, false>, gqk, dim3(256), s, a);
     }
+    if (e != hipSuccess) return e;
     constexpr bool WIDE = D <= 256 && (D / 16 >= 8 || 8 % (D / 16) == 0);   // decode_wide_ok
     if (a.keys_pv == 4 * kKeyTile) {
-        if (a.g <= 8) hipLaunchKernelGGL((decode_pv<D, 4, 1>), gpv, dim3(256), 0, s, a);
-        else hipLaunchKernelGGL((decode_pv<D, 4, 2>), gpv, dim3(256), 0, s, a);
+        e = a.g <= 8 ? launch(decode_pv<D, 4, 1>, gpv, dim3(256), s, a) : launch(decode_pv<D, 4, 2>, gpv, dim3(256), s, a);
     } else {
         if constexpr (WIDE) {
-            if (a.g <= 8) hipLaunchKernelGGL((decode_pv<D, 8, 1>), gpv, dim3(512), 0, s, a);
-            else hipLaunchKernelGGL((decode_pv<D, 8, 2>), gpv, dim3(512), 0, s, a);
+            e = a.g <= 8 ? launch(decode_pv<D, 8, 1>, gpv, dim3(512), s, a)
+                         : launch(decode_pv<D, 8, 2>, gpv, dim3(512), s, a);
         } else {
             return hipErrorInvalidValue;
         }
     }
-    hipLaunchKernelGGL(decode_combine<D>, dim3(kv_heads * a.sub * a.g, (D + 63) / 64), dim3(64 * kCombineSubs), 0, s, a);
-    return hipGetLastError();
+    if (e != hipSuccess) return e;
+    return launch(decode_combine<D>, dim3(kv_heads * a.sub * a.g, (D + 63) / 64), dim3(64 * kCombineSubs), s, a);
 }
 
 template <int D>
@@ -51,9 +52,8 @@ static hipError_t prefill_more_d(const PrefillArgs &a, int heads, const PrefillS
     constexpr int ROWS = 32 * NW;                                // HPW = 1: NW row blocks of one head
     const dim3 grid(static_cast<unsigned>((a.rows + ROWS - 1) / ROWS), heads);
     const int splits = prefill_splits(a, static_cast<uint64_t>(grid.x) * grid.y, heads, ps);
-    if (splits > 1) launch_prefill_split<D, 1, NW, false>(a, heads, ps, grid, splits, s);
-    else hipLaunchKernelGGL((prefill_attn<D, 1, false, NW>), grid, dim3(64 * NW), 0, s, a);
-    return hipGetLastError();
+    if (splits > 1) return launch_prefill_split<D, 1, NW, false>(a, heads, ps, grid, splits, s);
+    return launch(prefill_attn<D, 1, false, NW>, grid, dim3(64 * NW), s, a);
 }
 
 #define HSDPA_MORE_DIMS(X) \

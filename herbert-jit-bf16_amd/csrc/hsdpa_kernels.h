@@ -5,7 +5,30 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <tuple>
+#include <type_traits>
+#include <utility>
+
 namespace hsdpa {
+
+// Launch `kernel` on stream `s` and return that launch's own status; a HIP
+// error left over from an earlier, unrelated call is not reported as this
+// one's (hipLaunchKernel returns the launch's result, where
+// hipGetLastError would also return a stale one).
+template <typename K, typename T, size_t... I>
+inline hipError_t launch_held(K kernel, dim3 grid, dim3 block, hipStream_t s, T &held, std::index_sequence<I...>)
+{
+    void *ptrs[] = {static_cast<void *>(&std::get<I>(held))...};
+    return hipLaunchKernel(reinterpret_cast<const void *>(kernel), grid, block, ptrs, 0, s);
+}
+
+template <typename... P, typename... A>
+inline hipError_t launch(void (*kernel)(P...), dim3 grid, dim3 block, hipStream_t s, A &&...args)
+{
+    static_assert(sizeof...(P) == sizeof...(A), "one argument per kernel parameter");
+    std::tuple<std::decay_t<P>...> held(std::forward<A>(args)...);
+    return launch_held(kernel, grid, block, s, held, std::index_sequence_for<P...>{});
+}
 
 // Decode: one query row, g query heads per KV head, n visible keys.
 struct DecodeArgs {
@@ -35,6 +58,12 @@ struct DecodeArgs {
     int G;                  // query heads per KV head
     uint64_t past;
     uint64_t q_row, out_row, gate_row;
+    // The Fused form (the online softmax over blocks of 16 keys): pass 1 also
+    // stores each block's maximum, pass 2 the product of its blocks'
+    // corrections; unused by the Chained form.
+    float *bmax;            // [groups][g][nblk] maxima of the 16-key blocks
+    float *part_x;          // [groups][nwg_pv][g] products of a workgroup's corrections
+    uint64_t nblk;          // bmax row length: npad / 16
 };
 
 // Causal prefill: `rows` query rows after `past` cached positions.
@@ -54,7 +83,7 @@ struct PrefillArgs {
 // The split form of the causal kernel (see prefill_split_max): workspace for
 // its partial maxima, outputs and sums, and what the launcher needs to choose
 // the number of splits. units: the most (split, 32-row group, head) cells the
-// workspace holds. No split when `so` is null.
+// workspace holds. No split when units is 0.
 struct PrefillSplit {
     float *smax, *so, *sl;
     uint64_t units;
@@ -148,8 +177,14 @@ hipError_t launch_gate(const GateArgs &a, hipStream_t s);
 hipError_t launch_kv_append(const KvAppendArgs &a, bool vec, hipStream_t s);
 hipError_t launch_decode(const DecodeArgs &a, int head_dim, int kv_heads, hipStream_t s);
 hipError_t launch_prefill(const PrefillArgs &a, int head_dim, int heads, const PrefillSplit &ps, hipStream_t s);
+// the key splits launch_prefill would choose (1: the one-workgroup kernel)
+int prefill_split_count(const PrefillArgs &a, int head_dim, int heads, const PrefillSplit &ps);
 // the head dimensions other than 64, 128 and 256 (hsdpa_attn_more.hip)
 hipError_t launch_decode_more(const DecodeArgs &a, int head_dim, int kv_heads, hipStream_t s);
+// the Fused form of the decode passes, head dimensions 32 to 256 (hsdpa_fused.hip)
+hipError_t launch_decode_fused(const DecodeArgs &a, int head_dim, int kv_heads, hipStream_t s);
+// the pass-2 workgroups a Fused combine can scan per head (its LDS)
+constexpr int kFusedMaxSeg = 512;
 hipError_t launch_prefill_more(const PrefillArgs &a, int head_dim, int heads, const PrefillSplit &ps, hipStream_t s);
 
 // Splits for a causal call whose one-workgroup grid has `wgs` workgroups: enough
@@ -158,7 +193,7 @@ hipError_t launch_prefill_more(const PrefillArgs &a, int head_dim, int heads, co
 // the rows see fewer than 8 tiles.
 inline int prefill_splits(const PrefillArgs &a, uint64_t wgs, int heads, const PrefillSplit &ps)
 {
-    if (!ps.so || ps.cus <= 0 || wgs * 2 > static_cast<uint64_t>(ps.cus)) return 1;
+    if (ps.units == 0 || ps.cus <= 0 || wgs * 2 > static_cast<uint64_t>(ps.cus)) return 1;
     const uint64_t ntiles = (a.past + a.rows + kKeyTile - 1) / kKeyTile;
     if (ntiles < 8) return 1;
     uint64_t s = static_cast<uint64_t>(ps.cus) / wgs;

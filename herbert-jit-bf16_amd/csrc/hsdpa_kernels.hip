@@ -290,25 +290,27 @@ static hipError_t decode_dm(const DecodeArgs &a, int kv_heads, hipStream_t s)
     const auto pad8 = [](int n) { return static_cast<unsigned>((n + 7) / 8 * 8); };
     const dim3 gqk = xcd ? dim3(pad8(a.nwg_qk) * a.sub, kv_heads, 1) : dim3(a.nwg_qk, kv_heads, a.sub);
     const dim3 gpv = xcd ? dim3(pad8(a.nwg_pv) * a.sub, kv_heads, 1) : dim3(a.nwg_pv, kv_heads, a.sub);
-    if (a.keys_qk > 4 * kKeyTile) hipLaunchKernelGGL((decode_qk<D, true, MR>), gqk, dim3(256), 0, s, a);
-    else hipLaunchKernelGGL((decode_qk<D, false, MR>), gqk, dim3(256), 0, s, a);
+    hipError_t e = a.keys_qk > 4 * kKeyTile ? launch(decode_qk<D, true, MR>, gqk, dim3(256), s, a)
+                                            : launch(decode_qk<D, false, MR>, gqk, dim3(256), s, a);
+    if (e != hipSuccess) return e;
     if (a.g <= 8) {
-        if (a.keys_pv == 4 * kKeyTile) hipLaunchKernelGGL((decode_pv<D, 4, 1, false, MR>), gpv, dim3(256), 0, s, a);
-        else if (a.keys_pv <= kDecodeKeysPV) hipLaunchKernelGGL((decode_pv<D, 8, 1, false, MR>), gpv, dim3(512), 0, s, a);
-        else if constexpr (!MR || D < 256) hipLaunchKernelGGL((decode_pv<D, 8, 1, true, MR>), gpv, dim3(512), 0, s, a);
+        if (a.keys_pv == 4 * kKeyTile) e = launch(decode_pv<D, 4, 1, false, MR>, gpv, dim3(256), s, a);
+        else if (a.keys_pv <= kDecodeKeysPV) e = launch(decode_pv<D, 8, 1, false, MR>, gpv, dim3(512), s, a);
+        else if constexpr (!MR || D < 256) e = launch(decode_pv<D, 8, 1, true, MR>, gpv, dim3(512), s, a);
         else return hipErrorInvalidValue;                   // decode_pv_loop_ok
     } else {
         if (a.keys_pv == 4 * kKeyTile) {
-            hipLaunchKernelGGL((decode_pv<D, 4, 2, false, MR>), gpv, dim3(256), 0, s, a);
+            e = launch(decode_pv<D, 4, 2, false, MR>, gpv, dim3(256), s, a);
         } else if (a.keys_pv > kDecodeKeysPV) {
-            if constexpr (D < 256) hipLaunchKernelGGL((decode_pv<D, 8, 2, true, MR>), gpv, dim3(512), 0, s, a);
+            if constexpr (D < 256) e = launch(decode_pv<D, 8, 2, true, MR>, gpv, dim3(512), s, a);
             else return hipErrorInvalidValue;               // decode_pv_loop_ok
         } else {
-            hipLaunchKernelGGL((decode_pv<D, 8, 2, false, MR>), gpv, dim3(512), 0, s, a);
+            e = launch(decode_pv<D, 8, 2, false, MR>, gpv, dim3(512), s, a);
         }
     }
-    hipLaunchKernelGGL((decode_combine<D, MR != 0>), dim3(kv_heads * a.sub * a.g, (D + 63) / 64), dim3(64 * kCombineSubs), 0, s, a);
-    return hipGetLastError();
+    if (e != hipSuccess) return e;
+    return launch(decode_combine<D, MR != 0>, dim3(kv_heads * a.sub * a.g, (D + 63) / 64), dim3(64 * kCombineSubs),
+                  s, a);
 }
 
 template <int D>
@@ -328,27 +330,43 @@ hipError_t launch_decode(const DecodeArgs &a, int head_dim, int kv_heads, hipStr
     }
 }
 
-template <int D, int HPW>
-static void prefill_dh(const PrefillArgs &a, int heads, const PrefillSplit &ps, hipStream_t s)
+// The causal kernel's grid: (row groups, head groups) of HPW query heads x
+// 32 * 8 / HPW rows at the tuned head dimensions (HPW the largest of 8, 4, 2
+// that divides the group size), one head x 32 NW rows at the others.
+static dim3 prefill_grid(const PrefillArgs &a, int head_dim, int heads)
 {
-    const int rows_per_wg = 32 * (8 / HPW);
-    const dim3 grid(static_cast<unsigned>((a.rows + rows_per_wg - 1) / rows_per_wg), heads / HPW);
-    const int splits = prefill_splits(a, static_cast<uint64_t>(grid.x) * grid.y, heads, ps);
-    if (splits > 1) {
-        launch_prefill_split<D, HPW, 8>(a, heads, ps, grid, splits, s);
-        return;
+    if (head_dim == 64 || head_dim == 128 || head_dim == 256) {
+        const int hpw = a.gqa % 8 == 0 ? 8 : a.gqa % 4 == 0 ? 4 : a.gqa % 2 == 0 ? 2 : 1;
+        const uint64_t rows_per_wg = 32 * (8 / hpw);
+        return dim3(static_cast<unsigned>((a.rows + rows_per_wg - 1) / rows_per_wg), heads / hpw);
     }
-    if (scale_is_pow2(a.scale)) hipLaunchKernelGGL((prefill_attn<D, HPW, true>), grid, dim3(512), 0, s, a);
-    else hipLaunchKernelGGL((prefill_attn<D, HPW, false>), grid, dim3(512), 0, s, a);
+    const uint64_t rows_per_wg = 32 * (head_dim > 256 ? 4 : 8);
+    return dim3(static_cast<unsigned>((a.rows + rows_per_wg - 1) / rows_per_wg), heads);
+}
+
+int prefill_split_count(const PrefillArgs &a, int head_dim, int heads, const PrefillSplit &ps)
+{
+    const dim3 g = prefill_grid(a, head_dim, heads);
+    return prefill_splits(a, static_cast<uint64_t>(g.x) * g.y, heads, ps);
+}
+
+template <int D, int HPW>
+static hipError_t prefill_dh(const PrefillArgs &a, int heads, const PrefillSplit &ps, hipStream_t s)
+{
+    const dim3 grid = prefill_grid(a, D, heads);
+    const int splits = prefill_splits(a, static_cast<uint64_t>(grid.x) * grid.y, heads, ps);
+    if (splits > 1) return launch_prefill_split<D, HPW, 8>(a, heads, ps, grid, splits, s);
+    if (scale_is_pow2(a.scale)) return launch(prefill_attn<D, HPW, true>, grid, dim3(512), s, a);
+    return launch(prefill_attn<D, HPW, false>, grid, dim3(512), s, a);
 }
 
 template <int D>
-static void prefill_d(const PrefillArgs &a, int heads, const PrefillSplit &ps, hipStream_t s)
+static hipError_t prefill_d(const PrefillArgs &a, int heads, const PrefillSplit &ps, hipStream_t s)
 {
-    if (a.gqa % 8 == 0) prefill_dh<D, 8>(a, heads, ps, s);
-    else if (a.gqa % 4 == 0) prefill_dh<D, 4>(a, heads, ps, s);
-    else if (a.gqa % 2 == 0) prefill_dh<D, 2>(a, heads, ps, s);
-    else prefill_dh<D, 1>(a, heads, ps, s);
+    if (a.gqa % 8 == 0) return prefill_dh<D, 8>(a, heads, ps, s);
+    if (a.gqa % 4 == 0) return prefill_dh<D, 4>(a, heads, ps, s);
+    if (a.gqa % 2 == 0) return prefill_dh<D, 2>(a, heads, ps, s);
+    return prefill_dh<D, 1>(a, heads, ps, s);
 }
 
 hipError_t launch_kv_append(const KvAppendArgs &a, bool vec, hipStream_t s)
@@ -356,41 +374,34 @@ hipError_t launch_kv_append(const KvAppendArgs &a, bool vec, hipStream_t s)
     const uint64_t total = a.rows * a.heads * a.head_dim / (vec ? 8 : 1);
     const uint64_t wgs = (total + 255) / 256;
     const dim3 grid(static_cast<unsigned>(wgs < 16384 ? wgs : 16384));
-    if (vec) hipLaunchKernelGGL(kv_append<true>, grid, dim3(256), 0, s, a);
-    else hipLaunchKernelGGL(kv_append<false>, grid, dim3(256), 0, s, a);
-    return hipGetLastError();
+    return vec ? launch(kv_append<true>, grid, dim3(256), s, a) : launch(kv_append<false>, grid, dim3(256), s, a);
 }
 
 hipError_t launch_norm_rope(const NormRopeArgs &a, hipStream_t s)
 {
-    hipLaunchKernelGGL(head_norm_rope, dim3(static_cast<unsigned>(a.rows), static_cast<unsigned>(a.heads)), dim3(64), 0,
-                       s, a);
-    return hipGetLastError();
+    return launch(head_norm_rope, dim3(static_cast<unsigned>(a.rows), static_cast<unsigned>(a.heads)), dim3(64), s, a);
 }
 
 hipError_t launch_layer_prep(const LayerPrepArgs &a, hipStream_t s)
 {
-    hipLaunchKernelGGL(layer_prep, dim3(static_cast<unsigned>(a.rows), static_cast<unsigned>(a.heads + a.kv_heads)),
-                       dim3(64), 0, s, a);
-    return hipGetLastError();
+    return launch(layer_prep, dim3(static_cast<unsigned>(a.rows), static_cast<unsigned>(a.heads + a.kv_heads)),
+                  dim3(64), s, a);
 }
 
 hipError_t launch_gate(const GateArgs &a, hipStream_t s)
 {
     const uint64_t wgs = (a.rows * a.width + 255) / 256;
-    hipLaunchKernelGGL(output_gate, dim3(static_cast<unsigned>(wgs < 16384 ? wgs : 16384)), dim3(256), 0, s, a);
-    return hipGetLastError();
+    return launch(output_gate, dim3(static_cast<unsigned>(wgs < 16384 ? wgs : 16384)), dim3(256), s, a);
 }
 
 hipError_t launch_prefill(const PrefillArgs &a, int head_dim, int heads, const PrefillSplit &ps, hipStream_t s)
 {
     switch (head_dim) {
-    case 64: prefill_d<64>(a, heads, ps, s); break;
-    case 128: prefill_d<128>(a, heads, ps, s); break;
-    case 256: prefill_d<256>(a, heads, ps, s); break;
+    case 64: return prefill_d<64>(a, heads, ps, s);
+    case 128: return prefill_d<128>(a, heads, ps, s);
+    case 256: return prefill_d<256>(a, heads, ps, s);
     default: return launch_prefill_more(a, head_dim, heads, ps, s);
     }
-    return hipGetLastError();
 }
 
 }  // namespace hsdpa

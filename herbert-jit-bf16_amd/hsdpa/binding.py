@@ -19,12 +19,14 @@ STATUS = {
     0: "HSDPA_OK", 1: "HSDPA_ERR_EMPTY", 2: "HSDPA_ERR_HEAD_DIM", 3: "HSDPA_ERR_GQA",
     4: "HSDPA_ERR_STRIDE", 5: "HSDPA_ERR_SINK_UNSUPPORTED", 6: "HSDPA_ERR_CAPACITY",
     7: "HSDPA_ERR_WORKSPACE", 8: "HSDPA_ERR_ALIGNMENT", 9: "HSDPA_ERR_NULL", 10: "HSDPA_ERR_HIP",
-    11: "HSDPA_ERR_NO_DEVICE", 12: "HSDPA_ERR_BATCH", 13: "HSDPA_ERR_LAYOUT",
+    11: "HSDPA_ERR_NO_DEVICE", 12: "HSDPA_ERR_BATCH", 13: "HSDPA_ERR_LAYOUT", 14: "HSDPA_ERR_FORM",
 }
+FORMS = {"chained": 0, "fused": 1}
+KERNELS = {0: "none", 1: "decode", 2: "few_rows", 3: "causal", 4: "causal_split", 5: "decode_rows"}
 EXPORTS = ["hsdpa_plan_create", "hsdpa_plan_destroy", "hsdpa_workspace_bytes", "hsdpa_attention",
            "hsdpa_status_string", "hsdpa_version", "hsdpa_kv_check", "hsdpa_kv_append",
            "hsdpa_head_norm_rope", "hsdpa_output_gate", "hsdpa_kv_restore", "hsdpa_kv_take",
-           "hsdpa_attention_layer"]
+           "hsdpa_attention_layer", "hsdpa_attention_route"]
 
 
 class HsdpaError(RuntimeError):
@@ -38,7 +40,8 @@ class Spec(ctypes.Structure):
     _fields_ = [("heads", ctypes.c_uint64), ("gqa", ctypes.c_uint64), ("head_dim", ctypes.c_uint64),
                 ("q_row", ctypes.c_uint64), ("q_head", ctypes.c_uint64), ("out_row", ctypes.c_uint64),
                 ("kv_capacity", ctypes.c_uint64), ("kv_stride", ctypes.c_uint64),
-                ("grouped", ctypes.c_uint32), ("sink", ctypes.c_uint32)]
+                ("grouped", ctypes.c_uint32), ("sink", ctypes.c_uint32), ("form", ctypes.c_uint32),
+                ("reserved", ctypes.c_uint32), ("max_rows", ctypes.c_uint64)]
 
 
 class Call(ctypes.Structure):
@@ -46,6 +49,13 @@ class Call(ctypes.Structure):
                 ("output", ctypes.c_void_p), ("rows", ctypes.c_uint64), ("past", ctypes.c_uint64),
                 ("scale", ctypes.c_float), ("sink", ctypes.c_float), ("workspace", ctypes.c_void_p),
                 ("workspace_bytes", ctypes.c_uint64)]
+
+
+class Route(ctypes.Structure):
+    """hsdpa_route: the kernels a call would run."""
+    _fields_ = [("main", ctypes.c_uint32), ("main_form", ctypes.c_uint32), ("tail", ctypes.c_uint32),
+                ("tail_form", ctypes.c_uint32), ("main_rows", ctypes.c_uint64), ("tail_rows", ctypes.c_uint64),
+                ("splits", ctypes.c_uint32), ("launches", ctypes.c_uint32)]
 
 
 class KvSpec(ctypes.Structure):
@@ -132,6 +142,8 @@ def library():
         L.hsdpa_kv_take.restype = ctypes.c_int
         L.hsdpa_attention_layer.argtypes = [ctypes.c_void_p, ctypes.POINTER(LayerCall), ctypes.c_void_p]
         L.hsdpa_attention_layer.restype = ctypes.c_int
+        L.hsdpa_attention_route.argtypes = [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_uint64, ctypes.POINTER(Route)]
+        L.hsdpa_attention_route.restype = ctypes.c_int
         _lib = L
     return _lib
 
@@ -142,13 +154,14 @@ class Plan:
 
     def __init__(self, heads: int, gqa: int, head_dim: int, kv_capacity: int, q_row: int | None = None,
                  q_head: int | None = None, out_row: int | None = None, kv_stride: int | None = None,
-                 grouped: bool = False, sink: bool = False):
+                 grouped: bool = False, sink: bool = False, form: str | int = "chained", max_rows: int = 0):
+        form_code = FORMS[form] if isinstance(form, str) else int(form)
         self.spec = Spec(heads, gqa, head_dim,
                          heads * head_dim if q_row is None else q_row,
                          head_dim if q_head is None else q_head,
                          heads * head_dim if out_row is None else out_row,
                          kv_capacity, kv_capacity * head_dim if kv_stride is None else kv_stride,
-                         int(grouped), int(sink))
+                         int(grouped), int(sink), form_code, 0, max_rows)
         self._h = ctypes.c_void_p()
         rc = library().hsdpa_plan_create(ctypes.byref(self.spec), ctypes.byref(self._h))
         if rc != 0:
@@ -161,6 +174,16 @@ class Plan:
     @property
     def workspace_bytes(self) -> int:
         return int(library().hsdpa_workspace_bytes(self._h))
+
+    def route(self, rows: int, past: int) -> dict:
+        """The kernels a call of `rows` rows after `past` positions would run."""
+        r = Route()
+        rc = library().hsdpa_attention_route(self._h, rows, past, ctypes.byref(r))
+        if rc != 0:
+            raise HsdpaError(rc, "hsdpa_attention_route")
+        return {"main": KERNELS[r.main], "main_form": "fused" if r.main_form else "chained",
+                "tail": KERNELS[r.tail], "tail_form": "fused" if r.tail_form else "chained",
+                "main_rows": r.main_rows, "tail_rows": r.tail_rows, "splits": r.splits, "launches": r.launches}
 
     def attention_raw(self, q: int, keys: int, values: int, output: int, rows: int, past: int, scale: float,
                       workspace: int, workspace_bytes: int, stream: int = 0, sink: float = 0.0) -> None:

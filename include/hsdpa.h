@@ -77,9 +77,27 @@ typedef enum hsdpa_status {
     HSDPA_ERR_NULL = 9,             /* a required pointer is null */
     HSDPA_ERR_HIP = 10,             /* a HIP launch or runtime call failed */
     HSDPA_ERR_NO_DEVICE = 11,       /* no gfx950 device current */
-    HSDPA_ERR_BATCH = 12,           /* kv append: rows > max_batch (the frame's bound) */
-    HSDPA_ERR_LAYOUT = 13           /* kv append: the R16 copies, an AArch64 layout (kv.rs:19-21) */
+    HSDPA_ERR_BATCH = 12,           /* kv append: rows > max_batch (the frame's bound);
+                                       attention: rows > the plan's max_rows */
+    HSDPA_ERR_LAYOUT = 13,          /* kv append: the R16 copies, an AArch64 layout (kv.rs:19-21) */
+    HSDPA_ERR_FORM = 14             /* an unknown decode form (the knob's parse, knobs.rs:66-68) */
 } hsdpa_status;
+
+/* The decode head form (SdpaForm, src/jit/ir.rs:100-115; the knob
+ * sdpa_form, src/jit/knobs.rs:66-68). Chained is the reference's default:
+ * the exponentials at the row maximum, divided by their sum. Fused is its
+ * online softmax over blocks of 16 positions
+ * (src/jit/target/x86/emit_sdpa/x86/decode.rs:501-669): each block's
+ * exponentials at the running maximum so far, the accumulators rescaled by
+ * P(m_old - m_new), the sum's reciprocal at the end. Under Fused, like the
+ * reference, the rows the engine serves with its prefill block (full chunks
+ * of 8 rows) keep the Chained numerics; the other rows (a decode row, the
+ * last rows % 8 of a chunk) take the Fused ones; above head_dim 256 the form
+ * falls back to Chained (src/jit/sdpa.rs:491-510). */
+typedef enum hsdpa_form {
+    HSDPA_FORM_CHAINED = 0,
+    HSDPA_FORM_FUSED = 1
+} hsdpa_form;
 
 /* Per-layer geometry, fixed at mount (AttentionSpec + cache reserve). */
 typedef struct hsdpa_spec {
@@ -93,6 +111,11 @@ typedef struct hsdpa_spec {
     uint64_t kv_stride;    /* elements between two KV heads of one cache (>= kv_capacity*head_dim) */
     uint32_t grouped;      /* AttentionSpec::grouped: task order only, no effect on results */
     uint32_t sink;         /* SdpaShape::sink: must be 0 */
+    uint32_t form;         /* hsdpa_form */
+    uint32_t reserved;     /* 0 */
+    uint64_t max_rows;     /* the most rows one call will pass (0: any, up to kv_capacity); sizes the
+                              workspace, like KvSpec::max_batch bounds the frame (abi.rs:57-73):
+                              1 gives a decode-only plan with a workspace of a few MiB */
 } hsdpa_spec;
 
 /* One call of the node (AttentionCall). rows and past are values here: the
@@ -118,15 +141,43 @@ hsdpa_status hsdpa_plan_create(const hsdpa_spec *spec, hsdpa_plan **out);
 
 void hsdpa_plan_destroy(hsdpa_plan *plan);
 
-/* Device scratch a call of this plan needs, for any rows and past within
- * kv_capacity. Calls that may run concurrently need distinct workspaces. */
+/* Device scratch a call of this plan needs, for any rows (up to max_rows) and
+ * past within kv_capacity. Calls that may run concurrently need distinct
+ * workspaces. */
 uint64_t hsdpa_workspace_bytes(const hsdpa_plan *plan);
+
+/* The kernels a call of `rows` rows after `past` positions would run, without
+ * running them (the reference prints its plan under HERBERT_JIT_DEBUG_PLAN,
+ * src/jit/sdpa.rs:291-306). A call may take two routes: its leading rows on
+ * `main`, its last `tail_rows` rows on `tail` (the Fused form's rows outside
+ * full chunks of 8). */
+typedef enum hsdpa_kernels {
+    HSDPA_KERNELS_NONE = 0,
+    HSDPA_KERNELS_DECODE = 1,         /* one row on the decode passes (scores, P.V, combine) */
+    HSDPA_KERNELS_FEW_ROWS = 2,       /* a few rows as (row, head) columns of the decode passes */
+    HSDPA_KERNELS_CAUSAL = 3,         /* the causal kernel, one workgroup per row group */
+    HSDPA_KERNELS_CAUSAL_SPLIT = 4,   /* the causal kernel split over the keys (maxima, P.V, combine) */
+    HSDPA_KERNELS_DECODE_ROWS = 5     /* one decode per row, in turn */
+} hsdpa_kernels;
+
+typedef struct hsdpa_route {
+    uint32_t main;          /* hsdpa_kernels of the leading rows */
+    uint32_t main_form;     /* hsdpa_form of their numerics */
+    uint32_t tail;          /* hsdpa_kernels of the last tail_rows rows (NONE: no tail) */
+    uint32_t tail_form;
+    uint64_t main_rows, tail_rows;
+    uint32_t splits;        /* key splits of CAUSAL_SPLIT, else 1 */
+    uint32_t launches;      /* kernel launches of the whole call */
+} hsdpa_route;
+
+hsdpa_status hsdpa_attention_route(const hsdpa_plan *plan, uint64_t rows, uint64_t past, hsdpa_route *out);
 
 /* The whole attention node: every query head of every row, the decode kernels
  * when rows == 1 (and for up to 8 rows at head_dim 64, 128 and 256 while
  * rows * gqa <= 64), causal prefill otherwise, enqueued on `stream` (a hipStream_t;
  * NULL is the default stream). Validation happens on the host before any
- * launch; nothing is allocated. */
+ * launch; nothing is allocated. HSDPA_ERR_HIP after a launch was enqueued
+ * leaves the output rows unspecified. */
 hsdpa_status hsdpa_attention(const hsdpa_plan *plan, const hsdpa_call *call, void *stream);
 
 /* ---- KV append: the node before the attention ------------------------------

@@ -119,7 +119,7 @@ def attention(w, impl: str = "auto", threads: int = 0, form: str = "chained") ->
     when the host has it, which is bit-identical to the scalar one).
     form: 'chained' (the engine's default), 'fused' (the knob's online
     softmax) or 'avx2' (a host without AVX-512 BF16); the last two run the
-    scalar emulation on `threads` threads (0: all cores)."""
+    scalar emulation on `threads` threads (0: the host's cores, at most 16)."""
     L = lib()
     if form != "chained":
         out = np.zeros((w.rows, w.heads, w.head_dim), dtype=np.uint16)
@@ -129,7 +129,7 @@ def attention(w, impl: str = "auto", threads: int = 0, form: str = "chained") ->
         spec = Spec(w.heads, w.gqa, w.head_dim, w.q_row, w.head_dim, w.out_row)
         call = Call(_ptr(q), _ptr(k), _ptr(v), _ptr(out), w.rows, w.past, w.kv_stride, w.scale, 0.0)
         rc = L.oracle_attention_form(ctypes.byref(spec), ctypes.byref(call), FORMS[form],
-                                     threads or (os.cpu_count() or 1))
+                                     threads or min(16, os.cpu_count() or 1))
         if rc != 0:
             raise RuntimeError(f"oracle attention ({form}) failed rc={rc}")
         return out

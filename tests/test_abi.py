@@ -45,9 +45,9 @@ def test_library_has_gfx950_code():
 
 def test_status_strings_and_version():
     lib = hsdpa.library()
-    for code in range(12):
-        assert lib.hsdpa_status_string(code)
-    assert lib.hsdpa_version() >= 100
+    for code in range(15):
+        assert lib.hsdpa_status_string(code) != b"unknown status", code
+    assert lib.hsdpa_version() >= 200
 
 
 @pytest.mark.parametrize("kw,code", [
@@ -65,6 +65,8 @@ def test_status_strings_and_version():
     (dict(heads=16, gqa=8, head_dim=256, kv_capacity=10, kv_stride=2000), "HSDPA_ERR_STRIDE"),
     (dict(heads=16, gqa=8, head_dim=256, kv_capacity=0), "HSDPA_ERR_CAPACITY"),
     (dict(heads=16, gqa=8, head_dim=256, kv_capacity=10, q_row=16 * 256 + 4), "HSDPA_ERR_ALIGNMENT"),
+    (dict(heads=16, gqa=8, head_dim=256, kv_capacity=10, form=2), "HSDPA_ERR_FORM"),
+    (dict(heads=16, gqa=8, head_dim=256, kv_capacity=10, max_rows=11), "HSDPA_ERR_CAPACITY"),
 ])
 def test_plan_refusals(kw, code):
     with pytest.raises(hsdpa.HsdpaError) as e:
@@ -86,6 +88,54 @@ def test_workspace_grows_with_capacity():
     a = hsdpa.Plan(16, 8, 256, 1024).workspace_bytes
     b = hsdpa.Plan(16, 8, 256, 32768).workspace_bytes
     assert b > a and b % 256 == 0
+
+
+def test_workspace_follows_max_rows_and_form():
+    """A plan sized for what it serves: a decode-only plan (max_rows 1) needs
+    the scores, the pass-1 maxima and one round of pass-2 partials, a few MiB
+    at 32K keys; any rows adds the few-rows columns and the split causal
+    kernel's cells; the Fused form adds the 16-key block maxima and the
+    partials' correction products."""
+    any_rows = hsdpa.Plan(16, 8, 256, 32768).workspace_bytes
+    decode = hsdpa.Plan(16, 8, 256, 32768, max_rows=1).workspace_bytes
+    fused = hsdpa.Plan(16, 8, 256, 32768, max_rows=1, form="fused").workspace_bytes
+    # scores 2 x 8 x 32768 f32, partials of 128 workgroups x 8 columns x 256 f32 per KV head
+    assert 2 * 8 * 32768 * 4 + 2 * 128 * 8 * 256 * 4 <= decode < 5 << 20
+    assert any_rows > 10 * decode
+    assert fused - decode >= 2 * 8 * (32768 // 16) * 4
+    # no split cells where every call runs on the decode kernels
+    assert hsdpa.Plan(16, 8, 256, 32768, max_rows=8).workspace_bytes < 40 << 20
+
+
+def test_route_names_the_kernels():
+    """hsdpa_attention_route reports what a call would run, with no device:
+    the decode passes for one row, (row, head) columns for a few rows, the
+    causal kernel or its split form otherwise; under the Fused form the rows
+    outside full chunks of 8 take the Fused numerics on the decode kernels."""
+    p = hsdpa.Plan(16, 8, 256, 40000)
+    assert p.route(1, 32767)["main"] == "decode"
+    assert p.route(4, 100)["main"] == "few_rows"
+    r = p.route(4096, 8192)
+    assert r["main"] == "causal" and r["launches"] == 1 and r["tail"] == "none"
+    r = p.route(256, 32768)
+    assert r["main"] == "causal_split" and r["splits"] > 1 and r["launches"] == 3
+    f = hsdpa.Plan(16, 8, 256, 40000, form="fused")
+    assert f.route(1, 100)["main_form"] == "fused"
+    assert f.route(7, 100)["main_form"] == "fused"
+    assert f.route(8, 100)["main_form"] == "chained"          # a full chunk: the block kernel's numerics
+    r = f.route(13, 100)
+    assert (r["main_rows"], r["main_form"], r["tail_rows"], r["tail"], r["tail_form"]) == \
+        (8, "chained", 5, "few_rows", "fused")
+    r = f.route(4096 + 3, 8192)
+    assert (r["main"], r["tail"], r["tail_rows"], r["tail_form"]) == ("causal", "few_rows", 3, "fused")
+    # above head_dim 256 the Fused form falls back to Chained
+    assert hsdpa.Plan(4, 2, 288, 100, form="fused").route(1, 10)["main_form"] == "chained"
+    # a group the decode kernels cannot take keeps the causal kernel (and the Chained numerics)
+    r = hsdpa.Plan(17, 17, 128, 100, form="fused").route(1, 10)
+    assert r["main"] == "causal" and r["main_form"] == "chained"
+    # one row per decode where the tail does not fit the decode columns
+    r = hsdpa.Plan(32, 16, 128, 1000, form="fused").route(13, 100)
+    assert r["tail"] == "decode_rows" and r["tail_form"] == "fused" and r["launches"] == 1 + 5 * 3
 
 
 def _call(plan, rows=1, past=0, scale=0.0625, sink=0.0, ws_bytes=None, q=0x10000, k=0x20000, v=0x30000,
@@ -111,6 +161,8 @@ def test_call_refusals_before_any_device_work():
     assert _name(_call(p, k=0x20002)) == "HSDPA_ERR_ALIGNMENT"
     assert _name(_call(p, ws_bytes=16)) == "HSDPA_ERR_WORKSPACE"
     assert hsdpa.library().hsdpa_attention(None, None, None) == 9
+    one = hsdpa.Plan(16, 8, 256, 100, max_rows=1)
+    assert _name(_call(one, rows=2)) == "HSDPA_ERR_BATCH"
 
 
 def test_call_without_gpu_fails_loudly():
@@ -154,7 +206,7 @@ RECORDS = {
     "hsdpa_spec": binding.Spec, "hsdpa_call": binding.Call, "hsdpa_kv_spec": binding.KvSpec,
     "hsdpa_kv_call": binding.KvCall, "hsdpa_norm_rope_spec": binding.NormRopeSpec,
     "hsdpa_norm_rope_call": binding.NormRopeCall, "hsdpa_gate_spec": binding.GateSpec,
-    "hsdpa_gate_call": binding.GateCall, "hsdpa_layer_call": binding.LayerCall,
+    "hsdpa_gate_call": binding.GateCall, "hsdpa_layer_call": binding.LayerCall, "hsdpa_route": binding.Route,
 }
 
 

@@ -3,6 +3,7 @@ CPU restatement of the reference's emitted SDPA, on identical seeded inputs."""
 import numpy as np
 import pytest
 
+import hsdpa
 import oracle
 from hsdpa import workloads as W
 from parity import assert_parity
@@ -12,43 +13,45 @@ from gpu_util import run_hsdpa
 pytestmark = pytest.mark.gpu
 
 SMALL = [
-    # name, heads, kv_heads, head_dim, rows, past
-    ("decode_d256_n1", 8, 2, 256, 1, 0),
-    ("decode_d256_n37", 8, 2, 256, 1, 36),
-    ("decode_d128_n300", 16, 4, 128, 1, 299),
-    ("decode_d64_g1", 4, 4, 64, 1, 77),
-    ("prefill_d256_r2", 8, 2, 256, 2, 0),
-    ("prefill_d256_r19_p37", 8, 2, 256, 19, 37),
-    ("prefill_d128_r70_p5", 8, 8, 128, 70, 5),
-    ("prefill_d64_r33_p100_g2", 8, 4, 64, 33, 100),
-    ("prefill_d256_r129_p0_g3", 6, 2, 256, 129, 0),
+    # name, heads, kv_heads, head_dim, rows, past, the kernels the call must take
+    ("decode_d256_n1", 8, 2, 256, 1, 0, "decode"),
+    ("decode_d256_n37", 8, 2, 256, 1, 36, "decode"),
+    ("decode_d128_n300", 16, 4, 128, 1, 299, "decode"),
+    ("decode_d64_g1", 4, 4, 64, 1, 77, "decode"),
+    ("prefill_d256_r2_g40", 80, 2, 256, 2, 0, "causal"),              # 80 columns: past the decode kernels
+    ("prefill_d256_r19_p37", 8, 2, 256, 19, 37, "causal"),
+    ("prefill_d128_r70_p5", 8, 8, 128, 70, 5, "causal"),
+    ("prefill_d64_r33_p100_g2", 8, 4, 64, 33, 100, "causal"),
+    ("prefill_d256_r129_p0_g3", 6, 2, 256, 129, 0, "causal"),
     # pass 1 in several rounds per workgroup, the last workgroup partial
-    ("decode_d256_n50001_two_rounds", 16, 2, 256, 1, 50000),
-    ("decode_d128_n70001_five_rounds", 16, 4, 128, 1, 70000),
+    ("decode_d256_n50001_two_rounds", 16, 2, 256, 1, 50000, "decode"),
+    ("decode_d128_n70001_five_rounds", 16, 4, 128, 1, 70000, "decode"),
     # two tiles per wave once one tile per wave needs more than a workgroup per CU
-    ("decode_d256_n20001_two_tiles", 16, 2, 256, 1, 20000),
-    ("decode_d128_n9000_kv4_two_tiles", 16, 4, 128, 1, 8999),
+    ("decode_d256_n20001_two_tiles", 16, 2, 256, 1, 20000, "decode"),
+    ("decode_d128_n9000_kv4_two_tiles", 16, 4, 128, 1, 8999, "decode"),
     # pass 2 in chunks, one round of workgroups, the last chunk of each run partial
-    ("decode_d256_n40001_chunked", 16, 2, 256, 1, 40000),
-    ("decode_d128_kv8_n9000_chunked", 64, 8, 128, 1, 8999),
-    ("decode_d128_g16_n20001_chunked", 64, 4, 128, 1, 20000),   # two P column blocks
+    ("decode_d256_n40001_chunked", 16, 2, 256, 1, 40000, "decode"),
+    ("decode_d128_kv8_n9000_chunked", 64, 8, 128, 1, 8999, "decode"),
+    ("decode_d128_g16_n20001_chunked", 64, 4, 128, 1, 20000, "decode"),   # two P column blocks
     # short chunks after long caches: the causal kernel split over the keys
-    ("prefill_split_d256_r64_p3000", 16, 2, 256, 64, 3000),
-    ("prefill_split_d256_r300_p9000", 16, 2, 256, 300, 9000),
-    ("prefill_split_d128_r100_p5000_g4", 16, 4, 128, 100, 5000),
-    ("prefill_split_d64_r40_p2000_g2", 8, 4, 64, 40, 2000),
-    ("prefill_split_d96_r50_p4000", 8, 2, 96, 50, 4000),
-    ("prefill_split_d384_r33_p2500", 4, 2, 384, 33, 2500),
-    ("prefill_split_d256_r7_p257_uneven", 8, 2, 256, 7, 257),
+    ("prefill_split_d256_r64_p3000", 16, 2, 256, 64, 3000, "causal_split"),
+    ("prefill_split_d256_r300_p9000", 16, 2, 256, 300, 9000, "causal_split"),
+    ("prefill_split_d128_r100_p5000_g4", 16, 4, 128, 100, 5000, "causal_split"),
+    ("prefill_split_d64_r40_p2000_g2", 8, 4, 64, 40, 2000, "causal_split"),
+    ("prefill_split_d96_r50_p4000", 8, 2, 96, 50, 4000, "causal_split"),
+    ("prefill_split_d384_r33_p2500", 4, 2, 384, 33, 2500, "causal_split"),
+    ("prefill_split_d256_r7_p257_uneven_g40", 80, 2, 256, 7, 257, "causal_split"),   # 9 tiles over 2 splits
 ]
 
 
 @pytest.mark.parametrize("case", SMALL, ids=[c[0] for c in SMALL])
 def test_small_shapes(torch_cuda, case):
-    name, h, kvh, d, rows, past = case
+    name, h, kvh, d, rows, past, kernels = case
     w = W.make(name, heads=h, kv_heads=kvh, head_dim=d, rows=rows, past=past, seed=11)
+    plan = hsdpa.Plan(w.heads, w.gqa, w.head_dim, w.capacity)
+    assert plan.route(rows, past)["main"] == kernels, plan.route(rows, past)
     print(f"case {name}", flush=True)
-    out = run_hsdpa(w)
+    out = run_hsdpa(w, plan)
     ref = oracle.attention(w)
     r = assert_parity(out, ref, w, name)
     print(name, r, flush=True)
