@@ -642,6 +642,25 @@ hsdpa_status hsdpa_attention(const hsdpa_plan *plan, const hsdpa_call *call, voi
     return run_attention(plan, call, nullptr, 0, static_cast<hipStream_t>(stream), true, nullptr);
 }
 
+hsdpa_status hsdpa_attention_static(const hsdpa_plan *plan, const hsdpa_call *call, void *stream)
+{
+    if (!plan || !call) return HSDPA_ERR_NULL;
+    if (call->sink != 0.0f) return HSDPA_ERR_SINK_UNSUPPORTED;
+    if (call->rows == 0) return HSDPA_OK;
+    if (plan->ws_bytes > HSDPA_STATIC_SCRATCH_BYTES) return HSDPA_ERR_STATIC_SCRATCH;
+    int cus = 0;
+    const hsdpa_status dev = check_device(&cus);
+    if (dev != HSDPA_OK) return dev;
+    void *scratch = nullptr;
+    if (hsdpa::static_scratch(&scratch) != hipSuccess) return HSDPA_ERR_HIP;
+    hsdpa_call c = *call;
+    c.workspace = scratch;
+    c.workspace_bytes = HSDPA_STATIC_SCRATCH_BYTES;
+    const hsdpa_status st = check_attention_call(plan, &c);
+    if (st != HSDPA_OK) return st;
+    return run_attention(plan, &c, nullptr, 0, static_cast<hipStream_t>(stream), true, nullptr);
+}
+
 hsdpa_status hsdpa_attention_route(const hsdpa_plan *plan, uint64_t rows, uint64_t past, hsdpa_route *out)
 {
     if (!plan || !out) return HSDPA_ERR_NULL;
@@ -735,6 +754,7 @@ const char *hsdpa_status_string(hsdpa_status status)
     case HSDPA_ERR_BATCH: return "more rows than the reserve's max_batch or the plan's max_rows";
     case HSDPA_ERR_LAYOUT: return "the R16 copies of the KV cache are an AArch64 layout";
     case HSDPA_ERR_FORM: return "unknown decode form";
+    case HSDPA_ERR_STATIC_SCRATCH: return "the plan's workspace exceeds the static scratch (HSDPA_STATIC_SCRATCH_BYTES)";
     }
     return "unknown status";
 }

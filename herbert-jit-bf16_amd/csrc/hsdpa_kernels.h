@@ -183,6 +183,9 @@ int prefill_split_count(const PrefillArgs &a, int head_dim, int heads, const Pre
 hipError_t launch_decode_more(const DecodeArgs &a, int head_dim, int kv_heads, hipStream_t s);
 // the Fused form of the decode passes, head dimensions 32 to 256 (hsdpa_fused.hip)
 hipError_t launch_decode_fused(const DecodeArgs &a, int head_dim, int kv_heads, hipStream_t s);
+// the current device's copy of the static scratch of hsdpa_attention_static
+// (hsdpa_static.hip)
+hipError_t static_scratch(void **ptr);
 // the pass-2 workgroups a Fused combine can scan per head (its LDS)
 constexpr int kFusedMaxSeg = 512;
 hipError_t launch_prefill_more(const PrefillArgs &a, int head_dim, int heads, const PrefillSplit &ps, hipStream_t s);

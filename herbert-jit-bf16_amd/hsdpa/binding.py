@@ -20,13 +20,15 @@ STATUS = {
     4: "HSDPA_ERR_STRIDE", 5: "HSDPA_ERR_SINK_UNSUPPORTED", 6: "HSDPA_ERR_CAPACITY",
     7: "HSDPA_ERR_WORKSPACE", 8: "HSDPA_ERR_ALIGNMENT", 9: "HSDPA_ERR_NULL", 10: "HSDPA_ERR_HIP",
     11: "HSDPA_ERR_NO_DEVICE", 12: "HSDPA_ERR_BATCH", 13: "HSDPA_ERR_LAYOUT", 14: "HSDPA_ERR_FORM",
+    15: "HSDPA_ERR_STATIC_SCRATCH",
 }
+STATIC_SCRATCH_BYTES = 32 << 20
 FORMS = {"chained": 0, "fused": 1}
 KERNELS = {0: "none", 1: "decode", 2: "few_rows", 3: "causal", 4: "causal_split", 5: "decode_rows"}
 EXPORTS = ["hsdpa_plan_create", "hsdpa_plan_destroy", "hsdpa_workspace_bytes", "hsdpa_attention",
            "hsdpa_status_string", "hsdpa_version", "hsdpa_kv_check", "hsdpa_kv_append",
            "hsdpa_head_norm_rope", "hsdpa_output_gate", "hsdpa_kv_restore", "hsdpa_kv_take",
-           "hsdpa_attention_layer", "hsdpa_attention_route"]
+           "hsdpa_attention_layer", "hsdpa_attention_route", "hsdpa_attention_static"]
 
 
 class HsdpaError(RuntimeError):
@@ -144,6 +146,8 @@ def library():
         L.hsdpa_attention_layer.restype = ctypes.c_int
         L.hsdpa_attention_route.argtypes = [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_uint64, ctypes.POINTER(Route)]
         L.hsdpa_attention_route.restype = ctypes.c_int
+        L.hsdpa_attention_static.argtypes = [ctypes.c_void_p, ctypes.POINTER(Call), ctypes.c_void_p]
+        L.hsdpa_attention_static.restype = ctypes.c_int
         _lib = L
     return _lib
 

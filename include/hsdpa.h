@@ -80,7 +80,9 @@ typedef enum hsdpa_status {
     HSDPA_ERR_BATCH = 12,           /* kv append: rows > max_batch (the frame's bound);
                                        attention: rows > the plan's max_rows */
     HSDPA_ERR_LAYOUT = 13,          /* kv append: the R16 copies, an AArch64 layout (kv.rs:19-21) */
-    HSDPA_ERR_FORM = 14             /* an unknown decode form (the knob's parse, knobs.rs:66-68) */
+    HSDPA_ERR_FORM = 14,            /* an unknown decode form (the knob's parse, knobs.rs:66-68) */
+    HSDPA_ERR_STATIC_SCRATCH = 15   /* hsdpa_attention_static: the plan's workspace exceeds
+                                       HSDPA_STATIC_SCRATCH_BYTES */
 } hsdpa_status;
 
 /* The decode head form (SdpaForm, src/jit/ir.rs:100-115; the knob
@@ -179,6 +181,22 @@ hsdpa_status hsdpa_attention_route(const hsdpa_plan *plan, uint64_t rows, uint64
  * launch; nothing is allocated. HSDPA_ERR_HIP after a launch was enqueued
  * leaves the output rows unspecified. */
 hsdpa_status hsdpa_attention(const hsdpa_plan *plan, const hsdpa_call *call, void *stream);
+
+/* The attention node without a caller workspace: as hsdpa_attention, with
+ * the library's own device scratch in place of call->workspace (the call's
+ * workspace and workspace_bytes are ignored). It has no counterpart in the
+ * reference; it is for callers that cannot allocate device memory: code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc.
+ * The scratch is one static array of HSDPA_STATIC_SCRATCH_BYTES per GPU,
+ * held until the process ends; a plan whose hsdpa_workspace_bytes exceeds it
+ * is refused (HSDPA_ERR_STATIC_SCRATCH) before any launch: a decode-only plan
+ * (max_rows = 1) fits up to about 400K cached positions at 16 query heads on 2
+ * KV heads of head_dim 256. The call allocates nothing (its first call on a
+ * device looks up that device's copy of the array). Every call on a GPU shares
+ * that GPU's array: calls that overlap on one GPU (different streams, or
+ * threads enqueueing at once) race on it; stream-ordered calls do not. */
+#define HSDPA_STATIC_SCRATCH_BYTES (32u << 20)
+hsdpa_status hsdpa_attention_static(const hsdpa_plan *plan, const hsdpa_call *call, void *stream);
 
 /* ---- KV append: the node before the attention ------------------------------
  * The keys and values of the current block, token-major (row r, KV head h at
