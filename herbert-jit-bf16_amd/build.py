@@ -20,9 +20,11 @@ SRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "hsdpa", "libhsdpa.so")
 # translation units, compiled in parallel and linked: the tuned attention
 # kernels and the element kernels, the attention kernels of the other head
-# dimensions, the decode passes under the Fused form, the static scratch of
-# the entry point that allocates nothing, the C ABI
-SOURCES = ["hsdpa_kernels.hip", "hsdpa_attn_more.hip", "hsdpa_fused.hip", "hsdpa_static.hip", "hsdpa_api.cpp"]
+# dimensions, the decode passes under the Fused form, the short-chunk
+# prefill, the static scratch of the entry point that allocates nothing, the
+# C ABI
+SOURCES = ["hsdpa_kernels.hip", "hsdpa_attn_more.hip", "hsdpa_fused.hip", "hsdpa_prefill_short.hip",
+           "hsdpa_static.hip", "hsdpa_api.cpp"]
 HIPCC = os.environ.get("HIPCC", shutil.which("hipcc") or "/opt/rocm/bin/hipcc")
 
 # -ffp-contract=off: the exponential and the score scaling must round exactly

@@ -555,6 +555,21 @@ static hsdpa_status run_part(const hsdpa_plan *plan, const hsdpa_call *call, con
     }
     ps.units = plan->split_units;
     ps.cus = plan->cus;
+    // a chunk the one-workgroup causal kernel would spread too thin (it would be
+    // split over its keys) and whose row blocks see few key tiles: the waves
+    // of each row block's workgroup split its keys instead, in one launch
+    hsdpa::PrefillSplit probe = ps;
+    probe.units = hsdpa::kSplitUnits;
+    const int sp_any = hsdpa::prefill_split_count(a, d, static_cast<int>(s.heads), probe);
+    const uint64_t ntiles = (n + hsdpa::kKeyTile - 1) / hsdpa::kKeyTile;
+    if (sp_any > 1 && hsdpa::prefill_short_ok(d) && ntiles <= static_cast<uint64_t>(hsdpa::kShortMaxTiles)) {
+        if (kernels) *kernels = HSDPA_KERNELS_CAUSAL_SHORT;
+        if (splits) *splits = 1;
+        if (launches) *launches += 1;
+        if (!launch) return HSDPA_OK;
+        const hipError_t e = hsdpa::launch_prefill_short(a, d, static_cast<int>(s.heads), st);
+        return e == hipSuccess ? HSDPA_OK : HSDPA_ERR_HIP;
+    }
     const int sp = hsdpa::prefill_split_count(a, d, static_cast<int>(s.heads), ps);
     if (kernels) *kernels = sp > 1 ? HSDPA_KERNELS_CAUSAL_SPLIT : HSDPA_KERNELS_CAUSAL;
     if (splits) *splits = static_cast<uint32_t>(sp);

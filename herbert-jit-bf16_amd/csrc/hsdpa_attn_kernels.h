@@ -1166,6 +1166,222 @@ __global__ __launch_bounds__(64 * NW, 1) void prefill_attn(PrefillArgs a)
 }
 
 // ---------------------------------------------------------------------------
+// Causal prefill of a short chunk, the keys of each row block split among the
+// waves of its workgroup: grid (row blocks of 32, heads), KS waves (one per
+// SIMD); wave k takes key tiles k, k + KS, ... (at most TPW) of its row block.
+// Pass 1 computes their scores once and keeps them in registers (TPW tiles of
+// 16 f32 per lane) with the wave's partial row maxima; the waves exchange
+// those through LDS into the exact row maximum; pass 2 takes the
+// exponentials of the kept scores (P = hi + lo) against V tiles into a
+// partial O and l. Each wave then posts its O to LDS and finishes a share of
+// the dimensions over all waves' partials, in a fixed order. Numerics follow
+// prefill_attn's (exponentials at the exact row maximum, P = hi + lo), with
+// Q.K^T in two accumulation chains and each row normalised by its
+// reciprocal: other f32 roundings, far below a bf16 ulp.
+// Where the one-workgroup causal kernel runs a row block's tiles one after
+// the other in every wave, so that the longest row block's tiles are its
+// critical path, and the split kernels pass f32 partials through memory,
+// this keeps the split inside the workgroup and computes Q.K^T once: for 512
+// rows with no cache, at most 4 tiles per wave, in one launch. Each wave
+// stages its own tiles (K rows padded to D + 8, V rows to D + 32) and loads
+// the next tile while computing this one.
+// ---------------------------------------------------------------------------
+template <int D, int KS, int TPW, bool POW2>
+__global__ __launch_bounds__(64 * KS, 1) void prefill_ks(PrefillArgs a)
+{
+    constexpr int SK = Pad<D>::K, SV = Pad<D>::V;
+    constexpr int TILE_U16 = kKeyTile * (SK + SV);               // one wave's K and V tile
+    constexpr int OFLOATS = (D / 32) * 16 * 64;                   // one wave's O partial
+    static_assert(KS * TILE_U16 * 2 >= KS * OFLOATS * 4, "the O partials fit the tile buffers");
+    __shared__ __attribute__((aligned(16))) uint16_t tiles[KS * TILE_U16];
+    __shared__ float mred[KS][32];
+    __shared__ float lred[KS][32];
+    const int wave = threadIdx.x >> 6, l = threadIdx.x & 63, col = l & 31, grp = l >> 5;
+    const int head = blockIdx.y, kvh = head / a.gqa;
+    const uint64_t rb = gridDim.x - 1 - blockIdx.x;             // heaviest row blocks first
+    const uint64_t r0 = rb * 32, row = r0 + col;
+    const bool rowv = row < a.rows;
+    const uint64_t rend = r0 + 32 < a.rows ? r0 + 32 : a.rows;
+    const int ntiles = static_cast<int>((a.past + rend + kKeyTile - 1) / kKeyTile);
+    const int nfull = static_cast<int>((a.past + r0 + 1) / kKeyTile);   // no mask needed below
+    const uint64_t lim = a.past + row;                          // last visible key of this row
+    uint16_t *kt = tiles + wave * TILE_U16;
+    uint16_t *vt = kt + kKeyTile * SK;
+
+    const uint16_t *kg = a.k + static_cast<uint64_t>(kvh) * a.kv_stride;
+    const uint16_t *vg = a.v + static_cast<uint64_t>(kvh) * a.kv_stride;
+    // this wave's tiles are its own LDS rows: LDS operations of one wave
+    // complete in order, so only the compiler has to be kept from reordering
+    auto wave_sync = [&]() {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    };
+    u32x4 kr[Tile<D, 64>::kPer], vr[Tile<D, 64>::kPer];
+    tile_gload<D, 64, false>(kg, static_cast<uint64_t>(wave) * kKeyTile, a.n, l, kr);
+
+    // pass 1: the scores of this wave's tiles (unscaled dot products when
+    // POW2), kept, and their row maxima
+    f32x16 sc[TPW];
+    float m = kNegInf;
+    {
+        u32x4 qb[D / 16];
+        const uint16_t *qp = a.q + (rowv ? row : 0) * a.q_row + static_cast<uint64_t>(head) * a.q_head;
+#pragma unroll
+        for (int s = 0; s < D / 16; s++) {
+            const u32x4 v = load16(qp + 16 * s + 8 * grp);
+            qb[s] = rowv ? v : u32x4{0, 0, 0, 0};
+        }
+        const int arow = swap23(col) * SK + 8 * grp;
+#pragma unroll
+        for (int i = 0; i < TPW; i++) {
+            const int t = wave + KS * i;
+            if (t < ntiles) {
+                const uint64_t t0 = static_cast<uint64_t>(t) * kKeyTile;
+                tile_lstore_padded<D, 64>(kt, SK, l, kr);
+                wave_sync();
+                // the next tile's K, or after the last one the first pass-2 V tile
+                if (t + KS < ntiles) tile_gload<D, 64, false>(kg, t0 + KS * kKeyTile, a.n, l, kr);
+                else tile_gload<D, 64, false>(vg, static_cast<uint64_t>(wave) * kKeyTile, a.n, l, vr);
+                // every K operand read issued before the first MFMA: with one
+                // wave per SIMD nothing else hides an LDS round trip per MFMA
+                u32x4 ka[D / 16];
+#pragma unroll
+                for (int s = 0; s < D / 16; s++) ka[s] = load16(kt + arow + 16 * s);
+                __builtin_amdgcn_sched_barrier(0);
+                // two accumulation chains: one wave per SIMD has no other wave
+                // to fill a dependent chain's gaps
+                f32x16 acc0 = {}, acc1 = {};
+#pragma unroll
+                for (int s = 0; s < D / 16; s += 2) {
+                    acc0 = mfma(ka[s], qb[s], acc0);
+                    acc1 = mfma(ka[s + 1], qb[s + 1], acc1);
+                }
+                const f32x16 acc = acc0 + acc1;
+                sc[i] = acc;
+                if (t < nfull) {
+#pragma unroll
+                    for (int r = 0; r < 16; r++) m = __builtin_fmaxf(m, POW2 ? acc[r] : acc[r] * a.scale);
+                } else {
+                    const int vis = static_cast<int>(static_cast<int64_t>(lim) - static_cast<int64_t>(t0));
+#pragma unroll
+                    for (int r = 0; r < 16; r++) {
+                        const float x = POW2 ? acc[r] : acc[r] * a.scale;
+                        if (key_of(r, grp) <= vis) m = __builtin_fmaxf(m, x);
+                    }
+                }
+                wave_sync();
+            }
+        }
+    }
+    // a wave with no tile still loads its (clamped, unused) first V tile
+    if (wave >= ntiles) tile_gload<D, 64, false>(vg, 0, a.n, l, vr);
+    m = __builtin_fmaxf(m, __shfl_xor(m, 32));
+    if (grp == 0) mred[wave][col] = m;
+    __syncthreads();
+#pragma unroll
+    for (int w = 0; w < KS; w++) m = __builtin_fmaxf(m, mred[w][col]);
+    // rows past the chunk: a finite maximum, their outputs are never stored
+    if (!rowv) m = 0.0f;
+    ExpArgs ex;
+    ex.m = m;
+    ex.scale = a.scale;
+    ex.clamp = POW2 ? -87.33654f / a.scale : -87.33654f;
+    ex.mul = POW2 ? 1.442695f * a.scale : 1.442695f;
+
+    // pass 2: exponentials of the kept scores at the exact maximum, P.V with
+    // P = hi + lo
+    f32x16 o[D / 32];
+#pragma unroll
+    for (int dt = 0; dt < D / 32; dt++) o[dt] = f32x16{};
+    float lsum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < TPW; i++) {
+        const int t = wave + KS * i;
+        if (t < ntiles) {
+            const uint64_t t0 = static_cast<uint64_t>(t) * kKeyTile;
+            tile_mask<D, 64>(t0, a.n, l, vr);
+            tile_lstore_padded<D, 64>(vt, SV, l, vr);
+            wave_sync();
+            if (t + KS < ntiles) tile_gload<D, 64, false>(vg, t0 + KS * kKeyTile, a.n, l, vr);
+            const bool full = t < nfull;
+            const int vis = static_cast<int>(static_cast<int64_t>(lim) - static_cast<int64_t>(t0));
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                // the V^T operands of this half are read while its exponentials are computed
+                u32x4 av[D / 32];
+#pragma unroll
+                for (int dt = 0; dt < D / 32; dt++) av[dt] = vt_operand_padded<D>(vt, 16 * h, 32 * dt, l);
+                float ev[8];
+#pragma unroll
+                for (int r = 0; r < 8; r++) {
+                    const float e = exp_score<POW2>(sc[i][8 * h + r], ex);
+                    ev[r] = full || key_of(8 * h + r, grp) <= vis ? e : 0.0f;
+                    lsum += ev[r];
+                }
+                u32x4 hi, lo;
+                split_pack_hw(ev, hi, lo);
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int dt = 0; dt < D / 32; dt++) {
+                    o[dt] = mfma(av[dt], hi, o[dt]);
+                    o[dt] = mfma(av[dt], lo, o[dt]);
+                }
+            }
+            wave_sync();
+        }
+    }
+    lsum += __shfl_xor(lsum, 32);
+    if (grp == 0) lred[wave][col] = lsum;
+    // every wave posts its O partial; wave w then finishes dimension blocks
+    // w, w + KS, ... over the partials of waves 0 .. KS-1 in that order
+    float *ox = reinterpret_cast<float *>(tiles);
+    __syncthreads();
+    {
+        float *dst = ox + wave * OFLOATS;
+#pragma unroll
+        for (int dt = 0; dt < D / 32; dt++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) dst[(dt * 16 + r) * 64 + l] = o[dt][r];
+    }
+    __syncthreads();
+    if (rowv) {
+        float L = 0.0f;
+#pragma unroll
+        for (int w = 0; w < KS; w++) L += lred[w][col];
+        // one division per row, then products (one more rounding, far below a
+        // bf16 ulp)
+        const float inv = 1.0f / L;
+        uint16_t *op = a.out + row * a.out_row + static_cast<uint64_t>(head) * D;
+        const uint16_t *gp = a.gate ? a.gate + row * a.gate_row + static_cast<uint64_t>(head) * D : nullptr;
+        for (int dt = wave; dt < D / 32; dt += KS) {
+            float f[16];
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                float x = ox[(dt * 16 + r) * 64 + l];
+#pragma unroll
+                for (int w = 1; w < KS; w++) x += ox[w * OFLOATS + (dt * 16 + r) * 64 + l];
+                f[r] = x;
+            }
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                uint32_t b0 = cvt_out(f[4 * c] * inv), b1 = cvt_out(f[4 * c + 1] * inv);
+                uint32_t b2 = cvt_out(f[4 * c + 2] * inv), b3 = cvt_out(f[4 * c + 3] * inv);
+                const int at = 32 * dt + 8 * c + 4 * grp;
+                if (gp) {
+                    const uint2 g = *reinterpret_cast<const uint2 *>(gp + at);
+                    b0 = gate_bf16(static_cast<uint16_t>(b0), static_cast<uint16_t>(g.x));
+                    b1 = gate_bf16(static_cast<uint16_t>(b1), static_cast<uint16_t>(g.x >> 16));
+                    b2 = gate_bf16(static_cast<uint16_t>(b2), static_cast<uint16_t>(g.y));
+                    b3 = gate_bf16(static_cast<uint16_t>(b3), static_cast<uint16_t>(g.y >> 16));
+                }
+                *reinterpret_cast<uint2 *>(op + at) = uint2{b0 | (b1 << 16), b2 | (b3 << 16)};
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Causal prefill split over the keys, for chunks whose grid of (row group,
 // head group) workgroups leaves compute units idle (a short chunk after a long
 // cache): gridDim.z workgroups share a row group's key tiles, tile range

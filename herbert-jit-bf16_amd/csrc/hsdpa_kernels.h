@@ -183,6 +183,15 @@ int prefill_split_count(const PrefillArgs &a, int head_dim, int heads, const Pre
 hipError_t launch_decode_more(const DecodeArgs &a, int head_dim, int kv_heads, hipStream_t s);
 // the Fused form of the decode passes, head dimensions 32 to 256 (hsdpa_fused.hip)
 hipError_t launch_decode_fused(const DecodeArgs &a, int head_dim, int kv_heads, hipStream_t s);
+// The causal prefill of a short chunk with the keys split among the waves of
+// each 32-row block's workgroup (hsdpa_prefill_short.hip), head dimensions 64,
+// 128 and 256: for chunks that would leave compute units idle, while each row
+// block sees at most kShortMaxTiles key tiles (beyond, the split kernels
+// spread the keys over more workgroups).
+constexpr int kShortWaves = 4;
+constexpr int kShortMaxTiles = 32;
+inline bool prefill_short_ok(int d) { return d == 64 || d == 128 || d == 256; }
+hipError_t launch_prefill_short(const PrefillArgs &a, int head_dim, int heads, hipStream_t s);
 // the current device's copy of the static scratch of hsdpa_attention_static
 // (hsdpa_static.hip)
 hipError_t static_scratch(void **ptr);

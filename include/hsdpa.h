@@ -159,7 +159,8 @@ typedef enum hsdpa_kernels {
     HSDPA_KERNELS_FEW_ROWS = 2,       /* a few rows as (row, head) columns of the decode passes */
     HSDPA_KERNELS_CAUSAL = 3,         /* the causal kernel, one workgroup per row group */
     HSDPA_KERNELS_CAUSAL_SPLIT = 4,   /* the causal kernel split over the keys (maxima, P.V, combine) */
-    HSDPA_KERNELS_DECODE_ROWS = 5     /* one decode per row, in turn */
+    HSDPA_KERNELS_DECODE_ROWS = 5,    /* one decode per row, in turn */
+    HSDPA_KERNELS_CAUSAL_SHORT = 6    /* a short chunk: each 32-row block's keys split among its waves */
 } hsdpa_kernels;
 
 typedef struct hsdpa_route {

@@ -40,7 +40,15 @@ SMALL = [
     ("prefill_split_d64_r40_p2000_g2", 8, 4, 64, 40, 2000, "causal_split"),
     ("prefill_split_d96_r50_p4000", 8, 2, 96, 50, 4000, "causal_split"),
     ("prefill_split_d384_r33_p2500", 4, 2, 384, 33, 2500, "causal_split"),
-    ("prefill_split_d256_r7_p257_uneven_g40", 80, 2, 256, 7, 257, "causal_split"),   # 9 tiles over 2 splits
+    ("prefill_split_d256_r7_p1200_uneven_g40", 80, 2, 256, 7, 1200, "causal_split"),  # 38 tiles over 9 splits
+    # short chunks that few key tiles: each row block's keys split among its waves
+    ("prefill_short_d256_r512_p0_g4", 16, 4, 256, 512, 0, "causal_short"),
+    ("prefill_short_d256_r1024_p0_g8", 16, 2, 256, 1024, 0, "causal_short"),
+    ("prefill_short_d128_r300_p100", 16, 2, 128, 300, 100, "causal_short"),
+    ("prefill_short_d256_r200_p300_g8", 32, 4, 256, 200, 300, "causal_short"),
+    ("prefill_short_d256_r7_p257_g40", 80, 2, 256, 7, 257, "causal_short"),       # one partial row block
+    ("prefill_short_d64_r500_p0", 8, 2, 64, 500, 0, "causal_short"),
+    ("prefill_short_d256_r33_p0", 16, 2, 256, 33, 0, "causal"),                   # fills no split: one-workgroup kernel
 ]
 
 
