@@ -47,13 +47,25 @@ MFMA_BF16_PEAK_TFS = 2500.0  # MI355X dense bf16 MFMA, TFLOP/s
 # Memory traffic per call, from rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE runs
 # of this script (KiB per dispatch, summed over the kernels of one call).
 # FETCH_SIZE is scaled by 2 and WRITE_SIZE by 1: a 256 MiB device copy reads
-# 131 086 KiB and writes 262 144 KiB on these counters. FETCH_SIZE counts
+# 131 087 KiB and writes 262 144 KiB on these counters. FETCH_SIZE counts
 # every L2 fill from the memory fabric, so Infinity Cache hits are included.
-# Summary and commands: profiles/pmc_traffic_decode32k_prefill4096.md
+# Summary and commands: profiles/pmc_traffic_bench_configs.md
 TRAFFIC_BYTES = {
-    "decode_32k": (2 * (16472.8 + 17512.5 + 1092.1) + (2112.0 + 2056.0 + 8.0)) * 1024,
-    "prefill_4096_after_8192": (2 * 171094.3 + 36352.9) * 1024,
+    "chained": {
+        "decode_1k": (2 * (563.4 + 596.3 + 67.2) + (34.0 + 64.5 + 4.0)) * 1024,
+        "decode_32k": (2 * (16467.7 + 17509.3 + 1090.5) + (2112.0 + 2056.0 + 8.0)) * 1024,
+        "prefill_512": (2 * 8830.2 + 4096.0) * 1024,
+        "prefill_4096_after_8192": (2 * 165007.9 + 36352.0) * 1024,
+        "decode_128k_outliers": (2 * (65622.8 + 69784.3 + 1090.5) + (8320.2 + 2568.0 + 8.0)) * 1024,
+    },
+    "fused": {
+        "decode_1k": (2 * (569.8 + 623.0 + 75.5) + (36.0 + 65.0 + 4.0)) * 1024,
+        "decode_32k": (2 * (16485.5 + 17542.2 + 1130.6) + (2240.0 + 2064.0 + 8.0)) * 1024,
+        "decode_128k_outliers": (2 * (65639.3 + 72584.0 + 1130.6) + (8832.4 + 16912.0 + 8.0)) * 1024,
+    },
 }
+PREFILL_KERNELS = {"prefill_512": "prefill_ks (one workgroup per 32-row block; its keys split among 4 waves)",
+                   "prefill_4096_after_8192": "prefill_attn"}
 
 
 def log(*a):
@@ -261,7 +273,7 @@ def bench_config(torch, hsdpa, W, name, kind, steps, warmup, form="chained"):
         val = nbytes / (ms * 1e-3) / 1e9
         log(f"{name} ({form}): {ms*1e3:.2f} us/step, {val:.1f} GB/s ({val/HBM_PEAK_GBS:.1%} of HBM peak), "
             f"wall {wall*1e3:.2f} ms")
-        tr = TRAFFIC_BYTES.get(name) if form == "chained" else None
+        tr = TRAFFIC_BYTES.get(form, {}).get(name)
         return {"value": round(val, 2), "unit": "GB/s", "ms_per_step": round(ms, 5), "steps": steps,
                 "config": {"workload": text, "algorithmic_bytes": nbytes, "kv_caches_rotated": copies},
                 "roofline": {"bound": "hbm", "achieved": round(val, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -270,13 +282,12 @@ def bench_config(torch, hsdpa, W, name, kind, steps, warmup, form="chained"):
     flops = w.prefill_flops()
     val = flops / (ms * 1e-3) / 1e12
     log(f"{name}: {ms*1e3:.2f} us/step, {val:.1f} TFLOP/s ({val/MFMA_BF16_PEAK_TFS:.1%} of MFMA peak)")
-    tr = TRAFFIC_BYTES.get(name)
+    tr = TRAFFIC_BYTES["chained"].get(name)
     return {"value": round(val, 2), "unit": "TFLOP/s", "ms_per_step": round(ms, 5), "steps": steps,
             "config": {"workload": text, "algorithmic_flops": flops},
             "roofline": {"bound": "mfma", "achieved": round(val, 2), "peak": MFMA_BF16_PEAK_TFS, "unit": "TFLOP/s",
                          "frac": round(val / MFMA_BF16_PEAK_TFS, 4), "traffic": round(tr) if tr else None,
-                         "kernel": "prefill_attn" if name == "prefill_4096_after_8192" else
-                                   "prefill_split_max + prefill_split_pv + prefill_split_combine"}}
+                         "kernel": PREFILL_KERNELS[name]}}
 
 
 def cpu_baseline(w_decode):
