@@ -1382,6 +1382,318 @@ __global__ __launch_bounds__(64 * KS, 1) void prefill_ks(PrefillArgs a)
 }
 
 // ---------------------------------------------------------------------------
+// Causal prefill of a short chunk, keys split among the waves for the scores
+// and dimensions split among them for P.V: grid (row blocks of 32, heads), 4
+// waves (one per SIMD), D >= 128. The row block's Q is loaded once, a quarter
+// per wave, and shared through LDS. Pass 1 is prefill_ks's: wave k computes
+// and keeps the scores of key tiles k, k + 4, ... (the next tile's load in
+// flight). After the row maxima are exchanged, pass 2 runs in rounds of 4
+// tiles: wave w accumulates O for its D / 4 dimensions over the round's tiles,
+// staging its V slices through its own LDS rows (VPF tiles loaded ahead, the
+// next tile's operands read after this one's MFMAs are issued), while the
+// exponentials of the next round's tiles (each wave its own, split hi + lo in
+// the lanes' operand layout) are computed between those MFMAs and posted to
+// LDS for all waves. Every workgroup runs MT tiles (the launch's largest
+// count, in whole rounds), the ones past its own fully masked: nothing
+// branches on the count. No partial outputs pass between the waves, only the
+// row sums (added in wave order). Numerics as prefill_ks.
+// ---------------------------------------------------------------------------
+template <int S>
+__device__ __forceinline__ u32x4 vt_operand_stride(const uint16_t *vtile, int kb, int d0, int l)
+{
+    const int j = l & 15, G = l >> 4;
+    const int key = kb + 8 * (G >> 1) + (j >> 2);
+    const int dim = d0 + 16 * (G & 1) + 4 * (j & 3);
+    const u32x2 a = tr_read(vtile + key * S + dim);
+    const u32x2 b = tr_read(vtile + (key + 4) * S + dim);
+    return u32x4{a.x, a.y, b.x, b.y};
+}
+
+// DW dimensions [d0, d0 + DW) of a 32-key V tile: 32 * DW/8 chunks of 16
+// bytes, lanes on consecutive chunks (each instruction reads whole 2*DW-byte
+// row pieces). Keys at or past lim read the tile's first row (or row 0) and are
+// zeroed when stored.
+template <int DW> struct Slice {
+    static constexpr int kPer = kKeyTile * (DW / 8) / 64;
+    static_assert(kKeyTile * (DW / 8) % 64 == 0, "whole chunks per lane");
+};
+
+template <int D, int DW>
+__device__ __forceinline__ void slice_gload(const uint16_t *base, uint64_t t0, uint64_t lim, int d0, int l,
+                                            u32x4 (&r)[Slice<DW>::kPer])
+{
+    const bool any = t0 < lim;
+    const uint16_t *tb = base + (any ? t0 : 0) * D + d0;
+    const uint32_t nvalid = any ? static_cast<uint32_t>(lim - t0 < kKeyTile ? lim - t0 : kKeyTile) : 0u;
+#pragma unroll
+    for (int i = 0; i < Slice<DW>::kPer; i++) {
+        const int c = l + 64 * i, key = c / (DW / 8), dc = c % (DW / 8);
+        const uint32_t off = static_cast<uint32_t>(key) < nvalid ? static_cast<uint32_t>(key * D + 8 * dc) : 0u;
+        r[i] = *reinterpret_cast<const u32x4 *>(tb + off);
+    }
+}
+
+template <int DW, int S>
+__device__ __forceinline__ void slice_mask_lstore(uint16_t *st, uint64_t t0, uint64_t lim, int l,
+                                                  const u32x4 (&r)[Slice<DW>::kPer])
+{
+    const uint32_t nvalid = t0 < lim ? static_cast<uint32_t>(lim - t0 < kKeyTile ? lim - t0 : kKeyTile) : 0u;
+#pragma unroll
+    for (int i = 0; i < Slice<DW>::kPer; i++) {
+        const int c = l + 64 * i, key = c / (DW / 8), dc = c % (DW / 8);
+        store16(st + key * S + 8 * dc, static_cast<uint32_t>(key) < nvalid ? r[i] : u32x4{0, 0, 0, 0});
+    }
+}
+
+template <int D, int KS, int MT, int VPF, bool POW2>
+__global__ __launch_bounds__(64 * KS, 1) void prefill_kd(PrefillArgs a)
+{
+    static_assert(KS == 4, "a round's exponentials are spread over its four tiles' products");
+    static_assert(MT % KS == 0 && VPF <= MT, "whole rounds");
+    static_assert(D / 32 >= KS, "every wave accumulates O for a share of the dimensions");
+    constexpr int TPW = MT / KS;                                // rounds; one tile per wave each
+    constexpr int SK = Pad<D>::K;
+    constexpr int DW = D / KS;                                  // dimensions per wave
+    constexpr int DPW = DW / 32;                                // 32-dimension blocks per wave
+    constexpr int SVS = DW + 32;                                // V slice row stride (bf16)
+    constexpr int QS = D / 16 / KS;                             // Q chunks each wave loads
+    constexpr int KT_U16 = kKeyTile * SK;                       // one wave's K tile
+    constexpr int Q_U16 = (D / 16) * 64 * 8;                    // Q in the lanes' operand layout
+    constexpr int P_U16 = MT * 4 * 64 * 8;                      // [tile][half][hi, lo][lane] x 8 bf16
+    constexpr int VS_U16 = 2 * kKeyTile * SVS;                  // one wave's two V slices
+    constexpr int PASS1 = KS * KT_U16 + Q_U16, PASS2 = P_U16 + KS * VS_U16;
+    __shared__ __attribute__((aligned(16))) uint16_t lds[PASS1 > PASS2 ? PASS1 : PASS2];
+    __shared__ float mred[KS][32];
+    __shared__ float lred[KS][32];
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int l = threadIdx.x & 63, col = l & 31, grp = l >> 5;
+    const int head = blockIdx.y, kvh = head / a.gqa;
+    const uint64_t rb = gridDim.x - 1 - blockIdx.x;             // heaviest row blocks first
+    const uint64_t r0 = rb * 32, row = r0 + col;
+    const bool rowv = row < a.rows;
+    const uint64_t rend = r0 + 32 < a.rows ? r0 + 32 : a.rows;
+    // the block's key tiles; every workgroup runs MT (the launch's largest),
+    // the ones past its own fully masked, so that nothing branches on the
+    // count (a branch makes the later waits wait for every load in flight)
+    const uint64_t nblk_keys = a.past + rend;
+    const uint64_t nblk = nblk_keys < a.n ? nblk_keys : a.n;   // loads at or past: one clamped address
+    const int nfull = static_cast<int>((a.past + r0 + 1) / kKeyTile);   // no mask needed below
+    const uint64_t lim = a.past + row;                          // last visible key of this row
+    uint16_t *kt = lds + wave * KT_U16;
+    uint16_t *qs = lds + KS * KT_U16;
+    uint16_t *pbuf = lds;
+    uint16_t *vs = lds + P_U16 + wave * VS_U16;
+    const int d0 = wave * DW;
+
+    const uint16_t *kg = a.k + static_cast<uint64_t>(kvh) * a.kv_stride;
+    const uint16_t *vg = a.v + static_cast<uint64_t>(kvh) * a.kv_stride;
+    auto wave_sync = [&]() {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    };
+    // a workgroup barrier ordering LDS only: __syncthreads' fence would also
+    // wait for every global load in flight, the prefetched tiles included
+    auto lds_barrier = [&]() {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+    };
+    u32x4 kr[Tile<D, 64>::kPer];
+    tile_gload<D, 64, false>(kg, static_cast<uint64_t>(wave) * kKeyTile, nblk, l, kr);
+    {
+        const uint16_t *qp = a.q + (rowv ? row : 0) * a.q_row + static_cast<uint64_t>(head) * a.q_head;
+#pragma unroll
+        for (int j = 0; j < QS; j++) {
+            const int sq = wave * QS + j;
+            const u32x4 v = load16(qp + 16 * sq + 8 * grp);
+            store16(qs + (sq * 64 + l) * 8, rowv ? v : u32x4{0, 0, 0, 0});
+        }
+    }
+    lds_barrier();
+
+    // pass 1: the scores of this wave's tiles (unscaled dot products when
+    // POW2), kept, and their row maxima
+    f32x16 sc[TPW];
+    float m = kNegInf;
+    {
+        u32x4 qb[D / 16];
+#pragma unroll
+        for (int sq = 0; sq < D / 16; sq++) qb[sq] = load16(qs + (sq * 64 + l) * 8);
+        const int arow = swap23(col) * SK + 8 * grp;
+#pragma unroll
+        for (int i = 0; i < TPW; i++) {
+            const int t = wave + KS * i;
+            const uint64_t t0 = static_cast<uint64_t>(t) * kKeyTile;
+            tile_lstore_padded<D, 64>(kt, SK, l, kr);
+            wave_sync();
+            if (i + 1 < TPW) tile_gload<D, 64, false>(kg, t0 + KS * kKeyTile, nblk, l, kr);
+            u32x4 ka[D / 16];
+#pragma unroll
+            for (int sq = 0; sq < D / 16; sq++) ka[sq] = load16(kt + arow + 16 * sq);
+            __builtin_amdgcn_sched_barrier(0);
+            f32x16 acc0 = {}, acc1 = {};
+#pragma unroll
+            for (int sq = 0; sq < D / 16; sq += 2) {
+                acc0 = mfma(ka[sq], qb[sq], acc0);
+                acc1 = mfma(ka[sq + 1], qb[sq + 1], acc1);
+            }
+            const f32x16 acc = acc0 + acc1;
+            sc[i] = acc;
+            const bool full = t < nfull;
+            const int vis = static_cast<int>(static_cast<int64_t>(lim) - static_cast<int64_t>(t0));
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const float x = POW2 ? acc[r] : acc[r] * a.scale;
+                m = __builtin_fmaxf(m, full || key_of(r, grp) <= vis ? x : kNegInf);
+            }
+            wave_sync();
+        }
+    }
+    // the first VPF V slices of this wave's dimensions, in flight across the
+    // exchange and the first round's exponentials
+    u32x4 vq[VPF][Slice<DW>::kPer];
+#pragma unroll
+    for (int j = 0; j < VPF; j++) slice_gload<D, DW>(vg, static_cast<uint64_t>(j) * kKeyTile, nblk, d0, l, vq[j]);
+    __builtin_amdgcn_sched_barrier(0);
+    m = __builtin_fmaxf(m, __shfl_xor(m, 32));
+    if (grp == 0) mred[wave][col] = m;
+    lds_barrier();                                              // also: every wave is done with its K tile
+#pragma unroll
+    for (int w = 0; w < KS; w++) m = __builtin_fmaxf(m, mred[w][col]);
+    // rows past the chunk: a finite maximum, their outputs are never stored
+    if (!rowv) m = 0.0f;
+    ExpArgs ex;
+    ex.m = m;
+    ex.scale = a.scale;
+    ex.clamp = POW2 ? -87.33654f / a.scale : -87.33654f;
+    ex.mul = POW2 ? 1.442695f * a.scale : 1.442695f;
+
+    // pass 2. exps_q(r, q): the exponentials of scores 4q .. 4q+3 of this
+    // wave's tile of round r at the exact maximum, masked by bits (so that the
+    // exponential is not made conditional); after quarters 1 and 3 the half's
+    // hi and lo are posted in the lanes' B-operand layout
+    float lsum = 0.0f;
+    float ev[16];
+    // one exponential: score k of this wave's tile of round r
+    auto exp_k = [&](int r, int k) {
+        const int t = wave + KS * r;
+        const uint64_t t0 = static_cast<uint64_t>(t) * kKeyTile;
+        const bool full = t < nfull;
+        const int vis = static_cast<int>(static_cast<int64_t>(lim) - static_cast<int64_t>(t0));
+        const float e = exp_score<POW2>(sc[r][k], ex);
+        const uint32_t keep = full || key_of(k, grp) <= vis ? 0xFFFFFFFFu : 0u;
+        ev[k] = __uint_as_float(__float_as_uint(e) & keep);
+        lsum += ev[k];
+    };
+    // half h of that tile's exponentials (8 of them), posted
+    auto post_half = [&](int r, int h) {
+        const int t = wave + KS * r;
+        u32x4 hi, lo;
+        split_pack_hw(ev + 8 * h, hi, lo);
+        store16(pbuf + ((t * 2 + h) * 2 + 0) * 512 + 8 * l, hi);
+        store16(pbuf + ((t * 2 + h) * 2 + 1) * 512 + 8 * l, lo);
+    };
+    auto exps_q = [&](int r, int q) {
+#pragma unroll
+        for (int k = 4 * q; k < 4 * q + 4; k++) exp_k(r, k);
+        if (q & 1) post_half(r, q >> 1);
+    };
+    u32x4 p[4], av[2][DPW];
+    auto read_p = [&](int t) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) p[j] = load16(pbuf + (t * 4 + j) * 512 + 8 * l);
+    };
+    // tile t's V slice (vq[t % VPF]) to its staging rows, its V^T operands
+    // read back, the slice VPF tiles on requested in its registers
+    auto stage = [&](int t) {
+        uint16_t *st = vs + (t & 1) * kKeyTile * SVS;
+        slice_mask_lstore<DW, SVS>(st, static_cast<uint64_t>(t) * kKeyTile, nblk, l, vq[t % VPF]);
+        wave_sync();
+#pragma unroll
+        for (int h = 0; h < 2; h++)
+#pragma unroll
+            for (int dt = 0; dt < DPW; dt++) av[h][dt] = vt_operand_stride<SVS>(st, 16 * h, 32 * dt, l);
+        if (t + VPF < MT) slice_gload<D, DW>(vg, static_cast<uint64_t>(t + VPF) * kKeyTile, nblk, d0, l, vq[t % VPF]);
+    };
+#pragma unroll
+    for (int q = 0; q < 4; q++) exps_q(0, q);
+    stage(0);
+    __builtin_amdgcn_sched_barrier(0);
+    lds_barrier();                                              // round 0's P posted
+    read_p(0);
+    f32x16 o[DPW];
+#pragma unroll
+    for (int dt = 0; dt < DPW; dt++) o[dt] = f32x16{};
+#pragma unroll
+    for (int r = 0; r < TPW; r++) {
+#pragma unroll
+        for (int j = 0; j < KS; j++) {
+            const int t = KS * r + j;
+            // this tile's products, one exponential of the next round issued
+            // after each of the first four, while the matrix core runs it (the
+            // order pinned: the scheduler would group them)
+            __builtin_amdgcn_sched_barrier(0);
+            int e_at = 0;
+#pragma unroll
+            for (int h = 0; h < 2; h++)
+#pragma unroll
+                for (int hl = 0; hl < 2; hl++)
+#pragma unroll
+                    for (int dt = 0; dt < DPW; dt++) {
+                        o[dt] = mfma(av[h][dt], p[2 * h + hl], o[dt]);
+                        __builtin_amdgcn_sched_barrier(0);
+                        if (r + 1 < TPW && e_at < 4) {
+                            exp_k(r + 1, 4 * j + e_at);
+                            __builtin_amdgcn_sched_barrier(0);
+                        }
+                        e_at++;
+                    }
+#pragma unroll
+            for (; e_at < 4; e_at++)
+                if (r + 1 < TPW) exp_k(r + 1, 4 * j + e_at);
+            if (r + 1 < TPW && (j & 1)) post_half(r + 1, j >> 1);
+            __builtin_amdgcn_sched_barrier(0);
+            if (t + 1 < MT) {
+                stage(t + 1);
+                if (j + 1 < KS) read_p(t + 1);
+            }
+        }
+        if (r + 1 < TPW) {
+            __builtin_amdgcn_sched_barrier(0);
+            lds_barrier();                                      // round r + 1's P posted
+            read_p(KS * (r + 1));
+        }
+    }
+    lsum += __shfl_xor(lsum, 32);
+    if (grp == 0) lred[wave][col] = lsum;
+    lds_barrier();
+    if (!rowv) return;
+    float L = 0.0f;
+#pragma unroll
+    for (int w = 0; w < KS; w++) L += lred[w][col];
+    const float inv = 1.0f / L;
+    uint16_t *op = a.out + row * a.out_row + static_cast<uint64_t>(head) * D + d0;
+    const uint16_t *gp = a.gate ? a.gate + row * a.gate_row + static_cast<uint64_t>(head) * D + d0 : nullptr;
+#pragma unroll
+    for (int dt = 0; dt < DPW; dt++)
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            uint32_t b0 = cvt_out(o[dt][4 * c] * inv), b1 = cvt_out(o[dt][4 * c + 1] * inv);
+            uint32_t b2 = cvt_out(o[dt][4 * c + 2] * inv), b3 = cvt_out(o[dt][4 * c + 3] * inv);
+            const int at = 32 * dt + 8 * c + 4 * grp;
+            if (gp) {
+                const uint2 g = *reinterpret_cast<const uint2 *>(gp + at);
+                b0 = gate_bf16(static_cast<uint16_t>(b0), static_cast<uint16_t>(g.x));
+                b1 = gate_bf16(static_cast<uint16_t>(b1), static_cast<uint16_t>(g.x >> 16));
+                b2 = gate_bf16(static_cast<uint16_t>(b2), static_cast<uint16_t>(g.y));
+                b3 = gate_bf16(static_cast<uint16_t>(b3), static_cast<uint16_t>(g.y >> 16));
+            }
+            *reinterpret_cast<uint2 *>(op + at) = uint2{b0 | (b1 << 16), b2 | (b3 << 16)};
+        }
+}
+
+// ---------------------------------------------------------------------------
 // Causal prefill split over the keys, for chunks whose grid of (row group,
 // head group) workgroups leaves compute units idle (a short chunk after a long
 // cache): gridDim.z workgroups share a row group's key tiles, tile range
