@@ -377,8 +377,8 @@ template <int MR> struct DecodeIds {
 
 // FUSED: also store the maximum of every 16-key block of each column (bmax):
 // the Fused form evaluates a block's exponentials at the running maximum of
-// the blocks up to it.
-template <int D, bool LOOP, int MR = 0, bool FUSED = false>
+// the blocks up to it. TWO (with LOOP): exactly two tiles per wave.
+template <int D, bool LOOP, int MR = 0, bool FUSED = false, bool TWO = false>
 __global__ __launch_bounds__(256) void decode_qk(DecodeArgs a)
 {
     constexpr int KS = D / 32;
@@ -485,6 +485,20 @@ __global__ __launch_bounds__(256) void decode_qk(DecodeArgs a)
         // itself the scheduler interleaves them and keeps only a few outstanding.
         __builtin_amdgcn_sched_barrier(0);
         tile(j0 + kKeyTile * wave, kr);
+    } else if constexpr (TWO) {
+        // exactly two rounds of one tile per wave (keys_qk = 256): both tiles
+        // requested before the first is scored. In the loop below the second
+        // is requested at the top of the loop and waits behind the first
+        // (32K keys on 2 KV heads: 21.3 -> 20.6 us); for more rounds the loop
+        // runs faster with one tile in flight (two: 0.8 us slower at 64K and
+        // 128K)
+        u32x4 kr0[Tile<D, 64>::kPer], kr1[Tile<D, 64>::kPer];
+        tile_gload<D, 64, MR != 2>(kbase, j0 + kKeyTile * wave, j1, l, kr0);
+        tile_gload<D, 64, MR != 2>(kbase, j0 + 4 * kKeyTile + kKeyTile * wave, j1, l, kr1);
+        __builtin_amdgcn_sched_barrier(0);
+        tile(j0 + kKeyTile * wave, kr0);
+        __builtin_amdgcn_sched_barrier(0);
+        tile(j0 + 4 * kKeyTile + kKeyTile * wave, kr1);
     } else {
         // keys_qk / 128 rounds of one tile per wave, the next round's tile in
         // flight while this one is scored; the prefetch after the last round

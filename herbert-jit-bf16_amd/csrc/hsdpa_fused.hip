@@ -30,8 +30,9 @@ static hipError_t fused_dm(const DecodeArgs &a, int kv_heads, hipStream_t s)
     const auto pad8 = [](int n) { return static_cast<unsigned>((n + 7) / 8 * 8); };
     const dim3 gqk = xcd ? dim3(pad8(a.nwg_qk) * a.sub, kv_heads, 1) : dim3(a.nwg_qk, kv_heads, a.sub);
     const dim3 gpv = xcd ? dim3(pad8(a.nwg_pv) * a.sub, kv_heads, 1) : dim3(a.nwg_pv, kv_heads, a.sub);
-    hipError_t e = a.keys_qk > 4 * kKeyTile ? launch(decode_qk<D, true, MR, true>, gqk, dim3(256), s, a)
-                                            : launch(decode_qk<D, false, MR, true>, gqk, dim3(256), s, a);
+    hipError_t e = a.keys_qk == 8 * kKeyTile ? launch(decode_qk<D, true, MR, true, true>, gqk, dim3(256), s, a)
+                   : a.keys_qk > 4 * kKeyTile  ? launch(decode_qk<D, true, MR, true>, gqk, dim3(256), s, a)
+                                               : launch(decode_qk<D, false, MR, true>, gqk, dim3(256), s, a);
     if (e != hipSuccess) return e;
     if (a.g <= 8) {
         if (a.keys_pv == 4 * kKeyTile) e = launch(decode_pv<D, 4, 1, false, MR, true>, gpv, dim3(256), s, a);
@@ -67,8 +68,9 @@ static hipError_t fused_more(const DecodeArgs &a, int kv_heads, hipStream_t s)
 {
     if (a.rows != 1) return hipErrorInvalidValue;           // decode_rows_ok
     const dim3 gqk(a.nwg_qk, kv_heads, a.sub), gpv(a.nwg_pv, kv_heads, a.sub);
-    hipError_t e = a.keys_qk > 4 * kKeyTile ? launch(decode_qk<D, true, 0, true>, gqk, dim3(256), s, a)
-                                            : launch(decode_qk<D, false, 0, true>, gqk, dim3(256), s, a);
+    hipError_t e = a.keys_qk == 8 * kKeyTile ? launch(decode_qk<D, true, 0, true, true>, gqk, dim3(256), s, a)
+                   : a.keys_qk > 4 * kKeyTile  ? launch(decode_qk<D, true, 0, true>, gqk, dim3(256), s, a)
+                                               : launch(decode_qk<D, false, 0, true>, gqk, dim3(256), s, a);
     if (e != hipSuccess) return e;
     constexpr bool WIDE = D / 16 >= 8 || 8 % (D / 16) == 0;        // decode_wide_ok
     if (a.keys_pv == 4 * kKeyTile) {
