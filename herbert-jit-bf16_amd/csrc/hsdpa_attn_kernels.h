@@ -162,6 +162,16 @@ __device__ __forceinline__ float wave_sum_hi(float x)
 
 __device__ __forceinline__ float fmaxnn(float a, float b) { return b > a ? b : a; }
 
+// A workgroup barrier that orders LDS only. __syncthreads' fence also waits
+// for every global load the wave has in flight, so a barrier placed while the
+// next tiles stream in would wait for them.
+__device__ __forceinline__ void lds_barrier()
+{
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // Maximum over each half wave (lanes 0..31 in lane 31, 32..63 in lane 63) and
 // over the whole wave (in lane 63) when `whole`. -inf is the identity; NaN
 // inputs are ignored like in the scalar reductions.
@@ -1505,13 +1515,6 @@ __global__ __launch_bounds__(64 * KS, 1) void prefill_kd(PrefillArgs a)
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    };
-    // a workgroup barrier ordering LDS only: __syncthreads' fence would also
-    // wait for every global load in flight, the prefetched tiles included
-    auto lds_barrier = [&]() {
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-        __builtin_amdgcn_s_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
     };
     u32x4 kr[Tile<D, 64>::kPer];
     tile_gload<D, 64, false>(kg, static_cast<uint64_t>(wave) * kKeyTile, nblk, l, kr);
