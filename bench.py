@@ -64,7 +64,7 @@ TRAFFIC_BYTES = {
         "decode_128k_outliers": (2 * (65639.3 + 72584.0 + 1130.6) + (8832.4 + 16912.0 + 8.0)) * 1024,
     },
 }
-PREFILL_KERNELS = {"prefill_512": "prefill_ks (one workgroup per 32-row block; its keys split among 4 waves)",
+PREFILL_KERNELS = {"prefill_512": "prefill_kd (one workgroup per 32-row block; its keys split among 8 waves)",
                    "prefill_4096_after_8192": "prefill_attn"}
 
 

@@ -1407,12 +1407,13 @@ __global__ __launch_bounds__(64 * KS, 1) void prefill_ks(PrefillArgs a)
 
 // ---------------------------------------------------------------------------
 // Causal prefill of a short chunk, keys split among the waves for the scores
-// and dimensions split among them for P.V: grid (row blocks of 32, heads), 4
-// waves (one per SIMD), D >= 128. The row block's Q is loaded once, a quarter
-// per wave, and shared through LDS. Pass 1 is prefill_ks's: wave k computes
-// and keeps the scores of key tiles k, k + 4, ... (the next tile's load in
-// flight). After the row maxima are exchanged, pass 2 runs in rounds of 4
-// tiles: wave w accumulates O for its D / 4 dimensions over the round's tiles,
+// and dimensions split among them for P.V: grid (row blocks of 32, heads), KS
+// waves: 4 (one per SIMD, D >= 128) or 8 (two per SIMD, D = 256). The row
+// block's Q is loaded once, a share per wave, and shared through LDS. Pass 1
+// is prefill_ks's: wave k computes and keeps the scores of key tiles k,
+// k + KS, ... (the next tile's load in flight). After the row maxima are
+// exchanged, pass 2 runs in rounds of KS tiles: wave w accumulates O for its
+// D / KS dimensions over the round's tiles,
 // staging its V slices through its own LDS rows (VPF tiles loaded ahead, the
 // next tile's operands read after this one's MFMAs are issued), while the
 // exponentials of the next round's tiles (each wave its own, split hi + lo in
@@ -1472,11 +1473,12 @@ __device__ __forceinline__ void slice_mask_lstore(uint16_t *st, uint64_t t0, uin
 template <int D, int KS, int MT, int VPF, bool POW2>
 __global__ __launch_bounds__(64 * KS, 1) void prefill_kd(PrefillArgs a)
 {
-    static_assert(KS == 4, "a round's exponentials are spread over its four tiles' products");
+    static_assert(KS == 4 || KS == 8, "a round's exponentials are spread over its tiles' products");
     static_assert(MT % KS == 0 && VPF <= MT, "whole rounds");
     static_assert(D / 32 >= KS, "every wave accumulates O for a share of the dimensions");
     constexpr int TPW = MT / KS;                                // rounds; one tile per wave each
     constexpr int SK = Pad<D>::K;
+    constexpr int EPT = 16 / KS;                                // next-round exponentials per tile of a round
     constexpr int DW = D / KS;                                  // dimensions per wave
     constexpr int DPW = DW / 32;                                // 32-dimension blocks per wave
     constexpr int SVS = DW + 32;                                // V slice row stride (bf16)
@@ -1648,7 +1650,7 @@ __global__ __launch_bounds__(64 * KS, 1) void prefill_kd(PrefillArgs a)
         for (int j = 0; j < KS; j++) {
             const int t = KS * r + j;
             // this tile's products, one exponential of the next round issued
-            // after each of the first four, while the matrix core runs it (the
+            // after each of the first EPT, while the matrix core runs it (the
             // order pinned: the scheduler would group them)
             __builtin_amdgcn_sched_barrier(0);
             int e_at = 0;
@@ -1660,16 +1662,17 @@ __global__ __launch_bounds__(64 * KS, 1) void prefill_kd(PrefillArgs a)
                     for (int dt = 0; dt < DPW; dt++) {
                         o[dt] = mfma(av[h][dt], p[2 * h + hl], o[dt]);
                         __builtin_amdgcn_sched_barrier(0);
-                        if (r + 1 < TPW && e_at < 4) {
-                            exp_k(r + 1, 4 * j + e_at);
+                        if (r + 1 < TPW && e_at < EPT) {
+                            exp_k(r + 1, EPT * j + e_at);
                             __builtin_amdgcn_sched_barrier(0);
                         }
                         e_at++;
                     }
 #pragma unroll
-            for (; e_at < 4; e_at++)
-                if (r + 1 < TPW) exp_k(r + 1, 4 * j + e_at);
-            if (r + 1 < TPW && (j & 1)) post_half(r + 1, j >> 1);
+            for (; e_at < EPT; e_at++)
+                if (r + 1 < TPW) exp_k(r + 1, EPT * j + e_at);
+            // a half's eight exponentials are complete after tiles KS/2 - 1 and KS - 1
+            if (r + 1 < TPW && (j + 1) % (KS / 2) == 0) post_half(r + 1, j / (KS / 2));
             __builtin_amdgcn_sched_barrier(0);
             if (t + 1 < MT) {
                 stage(t + 1);

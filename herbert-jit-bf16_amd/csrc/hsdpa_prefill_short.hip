@@ -8,11 +8,11 @@
 
 namespace hsdpa {
 
-template <int D, int MT, bool POW2>
+template <int D, int MT, bool POW2, int KS = kShortWaves>
 static hipError_t prefill_kd_mt(const PrefillArgs &a, int heads, hipStream_t s)
 {
     const dim3 grid(static_cast<unsigned>((a.rows + 31) / 32), static_cast<unsigned>(heads));
-    return launch(prefill_kd<D, kShortWaves, MT, 4, POW2>, grid, dim3(64 * kShortWaves), s, a);
+    return launch(prefill_kd<D, KS, MT, 4, POW2>, grid, dim3(64 * KS), s, a);
 }
 
 template <int D, bool POW2>
@@ -24,7 +24,14 @@ static hipError_t prefill_short_dp(const PrefillArgs &a, int heads, hipStream_t 
     // count rounded up to 8, 12 or 16 (a chunk reaches this kernel only with
     // more than 4 tiles: the split it replaces takes at least 4 per split);
     // beyond (their exponentials no longer fit the LDS), and at D = 64: O by
-    // keys
+    // keys. At D = 256 the row block's keys go to 8 waves, two per SIMD (one
+    // or two tiles each, 32 dimensions of O), in rounds of 8 tiles: 512 rows
+    // with no cache 20.5 -> 16.7 us, 481 after 30 23.0 -> 16.7, 100 after 220
+    // 18.5 -> 14.8 against 4 waves.
+    if constexpr (D == 256) {
+        if (ntiles <= 8) return prefill_kd_mt<D, 8, POW2, 8>(a, heads, s);
+        if (ntiles <= 16) return prefill_kd_mt<D, 16, POW2, 8>(a, heads, s);
+    }
     if constexpr (D >= 128) {
         if (ntiles <= 8) return prefill_kd_mt<D, 8, POW2>(a, heads, s);
         if (ntiles <= 12) return prefill_kd_mt<D, 12, POW2>(a, heads, s);
