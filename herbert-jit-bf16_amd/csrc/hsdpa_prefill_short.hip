@@ -19,7 +19,7 @@ template <int D, bool POW2>
 static hipError_t prefill_short_dp(const PrefillArgs &a, int heads, hipStream_t s)
 {
     const uint64_t ntiles = (a.past + a.rows + kKeyTile - 1) / kKeyTile;
-    // up to kShortKdTiles tiles at D >= 128: O by dimensions, no partial
+    // up to kShortKdTiles tiles at D = 128 and 256: O by dimensions, no partial
     // outputs between the waves, every workgroup running the launch's tile
     // count rounded up to 8, 12 or 16 (a chunk reaches this kernel only with
     // more than 4 tiles: the split it replaces takes at least 4 per split);
@@ -32,7 +32,7 @@ static hipError_t prefill_short_dp(const PrefillArgs &a, int heads, hipStream_t 
         if (ntiles <= 8) return prefill_kd_mt<D, 8, POW2, 8>(a, heads, s);
         if (ntiles <= 16) return prefill_kd_mt<D, 16, POW2, 8>(a, heads, s);
     }
-    if constexpr (D >= 128) {
+    if constexpr (D == 128) {
         if (ntiles <= 8) return prefill_kd_mt<D, 8, POW2>(a, heads, s);
         if (ntiles <= 12) return prefill_kd_mt<D, 12, POW2>(a, heads, s);
         if (ntiles <= static_cast<uint64_t>(kShortKdTiles)) return prefill_kd_mt<D, kShortKdTiles, POW2>(a, heads, s);
