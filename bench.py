@@ -54,7 +54,7 @@ TRAFFIC_BYTES = {
     "chained": {
         "decode_1k": (2 * (563.4 + 596.3 + 67.2) + (34.0 + 64.5 + 4.0)) * 1024,
         "decode_32k": (2 * (16467.7 + 17509.3 + 1090.5) + (2112.0 + 2056.0 + 8.0)) * 1024,
-        "prefill_512": (2 * 8830.2 + 4096.0) * 1024,
+        "prefill_512": (2 * 8603.6 + 4096.0) * 1024,
         "prefill_4096_after_8192": (2 * 165007.9 + 36352.0) * 1024,
         "decode_128k_outliers": (2 * (65622.8 + 69784.3 + 1090.5) + (8320.2 + 2568.0 + 8.0)) * 1024,
     },
