@@ -281,14 +281,17 @@ struct DecodeCfg {
 
 // Whether `rows` rows run on the decode kernels: one row whose g query heads
 // split into at most 4 groups of at most 16, or up to 8 rows as (row, head)
-// columns at head dimensions 64, 128 and 256 within the plan's columns.
+// columns at head dimensions 64, 128 and 256 within the plan's columns; at
+// those head dimensions, columns no equal split fits take padded groups
+// (decode_groups_pad).
 int decode_sub(const hsdpa_plan *p, uint64_t rows)
 {
     const uint64_t cols = rows * p->spec.gqa;
     const int d = static_cast<int>(p->spec.head_dim);
-    if (rows == 1) return cols <= static_cast<uint64_t>(4 * hsdpa::kDecodeMaxGroup) ? hsdpa::decode_groups(static_cast<int>(cols)) : 0;
+    const int even = cols <= static_cast<uint64_t>(4 * hsdpa::kDecodeMaxGroup) ? hsdpa::decode_groups(static_cast<int>(cols)) : 0;
+    if (rows == 1 && even) return even;
     if (rows > hsdpa::kDecodeMaxRows || !hsdpa::decode_rows_ok(d) || cols > p->dec_cols) return 0;
-    return hsdpa::decode_groups(static_cast<int>(cols));
+    return even ? even : hsdpa::decode_groups_pad(static_cast<int>(cols));
 }
 
 // The decode passes' grids for `rows` rows over n visible keys (decode_sub
@@ -299,7 +302,7 @@ DecodeCfg decode_cfg(const hsdpa_plan *p, uint64_t rows, uint64_t n, int sub)
     const int d = static_cast<int>(p->spec.head_dim);
     const uint64_t cols = rows * p->spec.gqa;
     c.sub = sub;
-    c.g = static_cast<int>(cols) / sub;
+    c.g = hsdpa::decode_group_cols(static_cast<int>(cols), sub);
     const uint64_t groups = p->kv_heads * static_cast<uint64_t>(sub);
     // pass 1: a tile per wave, or several in turn (the next one in flight)
     // once one tile per wave would need more than one workgroup per compute
@@ -368,7 +371,7 @@ uint64_t decode_nwg_pv_max(const hsdpa_plan *p, uint64_t rows, int sub)
     const uint64_t cap = p->spec.kv_capacity, groups = p->kv_heads * static_cast<uint64_t>(sub);
     const uint64_t per = static_cast<uint64_t>(p->cus) / groups > 0 ? static_cast<uint64_t>(p->cus) / groups : 1;
     const uint64_t by128 = (cap + 127) / 128, by256 = (cap + 255) / 256;
-    const int g = static_cast<int>(rows * p->spec.gqa) / sub;
+    const int g = hsdpa::decode_group_cols(static_cast<int>(rows * p->spec.gqa), sub);
     if (!hsdpa::decode_wide_ok(d)) return by128;
     const uint64_t one_round = std::min(by128, per);
     // the chunked pass 2 gives way to 256-key workgroups where it cannot run
@@ -415,7 +418,9 @@ hsdpa_status hsdpa_plan_create(const hsdpa_spec *spec, hsdpa_plan **out)
     int cus = 0;
     p->cus = check_device(&cus) == HSDPA_OK && cus > 0 ? cus : 256;
     // decode columns: the query heads of one row, or up to 8 rows of them
-    uint64_t cols = hsdpa::decode_groups(static_cast<int>(std::min<uint64_t>(g, 1u << 20))) ? g : 0;
+    const int gi = static_cast<int>(std::min<uint64_t>(g, 1u << 20));
+    const bool pad_ok = hsdpa::decode_rows_ok(static_cast<int>(d)) && hsdpa::decode_groups_pad(gi) > 0;
+    uint64_t cols = hsdpa::decode_groups(gi) || pad_ok ? g : 0;
     if (hsdpa::decode_rows_ok(static_cast<int>(d)) && p->max_rows > 1) {
         const uint64_t mr = std::min<uint64_t>(hsdpa::kDecodeMaxRows, p->max_rows);
         cols = std::max(cols, std::min<uint64_t>(hsdpa::kDecodeMaxCols, mr * g));
@@ -423,28 +428,31 @@ hsdpa_status hsdpa_plan_create(const hsdpa_spec *spec, hsdpa_plan **out)
     p->dec_cols = cols;
     p->dec_npad = align_up(cap, hsdpa::kDecodeKeysPV);
     p->dec_nwg_qk = (cap + hsdpa::kDecodeKeysQK - 1) / hsdpa::kDecodeKeysQK;
-    // the largest (pass-2 workgroup, column) count of any call the plan serves
-    uint64_t part = 0, cols_used = 0;
+    // the largest (pass-2 workgroup, column) count of any call the plan
+    // serves, its columns counting the padding of the last group
+    uint64_t part = 0, cols_used = 0, cols_pad = 0;
     for (uint64_t r = 1; r <= std::min<uint64_t>(hsdpa::kDecodeMaxRows, p->max_rows); r++) {
         const int sub = decode_sub(p, r);
         if (sub == 0) continue;
+        const uint64_t padded = static_cast<uint64_t>(sub) * hsdpa::decode_group_cols(static_cast<int>(r * g), sub);
         cols_used = std::max(cols_used, r * g);
-        part = std::max(part, decode_nwg_pv_max(p, r, sub) * r * g);
+        cols_pad = std::max(cols_pad, padded);
+        part = std::max(part, decode_nwg_pv_max(p, r, sub) * padded);
     }
     p->dec_cols = cols_used;
     p->dec_part = part;
     uint64_t off = 0;
     p->off_scores = off;
-    off = align_up(off + kvh * cols_used * p->dec_npad * 4, kAlign);
+    off = align_up(off + kvh * cols_pad * p->dec_npad * 4, kAlign);
     p->off_wgmax = off;
-    off = align_up(off + kvh * p->dec_nwg_qk * cols_used * 4, kAlign);
+    off = align_up(off + kvh * p->dec_nwg_qk * cols_pad * 4, kAlign);
     p->off_part_o = off;
     off = align_up(off + kvh * part * d * 4, kAlign);
     p->off_part_l = off;
     off = align_up(off + kvh * part * 4, kAlign);
     p->off_bmax = p->off_part_x = off;
     if (p->form == HSDPA_FORM_FUSED) {
-        off = align_up(off + kvh * cols_used * (p->dec_npad / 16) * 4, kAlign);
+        off = align_up(off + kvh * cols_pad * (p->dec_npad / 16) * 4, kAlign);
         p->off_part_x = off;
         off = align_up(off + kvh * part * 4, kAlign);
     }
@@ -516,6 +524,7 @@ static hsdpa_status run_part(const hsdpa_plan *plan, const hsdpa_call *call, con
         a.sub = c.sub;
         a.rows = static_cast<int>(rows);
         a.G = static_cast<int>(s.gqa);
+        a.cols = static_cast<int>(rows * s.gqa);
         a.past = past;
         a.q_row = s.q_row;
         a.out_row = s.out_row;

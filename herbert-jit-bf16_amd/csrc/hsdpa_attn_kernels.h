@@ -412,7 +412,8 @@ __global__ __launch_bounds__(256) void decode_qk(DecodeArgs a)
     const uint16_t *qp;
     uint64_t lim = a.n;                 // keys below lim are visible to this lane's column
     if constexpr (MR) {
-        const int c = id.z * a.g + (colv ? i : 0), row = c / a.G;
+        // a padded column (past rows * G) computes column 0's scores, never stored
+        const int cg = id.z * a.g + (colv ? i : 0), c = cg < a.cols ? cg : 0, row = c / a.G;
         qp = a.q + static_cast<uint64_t>(row) * a.q_row +
              static_cast<uint64_t>(static_cast<int>(blockIdx.y) * a.G + c - row * a.G) * a.q_head + 8 * G;
         lim = a.past + static_cast<uint64_t>(row) + 1;
@@ -957,6 +958,7 @@ __global__ __launch_bounds__(512) void decode_combine(DecodeArgs a)
         if constexpr (MR) {
             // group kvh = y sub + z; its column jh is column z g + jh of KV head y
             const int y = kvh / a.sub, c = (kvh - y * a.sub) * a.g + jh, row = c / a.G;
+            if (c >= a.cols) return;                            // a padded column
             const uint64_t head = static_cast<uint64_t>(y * a.G + c - row * a.G);
             oat = static_cast<uint64_t>(row) * a.out_row + head * D + dim;
             gat = static_cast<uint64_t>(row) * a.gate_row + head * D + dim;

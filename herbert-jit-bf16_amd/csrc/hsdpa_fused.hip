@@ -58,7 +58,9 @@ template <int D>
 static hipError_t fused_tuned(const DecodeArgs &a, int kv_heads, hipStream_t s)
 {
     if (a.xcd) return fused_dm<D, 2>(a, kv_heads, s);
-    return a.rows == 1 ? fused_dm<D, 0>(a, kv_heads, s) : fused_dm<D, 1>(a, kv_heads, s);
+    // one row in equal groups: the one-row kernels; a few rows, or padded
+    // groups: the kernels that map each column to its (row, head)
+    return a.rows == 1 && a.g * a.sub == a.cols ? fused_dm<D, 0>(a, kv_heads, s) : fused_dm<D, 1>(a, kv_heads, s);
 }
 
 // The other head dimensions up to 256: one row, the configurations of

@@ -56,6 +56,8 @@ struct DecodeArgs {
     int xcd;                // 1: the groups of a key range numbered onto one XCD (several groups)
     int rows;               // 1 for a decode step
     int G;                  // query heads per KV head
+    int cols;               // columns per KV head that hold a (row, head) pair: rows * G; sub * g may
+                            // exceed it by padding (the MR kernels compute a padded column and store nothing)
     uint64_t past;
     uint64_t q_row, out_row, gate_row;
     // The Fused form (the online softmax over blocks of 16 keys): pass 1 also
@@ -154,6 +156,20 @@ inline int decode_groups(int g)
         if (g % sub == 0 && g / sub <= kDecodeMaxGroup) return sub;
     return 0;
 }
+// Columns that no such split fits (a group size without a divisor up to 4
+// into groups of at most 16, more than 64 columns) run on the kernels that map
+// each column to a (row, head) pair, the few-rows instantiations: ceil(cols /
+// 16) groups of ceil(cols / sub) columns, the last one padded, up to
+// kDecodePadGroups groups (each streams the KV head's cache; where the causal
+// kernel would compute 32-row tiles for one row). Returns sub, or 0.
+constexpr int kDecodePadGroups = 16;
+inline int decode_groups_pad(int cols)
+{
+    const int sub = (cols + kDecodeMaxGroup - 1) / kDecodeMaxGroup;
+    return cols > 0 && sub <= kDecodePadGroups ? sub : 0;
+}
+// columns per group for `cols` columns in `sub` groups
+inline int decode_group_cols(int cols, int sub) { return (cols + sub - 1) / sub; }
 inline bool decode_wide_ok(int d) { return d <= 256 && (d / 16 >= 8 || 8 % (d / 16) == 0); }
 // A few rows after a cache run on the decode kernels (one column per (row,
 // head) pair, up to 4 groups of 16 columns per KV head) for the tuned head

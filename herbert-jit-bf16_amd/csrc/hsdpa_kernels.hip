@@ -318,7 +318,9 @@ template <int D>
 static hipError_t decode_d(const DecodeArgs &a, int kv_heads, hipStream_t s)
 {
     if (a.xcd) return decode_dm<D, 2>(a, kv_heads, s);
-    return a.rows == 1 ? decode_dm<D, 0>(a, kv_heads, s) : decode_dm<D, 1>(a, kv_heads, s);
+    // one row in equal groups: the one-row kernels; a few rows, or padded
+    // groups: the kernels that map each column to its (row, head)
+    return a.rows == 1 && a.g * a.sub == a.cols ? decode_dm<D, 0>(a, kv_heads, s) : decode_dm<D, 1>(a, kv_heads, s);
 }
 
 hipError_t launch_decode(const DecodeArgs &a, int head_dim, int kv_heads, hipStream_t s)

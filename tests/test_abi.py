@@ -130,8 +130,13 @@ def test_route_names_the_kernels():
     assert (r["main"], r["tail"], r["tail_rows"], r["tail_form"]) == ("causal", "few_rows", 3, "fused")
     # above head_dim 256 the Fused form falls back to Chained
     assert hsdpa.Plan(4, 2, 288, 100, form="fused").route(1, 10)["main_form"] == "chained"
-    # a group the decode kernels cannot take keeps the causal kernel (and the Chained numerics)
+    # a group size with no equal split into groups of at most 16 (17) takes padded
+    # groups on the decode kernels at the tuned head dimensions...
     r = hsdpa.Plan(17, 17, 128, 100, form="fused").route(1, 10)
+    assert r["main"] == "decode" and r["main_form"] == "fused"
+    assert hsdpa.Plan(160, 80, 256, 40000).route(1, 32767)["main"] == "decode"     # 80 heads: 5 groups of 16
+    # ...and keeps the causal kernel (and the Chained numerics) at the others
+    r = hsdpa.Plan(17, 17, 96, 100, form="fused").route(1, 10)
     assert r["main"] == "causal" and r["main_form"] == "chained"
     # one row per decode where the tail does not fit the decode columns
     r = hsdpa.Plan(32, 16, 128, 1000, form="fused").route(13, 100)

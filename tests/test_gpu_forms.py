@@ -57,6 +57,10 @@ FUSED = [
     ("fused_prefill_r70_p5_d128", 8, 8, 128, 70, 5, ("causal", "chained"), ("few_rows", "fused")),
     ("fused_prefill_r9_g16", 32, 2, 128, 9, 50, ("causal", "chained"), ("decode", "fused")),
     ("fused_prefill_r13_g16", 32, 2, 128, 13, 100, ("causal", "chained"), ("decode_rows", "fused")),
+    # padded groups (a group size with no equal split into groups of at most 16)
+    ("fused_d128_g17_padded", 17, 1, 128, 1, 900, ("decode", "fused"), None),
+    ("fused_d256_g17_padded_2kv_long", 34, 2, 256, 1, 40000, ("decode", "fused"), None),
+    ("fused_few_r5_g7_d256_padded", 7, 1, 256, 5, 300, ("few_rows", "fused"), None),
     # above head_dim 256 the form falls back to Chained, like the reference
     ("fused_d288_falls_back", 4, 2, 288, 1, 300, ("decode", "chained"), None),
 ]

@@ -132,27 +132,38 @@ def test_configs_full(torch_cuda, name):
 
 GROUPS = [
     # more than 16 query heads per KV head: the decode kernels take them in 2, 3
-    # or 4 equal groups; beyond that (or with no such divisor) the causal kernel
-    # serves the row
-    ("decode_g32_d128", 32, 1, 128, 1, 500),
-    ("decode_g16_d256", 32, 2, 256, 1, 999),
-    ("decode_g12_d256", 12, 1, 256, 1, 40),
-    ("decode_g48_d128_three_groups", 48, 1, 128, 1, 3000),
-    ("decode_g64_d64_four_groups", 128, 2, 64, 1, 20000),
-    ("decode_g24_d256_two_groups_8_wave", 48, 2, 256, 1, 33000),
-    ("decode_g20_d256_loop", 40, 2, 256, 1, 70000),
-    ("decode_g17_through_prefill", 17, 1, 128, 1, 900),
-    ("decode_g80_through_prefill", 80, 1, 64, 1, 300),
-    ("decode_g80_through_split_prefill", 80, 1, 64, 1, 6000),
+    # or 4 equal groups; a group size with no such split (17), or more than 64
+    # columns, in padded groups of at most 16 at head dimensions 64, 128 and
+    # 256 (the last group's extra columns computed and never stored); the causal
+    # kernel serves the row at the other head dimensions
+    # name, heads, kv_heads, head_dim, rows, past, the kernels the call must take
+    ("decode_g32_d128", 32, 1, 128, 1, 500, "decode"),
+    ("decode_g16_d256", 32, 2, 256, 1, 999, "decode"),
+    ("decode_g12_d256", 12, 1, 256, 1, 40, "decode"),
+    ("decode_g48_d128_three_groups", 48, 1, 128, 1, 3000, "decode"),
+    ("decode_g64_d64_four_groups", 128, 2, 64, 1, 20000, "decode"),
+    ("decode_g24_d256_two_groups_8_wave", 48, 2, 256, 1, 33000, "decode"),
+    ("decode_g20_d256_loop", 40, 2, 256, 1, 70000, "decode"),
+    ("decode_g17_d128_padded", 17, 1, 128, 1, 900, "decode"),                 # 2 groups of 9, one padded
+    ("decode_g17_d256_padded_2kv_long", 34, 2, 256, 1, 40000, "decode"),
+    ("decode_g80_d64_five_groups", 80, 1, 64, 1, 300, "decode"),              # 5 groups of 16
+    ("decode_g80_d64_five_groups_long", 80, 1, 64, 1, 6000, "decode"),
+    ("decode_g100_d128_padded", 100, 1, 128, 1, 2000, "decode"),              # 7 groups of 15, 5 padded
+    ("few_r2_g17_d128_padded", 17, 1, 128, 2, 500, "few_rows"),              # 34 columns: 3 groups of 12
+    ("few_r5_g7_d256_padded", 7, 1, 256, 5, 300, "few_rows"),                # 35 columns: 3 groups of 12
+    ("decode_g17_d96_through_split_prefill", 17, 1, 96, 1, 900, "causal_split"),
+    ("decode_g300_d64_through_split_prefill", 300, 1, 64, 1, 6000, "causal_split"),   # 19 groups: above 16
 ]
 
 
 @pytest.mark.parametrize("case", GROUPS, ids=[c[0] for c in GROUPS])
 def test_gqa_groups(torch_cuda, case):
-    name, h, kvh, d, rows, past = case
+    name, h, kvh, d, rows, past, kernels = case
     w = W.make(name, heads=h, kv_heads=kvh, head_dim=d, rows=rows, past=past, seed=5)
+    plan = hsdpa.Plan(w.heads, w.gqa, w.head_dim, w.capacity)
+    assert plan.route(rows, past)["main"] == kernels, plan.route(rows, past)
     print(f"case {name}", flush=True)
-    out = run_hsdpa(w)
+    out = run_hsdpa(w, plan)
     ref = oracle.attention(w)
     r = assert_parity(out, ref, w, name)
     print(name, r, flush=True)
