@@ -466,7 +466,7 @@ hsdpa_status hsdpa_plan_create(const hsdpa_spec *spec, hsdpa_plan **out)
     p->split_units = causal ? std::min<uint64_t>(hsdpa::kSplitUnits, 8 * static_cast<uint64_t>(p->cus)) : 0;
     const uint64_t cells = p->split_units * 32;
     p->off_smax = off;
-    off = align_up(off + cells * 4, kAlign);
+    off = align_up(off + p->split_units * hsdpa::kSplitMaxCells * 4, kAlign);
     p->off_so = off;
     off = align_up(off + cells * d * 4, kAlign);
     p->off_sl = off;
@@ -580,9 +580,11 @@ static hsdpa_status run_part(const hsdpa_plan *plan, const hsdpa_call *call, con
         return e == hipSuccess ? HSDPA_OK : HSDPA_ERR_HIP;
     }
     const int sp = hsdpa::prefill_split_count(a, d, static_cast<int>(s.heads), ps);
-    if (kernels) *kernels = sp > 1 ? HSDPA_KERNELS_CAUSAL_SPLIT : HSDPA_KERNELS_CAUSAL;
+    const bool paired = sp == 1 && hsdpa::prefill_pair_rows(a, d, static_cast<int>(s.heads), ps).srows > 0;
+    if (kernels)
+        *kernels = sp > 1 ? HSDPA_KERNELS_CAUSAL_SPLIT : paired ? HSDPA_KERNELS_CAUSAL_PAIRED : HSDPA_KERNELS_CAUSAL;
     if (splits) *splits = static_cast<uint32_t>(sp);
-    if (launches) *launches += sp > 1 ? 3 : 1;
+    if (launches) *launches += sp > 1 || paired ? 3 : 1;
     if (!launch) return HSDPA_OK;
     const hipError_t e = hsdpa::launch_prefill(a, d, static_cast<int>(s.heads), ps, st);
     return e == hipSuccess ? HSDPA_OK : HSDPA_ERR_HIP;

@@ -1729,12 +1729,18 @@ __global__ __launch_bounds__(64 * KS, 1) void prefill_kd(PrefillArgs a)
 //                         unnormalised so[z][row][head][D] and sl[z][row][head]
 //   prefill_split_combine out = bf16(sum_z O / sum_z l), z ascending (+ gate)
 // Same waves, tiles and numerics as prefill_attn.
+// The paired form (PAIRED, grid (R row groups, head groups), one round of
+// the compute units; prefill_pairs): workgroup i < j = R - 1 - i walks the
+// whole of row group i (output written directly), then the last h tiles of
+// row group j (slot 1); workgroup j walks the rest of row group j (slot 0).
+// The combine serves the rows of the split row groups only.
 // ---------------------------------------------------------------------------
 struct SplitArgs {
-    float *smax;            // [splits][heads][rows]
-    float *so;              // [splits][rows][heads][D]
-    float *sl;              // [splits][rows][heads]
+    float *smax;            // [slots][heads][rows]
+    float *so;              // [slots][srows][heads][D]: rows r0 .. r0 + srows - 1
+    float *sl;              // [slots][srows][heads]
     int heads;
+    uint64_t r0, srows;     // the rows with partials (the even split: all rows)
 };
 
 // The split kernels' workgroup (row group x, head group y, split z). When the
@@ -1754,7 +1760,50 @@ struct SplitIds {
     }
 };
 
-template <int D, int HPW, bool POW2, int NW>
+// A split workgroup's key ranges, walked in turn: row group rg, tiles
+// [tb, te), partial slot (-1: the row group's whole range, its output
+// written directly). One range under the even split, one or two paired.
+struct SplitSeg {
+    int rg, tb, te, slot;
+};
+
+template <bool PAIRED>
+struct SplitSegs {
+    int n;
+    SplitSeg s0, s1;
+    __device__ __forceinline__ SplitSegs(const PrefillArgs &a, const SplitIds &sid, uint64_t rpw)
+    {
+        const int R = static_cast<int>(gridDim.x);
+        s1 = SplitSeg{0, 0, 0, -1};
+        if constexpr (!PAIRED) {
+            const int rg = R - 1 - sid.x;                          // heaviest rows first
+            const int ntiles = static_cast<int>(causal_tiles(a.past, a.rows, rg, rpw));
+            const int nz = static_cast<int>(gridDim.z), per = (ntiles + nz - 1) / nz;
+            const int tb = sid.z * per < ntiles ? sid.z * per : ntiles;
+            n = 1;
+            s0 = SplitSeg{rg, tb, tb + per < ntiles ? tb + per : ntiles, sid.z};
+        } else {
+            // every workgroup starts at tile 0, so that the workgroups of a KV
+            // head on one XCD walk the same tiles at about the same time and
+            // its L2 serves all but the first; the light ones then walk the
+            // last tiles of their partners' row groups
+            const int i = sid.x < R - 1 - sid.x ? sid.x : R - 1 - sid.x, j = R - 1 - i;
+            const int ti = static_cast<int>(causal_tiles(a.past, a.rows, i, rpw));
+            const int tj = static_cast<int>(causal_tiles(a.past, a.rows, j, rpw));
+            const int h = i < j ? static_cast<int>(pair_share(ti, tj)) : 0;
+            if (sid.x == i) {
+                n = h > 0 ? 2 : 1;
+                s0 = SplitSeg{i, 0, ti, -1};
+                s1 = SplitSeg{j, tj - h, tj, 1};
+            } else {
+                n = 1;
+                s0 = SplitSeg{j, 0, tj - h, h > 0 ? 0 : -1};
+            }
+        }
+    }
+};
+
+template <int D, int HPW, bool POW2, int NW, bool PAIRED = false>
 __global__ __launch_bounds__(64 * NW, 1) void prefill_split_max(PrefillArgs a, SplitArgs sp)
 {
     constexpr int RB = NW / HPW, THREADS = 64 * NW;
@@ -1765,64 +1814,68 @@ __global__ __launch_bounds__(64 * NW, 1) void prefill_split_max(PrefillArgs a, S
     const SplitIds sid;
     const int head = sid.y * HPW + (wave % HPW);
     const int kvh = head / a.gqa;
-    const uint64_t rgroup = gridDim.x - 1 - sid.x;
-    const uint64_t wg_r0 = rgroup * (32 * RB);
-    const uint64_t w_r0 = wg_r0 + 32 * (wave / HPW);
-    const uint64_t row = w_r0 + col;
-    const bool rowv = row < a.rows;
-    const bool wact = w_r0 < a.rows;
-    const uint64_t wg_rend = wg_r0 + 32 * RB < a.rows ? wg_r0 + 32 * RB : a.rows;
-    const int ntiles = static_cast<int>((a.past + wg_rend + kKeyTile - 1) / kKeyTile);
-    const int nfull = wact ? static_cast<int>((a.past + w_r0 + 1) / kKeyTile) : 0;
-    const uint64_t lim = a.past + row;
-    const int per = (ntiles + static_cast<int>(gridDim.z) - 1) / static_cast<int>(gridDim.z);
-    const int tb = sid.z * per < ntiles ? sid.z * per : ntiles;
-    const int te = tb + per < ntiles ? tb + per : ntiles;
-
+    const SplitSegs<PAIRED> segs(a, sid, 32 * RB);
     const uint16_t *kg = a.k + static_cast<uint64_t>(kvh) * a.kv_stride;
-    u32x4 kr[Tile<D, THREADS>::kPer];
-    u32x4 qb[D / 16];
-    const uint16_t *qp = a.q + (rowv ? row : 0) * a.q_row + static_cast<uint64_t>(head) * a.q_head;
-#pragma unroll
-    for (int s = 0; s < D / 16; s++) {
-        const u32x4 v = load16(qp + 16 * s + 8 * grp);
-        qb[s] = rowv ? v : u32x4{0, 0, 0, 0};
-    }
     const int arow = swap23(col) * SK + 8 * grp;
-    float m = kNegInf;
-    if (tb < te) {
-        tile_gload<D, THREADS, false>(kg, static_cast<uint64_t>(tb) * kKeyTile, a.n, tid, kr);
-        tile_lstore_padded<D, THREADS>(kb[0], SK, tid, kr);
-        __syncthreads();
-        for (int t = tb; t < te; t++) {
-            const uint64_t t0 = static_cast<uint64_t>(t) * kKeyTile;
-            const bool last = t + 1 == te;
-            if (!last) tile_gload<D, THREADS, false>(kg, t0 + kKeyTile, a.n, tid, kr);
-            __builtin_amdgcn_sched_barrier(0);
-            const uint16_t *kt = kb[(t - tb) & 1];
-            f32x16 acc = {};
+    // one key range, then (paired) the second: the body is instantiated for
+    // each, so that no register stays live from one to the other
+    auto run = [&](const SplitSeg sg) {
+        const uint64_t wg_r0 = static_cast<uint64_t>(sg.rg) * (32 * RB);
+        const uint64_t w_r0 = wg_r0 + 32 * (wave / HPW);
+        const uint64_t row = w_r0 + col;
+        const bool rowv = row < a.rows;
+        const bool wact = w_r0 < a.rows;
+        const int nfull = wact ? static_cast<int>((a.past + w_r0 + 1) / kKeyTile) : 0;
+        const uint64_t lim = a.past + row;
+        const int tb = sg.tb, te = sg.te;
+
+        u32x4 kr[Tile<D, THREADS>::kPer];
+        u32x4 qb[D / 16];
+        const uint16_t *qp = a.q + (rowv ? row : 0) * a.q_row + static_cast<uint64_t>(head) * a.q_head;
 #pragma unroll
-            for (int s = 0; s < D / 16; s++) acc = mfma(load16(kt + arow + 16 * s), qb[s], acc);
-            if (t < nfull) {
-#pragma unroll
-                for (int r = 0; r < 16; r++) m = __builtin_fmaxf(m, POW2 ? acc[r] : acc[r] * a.scale);
-            } else {
-                const int vis = static_cast<int>(static_cast<int64_t>(lim) - static_cast<int64_t>(t0));
-#pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    const float s = POW2 ? acc[r] : acc[r] * a.scale;
-                    if (key_of(r, grp) <= vis) m = __builtin_fmaxf(m, s);
-                }
-            }
-            if (!last) tile_lstore_padded<D, THREADS>(kb[(t - tb + 1) & 1], SK, tid, kr);
-            __syncthreads();
+        for (int s = 0; s < D / 16; s++) {
+            const u32x4 v = load16(qp + 16 * s + 8 * grp);
+            qb[s] = rowv ? v : u32x4{0, 0, 0, 0};
         }
-    }
-    m = __builtin_fmaxf(m, __shfl_xor(m, 32));
-    if (rowv && grp == 0) sp.smax[(static_cast<uint64_t>(sid.z) * sp.heads + head) * a.rows + row] = m;
+        float m = kNegInf;
+        if (tb < te) {
+            tile_gload<D, THREADS, false>(kg, static_cast<uint64_t>(tb) * kKeyTile, a.n, tid, kr);
+            tile_lstore_padded<D, THREADS>(kb[0], SK, tid, kr);
+            __syncthreads();
+            // as prefill_attn's pass 1: the next tile's load is not branched
+            // around (past the cache it reads row 0, unused)
+            for (int t = tb; t < te; t++) {
+                const uint64_t t0 = static_cast<uint64_t>(t) * kKeyTile;
+                tile_gload<D, THREADS, false>(kg, t0 + kKeyTile, a.n, tid, kr);
+                __builtin_amdgcn_sched_barrier(0);
+                const uint16_t *kt = kb[(t - tb) & 1];
+                f32x16 acc = {};
+#pragma unroll
+                for (int s = 0; s < D / 16; s++) acc = mfma(load16(kt + arow + 16 * s), qb[s], acc);
+                if (t < nfull) {
+#pragma unroll
+                    for (int r = 0; r < 16; r++) m = __builtin_fmaxf(m, POW2 ? acc[r] : acc[r] * a.scale);
+                } else {
+                    const int vis = static_cast<int>(static_cast<int64_t>(lim) - static_cast<int64_t>(t0));
+#pragma unroll
+                    for (int r = 0; r < 16; r++) {
+                        const float s = POW2 ? acc[r] : acc[r] * a.scale;
+                        if (key_of(r, grp) <= vis) m = __builtin_fmaxf(m, s);
+                    }
+                }
+                if (t + 1 < te) tile_lstore_padded<D, THREADS>(kb[(t - tb + 1) & 1], SK, tid, kr);
+                __syncthreads();
+            }
+        }
+        m = __builtin_fmaxf(m, __shfl_xor(m, 32));
+        const int slot = sg.slot < 0 ? 0 : sg.slot;
+        if (rowv && grp == 0) sp.smax[(static_cast<uint64_t>(slot) * sp.heads + head) * a.rows + row] = m;
+    };
+    run(segs.s0);
+    if (PAIRED && segs.n > 1) run(segs.s1);
 }
 
-template <int D, int HPW, bool POW2, int NW>
+template <int D, int HPW, bool POW2, int NW, bool PAIRED = false>
 __global__ __launch_bounds__(64 * NW, 1) void prefill_split_pv(PrefillArgs a, SplitArgs sp)
 {
     constexpr int RB = NW / HPW, THREADS = 64 * NW;
@@ -1834,108 +1887,151 @@ __global__ __launch_bounds__(64 * NW, 1) void prefill_split_pv(PrefillArgs a, Sp
     const SplitIds sid;
     const int head = sid.y * HPW + (wave % HPW);
     const int kvh = head / a.gqa;
-    const uint64_t rgroup = gridDim.x - 1 - sid.x;
-    const uint64_t wg_r0 = rgroup * (32 * RB);
-    const uint64_t w_r0 = wg_r0 + 32 * (wave / HPW);
-    const uint64_t row = w_r0 + col;
-    const bool rowv = row < a.rows;
-    const bool wact = w_r0 < a.rows;
-    const uint64_t wg_rend = wg_r0 + 32 * RB < a.rows ? wg_r0 + 32 * RB : a.rows;
-    const int ntiles = static_cast<int>((a.past + wg_rend + kKeyTile - 1) / kKeyTile);
-    const int nfull = wact ? static_cast<int>((a.past + w_r0 + 1) / kKeyTile) : 0;
-    const uint64_t lim = a.past + row;
-    const int nz = static_cast<int>(gridDim.z);
-    const int per = (ntiles + nz - 1) / nz;
-    const int tb = sid.z * per < ntiles ? sid.z * per : ntiles;
-    const int te = tb + per < ntiles ? tb + per : ntiles;
-
-    // the exact row maximum: the largest of the splits' partial maxima (rows
-    // past the chunk take 0: computed, never stored)
-    float m = rowv ? kNegInf : 0.0f;
-    if (rowv)
-        for (int z = 0; z < nz; z++) m = __builtin_fmaxf(m, sp.smax[(static_cast<uint64_t>(z) * sp.heads + head) * a.rows + row]);
-    ExpArgs ex;
-    ex.m = m;
-    ex.scale = a.scale;
-    ex.clamp = POW2 ? -87.33654f / a.scale : -87.33654f;
-    ex.mul = POW2 ? 1.442695f * a.scale : 1.442695f;
-
+    const SplitSegs<PAIRED> segs(a, sid, 32 * RB);
     const uint16_t *kg = a.k + static_cast<uint64_t>(kvh) * a.kv_stride;
     const uint16_t *vg = a.v + static_cast<uint64_t>(kvh) * a.kv_stride;
-    u32x4 kr[Tile<D, THREADS>::kPer], vr[Tile<D, THREADS>::kPer];
-    u32x4 qb[D / 16];
-    const uint16_t *qp = a.q + (rowv ? row : 0) * a.q_row + static_cast<uint64_t>(head) * a.q_head;
-#pragma unroll
-    for (int s = 0; s < D / 16; s++) {
-        const u32x4 v = load16(qp + 16 * s + 8 * grp);
-        qb[s] = rowv ? v : u32x4{0, 0, 0, 0};
-    }
     const int arow = swap23(col) * SK + 8 * grp;
-    f32x16 o[D / 32];
-#pragma unroll
-    for (int dt = 0; dt < D / 32; dt++) o[dt] = f32x16{};
-    float lsum = 0.0f;
-    if (tb < te) {
-        tile_gload<D, THREADS, false>(kg, static_cast<uint64_t>(tb) * kKeyTile, a.n, tid, kr);
-        tile_gload<D, THREADS, false>(vg, static_cast<uint64_t>(tb) * kKeyTile, a.n, tid, vr);
-        tile_lstore_padded<D, THREADS>(kb[0], SK, tid, kr);
-        tile_mask<D, THREADS>(static_cast<uint64_t>(tb) * kKeyTile, a.n, tid, vr);
-        tile_lstore_padded<D, THREADS>(vb[0], SV, tid, vr);
-        __syncthreads();
-        for (int t = tb; t < te; t++) {
-            const uint64_t t0 = static_cast<uint64_t>(t) * kKeyTile;
-            const int b = (t - tb) & 1;
-            const bool last = t + 1 == te;
-            if (!last) tile_gload<D, THREADS, false>(kg, t0 + kKeyTile, a.n, tid, kr);
-            __builtin_amdgcn_sched_barrier(0);
-            f32x16 acc = {};
-#pragma unroll
-            for (int s = 0; s < D / 16; s++) acc = mfma(load16(kb[b] + arow + 16 * s), qb[s], acc);
-            const bool full = t < nfull;
-            const int vis = static_cast<int>(static_cast<int64_t>(lim) - static_cast<int64_t>(t0));
-#pragma unroll
-            for (int h = 0; h < 2; h++) {
-                float ev[8];
-#pragma unroll
-                for (int r = 0; r < 8; r++) {
-                    const float e = exp_score<POW2>(acc[8 * h + r], ex);
-                    ev[r] = full || key_of(8 * h + r, grp) <= vis ? e : 0.0f;
-                    lsum += ev[r];
-                }
-                u32x4 hi, lo;
-                split_pack_hw(ev, hi, lo);
-                if (h == 0 && !last) tile_gload<D, THREADS, false>(vg, t0 + kKeyTile, a.n, tid, vr);
-                __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-                for (int dt = 0; dt < D / 32; dt++) {
-                    const u32x4 av = vt_operand_padded<D>(vb[b], 16 * h, 32 * dt, l);
-                    o[dt] = mfma(av, hi, o[dt]);
-                    o[dt] = mfma(av, lo, o[dt]);
-                }
-            }
-            if (!last) {
-                tile_lstore_padded<D, THREADS>(kb[b ^ 1], SK, tid, kr);
-                tile_mask<D, THREADS>(t0 + kKeyTile, a.n, tid, vr);
-                tile_lstore_padded<D, THREADS>(vb[b ^ 1], SV, tid, vr);
-            }
-            __syncthreads();
+    auto run = [&](const SplitSeg sg, auto direct_t) {
+        constexpr bool DIRECT = decltype(direct_t)::value;   // a whole row group: output written directly
+        const uint64_t wg_r0 = static_cast<uint64_t>(sg.rg) * (32 * RB);
+        const uint64_t w_r0 = wg_r0 + 32 * (wave / HPW);
+        const uint64_t row = w_r0 + col;
+        const bool rowv = row < a.rows;
+        const bool wact = w_r0 < a.rows;
+        const int nfull = wact ? static_cast<int>((a.past + w_r0 + 1) / kKeyTile) : 0;
+        const uint64_t lim = a.past + row;
+        const int tb = sg.tb, te = sg.te;
+
+        // the exact row maximum: the largest of the partial maxima (rows past
+        // the chunk take 0: computed, never stored); a whole row group's is
+        // in slot 0
+        float m = rowv ? kNegInf : 0.0f;
+        if (rowv) {
+            const int nz = PAIRED ? (DIRECT ? 1 : 2) : static_cast<int>(gridDim.z);
+            for (int z = 0; z < nz; z++)
+                m = __builtin_fmaxf(m, sp.smax[(static_cast<uint64_t>(z) * sp.heads + head) * a.rows + row]);
         }
-    }
-    lsum += __shfl_xor(lsum, 32);
-    if (rowv) {
-        const uint64_t cell = (static_cast<uint64_t>(sid.z) * a.rows + row) * sp.heads + head;
-        float *op = sp.so + cell * D;
+        ExpArgs ex;
+        ex.m = m;
+        ex.scale = a.scale;
+        ex.clamp = POW2 ? -87.33654f / a.scale : -87.33654f;
+        ex.mul = POW2 ? 1.442695f * a.scale : 1.442695f;
+
+        u32x4 kr[Tile<D, THREADS>::kPer], vr[Tile<D, THREADS>::kPer];
+        u32x4 qb[D / 16];
+        const uint16_t *qp = a.q + (rowv ? row : 0) * a.q_row + static_cast<uint64_t>(head) * a.q_head;
 #pragma unroll
-        for (int dt = 0; dt < D / 32; dt++)
+        for (int s = 0; s < D / 16; s++) {
+            const u32x4 v = load16(qp + 16 * s + 8 * grp);
+            qb[s] = rowv ? v : u32x4{0, 0, 0, 0};
+        }
+        f32x16 o[D / 32];
 #pragma unroll
-            for (int c = 0; c < 4; c++)
-                *reinterpret_cast<f32x4 *>(op + 32 * dt + 8 * c + 4 * grp) =
-                    f32x4{o[dt][4 * c], o[dt][4 * c + 1], o[dt][4 * c + 2], o[dt][4 * c + 3]};
-        if (grp == 0) sp.sl[cell] = lsum;
+        for (int dt = 0; dt < D / 32; dt++) o[dt] = f32x16{};
+        float lsum = 0.0f;
+        if (tb < te) {
+            tile_gload<D, THREADS, false>(kg, static_cast<uint64_t>(tb) * kKeyTile, a.n, tid, kr);
+            tile_gload<D, THREADS, false>(vg, static_cast<uint64_t>(tb) * kKeyTile, a.n, tid, vr);
+            tile_lstore_padded<D, THREADS>(kb[0], SK, tid, kr);
+            tile_mask<D, THREADS>(static_cast<uint64_t>(tb) * kKeyTile, a.n, tid, vr);
+            tile_lstore_padded<D, THREADS>(vb[0], SV, tid, vr);
+            __syncthreads();
+            // as prefill_attn's pass 2: loads not branched around, the masked
+            // and unmasked halves of a tile instantiated apart, the P.V MFMAs
+            // at raised priority
+            for (int t = tb; t < te; t++) {
+                const uint64_t t0 = static_cast<uint64_t>(t) * kKeyTile;
+                const int b = (t - tb) & 1;
+                tile_gload<D, THREADS, false>(kg, t0 + kKeyTile, a.n, tid, kr);  // past the cache: row 0, unused
+                __builtin_amdgcn_sched_barrier(0);
+                f32x16 acc = {};
+#pragma unroll
+                for (int s = 0; s < D / 16; s++) acc = mfma(load16(kb[b] + arow + 16 * s), qb[s], acc);
+                const bool full = t < nfull;
+                const int vis = static_cast<int>(static_cast<int64_t>(lim) - static_cast<int64_t>(t0));
+                auto half = [&](int h, auto masked, u32x4 &hi, u32x4 &lo) {
+                    constexpr bool MASKED = decltype(masked)::value;
+                    float ev[8];
+#pragma unroll
+                    for (int r = 0; r < 8; r++) {
+                        const float e = exp_score<POW2>(acc[8 * h + r], ex);
+                        ev[r] = !MASKED || key_of(8 * h + r, grp) <= vis ? e : 0.0f;
+                        lsum += ev[r];
+                    }
+                    split_pack_hw(ev, hi, lo);
+                };
+                auto pv = [&](int h, const u32x4 &hi, const u32x4 &lo) {
+                    __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+                    for (int dt = 0; dt < D / 32; dt++) {
+                        const u32x4 av = vt_operand_padded<D>(vb[b], 16 * h, 32 * dt, l);
+                        o[dt] = mfma(av, hi, o[dt]);
+                        o[dt] = mfma(av, lo, o[dt]);
+                    }
+                    __builtin_amdgcn_s_setprio(0);
+                };
+                u32x4 hi, lo;
+                if (full) half(0, std::false_type{}, hi, lo);
+                else half(0, std::true_type{}, hi, lo);
+                tile_gload<D, THREADS, false>(vg, t0 + kKeyTile, a.n, tid, vr);
+                __builtin_amdgcn_sched_barrier(0);
+                pv(0, hi, lo);
+                if (full) half(1, std::false_type{}, hi, lo);
+                else half(1, std::true_type{}, hi, lo);
+                pv(1, hi, lo);
+                if (t + 1 < te) {
+                    tile_lstore_padded<D, THREADS>(kb[b ^ 1], SK, tid, kr);
+                    tile_mask<D, THREADS>(t0 + kKeyTile, a.n, tid, vr);
+                    tile_lstore_padded<D, THREADS>(vb[b ^ 1], SV, tid, vr);
+                }
+                __syncthreads();
+            }
+        }
+        lsum += __shfl_xor(lsum, 32);
+        if (!rowv) return;
+        if constexpr (DIRECT) {
+            // a whole row group: its output, as prefill_attn writes it
+            uint16_t *op = a.out + row * a.out_row + static_cast<uint64_t>(head) * D;
+            const uint16_t *gp = a.gate ? a.gate + row * a.gate_row + static_cast<uint64_t>(head) * D : nullptr;
+#pragma unroll
+            for (int dt = 0; dt < D / 32; dt++)
+#pragma unroll
+                for (int c = 0; c < 4; c++) {
+                    uint32_t b0 = cvt_out(o[dt][4 * c] / lsum), b1 = cvt_out(o[dt][4 * c + 1] / lsum);
+                    uint32_t b2 = cvt_out(o[dt][4 * c + 2] / lsum), b3 = cvt_out(o[dt][4 * c + 3] / lsum);
+                    const int at = 32 * dt + 8 * c + 4 * grp;
+                    if (gp) {
+                        const uint2 g = *reinterpret_cast<const uint2 *>(gp + at);
+                        b0 = gate_bf16(static_cast<uint16_t>(b0), static_cast<uint16_t>(g.x));
+                        b1 = gate_bf16(static_cast<uint16_t>(b1), static_cast<uint16_t>(g.x >> 16));
+                        b2 = gate_bf16(static_cast<uint16_t>(b2), static_cast<uint16_t>(g.y));
+                        b3 = gate_bf16(static_cast<uint16_t>(b3), static_cast<uint16_t>(g.y >> 16));
+                    }
+                    *reinterpret_cast<uint2 *>(op + at) = uint2{b0 | (b1 << 16), b2 | (b3 << 16)};
+                }
+        } else {
+            const uint64_t cell = (static_cast<uint64_t>(sg.slot) * sp.srows + (row - sp.r0)) * sp.heads + head;
+            float *op = sp.so + cell * D;
+#pragma unroll
+            for (int dt = 0; dt < D / 32; dt++)
+#pragma unroll
+                for (int c = 0; c < 4; c++)
+                    *reinterpret_cast<f32x4 *>(op + 32 * dt + 8 * c + 4 * grp) =
+                        f32x4{o[dt][4 * c], o[dt][4 * c + 1], o[dt][4 * c + 2], o[dt][4 * c + 3]};
+            if (grp == 0) sp.sl[cell] = lsum;
+        }
+    };
+    if constexpr (PAIRED) {
+        // a light workgroup: its row group whole, then its partner's tail
+        if (segs.s0.slot < 0) run(segs.s0, std::true_type{});
+        else run(segs.s0, std::false_type{});
+        if (segs.n > 1) run(segs.s1, std::false_type{});
+    } else {
+        run(segs.s0, std::false_type{});
     }
 }
 
-// grid (rows, heads), D threads: one output element each.
+// grid (rows with partials, heads), D threads: one output element each.
 template <int D>
 __global__ __launch_bounds__(D) void prefill_split_combine(PrefillArgs a, SplitArgs sp, int splits);
 
@@ -1955,7 +2051,7 @@ template <int D, int HPW, int NW, bool POW2_FORM = true>
 static hipError_t launch_prefill_split(const PrefillArgs &a, int heads, const PrefillSplit &ps, dim3 grid, int splits,
                                        hipStream_t s)
 {
-    const SplitArgs sp{ps.smax, ps.so, ps.sl, heads};
+    const SplitArgs sp{ps.smax, ps.so, ps.sl, heads, 0, a.rows};
     const dim3 gs(grid.x, grid.y, static_cast<unsigned>(splits));
     hipError_t e;
     if (POW2_FORM && scale_is_pow2(a.scale)) {
@@ -1969,14 +2065,33 @@ static hipError_t launch_prefill_split(const PrefillArgs &a, int heads, const Pr
     return launch(prefill_split_combine<D>, dim3(static_cast<unsigned>(a.rows), heads), dim3(D), s, a, sp, splits);
 }
 
+// The paired form on the causal kernel's grid (row groups, head groups); pr
+// from prefill_pairs.
+template <int D, int HPW, int NW, bool POW2_FORM = true>
+static hipError_t launch_prefill_paired(const PrefillArgs &a, int heads, const PrefillSplit &ps, dim3 grid,
+                                        const PairRows &pr, hipStream_t s)
+{
+    const SplitArgs sp{ps.smax, ps.so, ps.sl, heads, pr.r0, pr.srows};
+    hipError_t e;
+    if (POW2_FORM && scale_is_pow2(a.scale)) {
+        e = launch(prefill_split_max<D, HPW, POW2_FORM, NW, true>, grid, dim3(64 * NW), s, a, sp);
+        if (e == hipSuccess) e = launch(prefill_split_pv<D, HPW, POW2_FORM, NW, true>, grid, dim3(64 * NW), s, a, sp);
+    } else {
+        e = launch(prefill_split_max<D, HPW, false, NW, true>, grid, dim3(64 * NW), s, a, sp);
+        if (e == hipSuccess) e = launch(prefill_split_pv<D, HPW, false, NW, true>, grid, dim3(64 * NW), s, a, sp);
+    }
+    if (e != hipSuccess) return e;
+    return launch(prefill_split_combine<D>, dim3(static_cast<unsigned>(pr.srows), heads), dim3(D), s, a, sp, 2);
+}
+
 template <int D>
 __global__ __launch_bounds__(D) void prefill_split_combine(PrefillArgs a, SplitArgs sp, int splits)
 {
-    const uint64_t row = blockIdx.x, head = blockIdx.y;
+    const uint64_t row = sp.r0 + blockIdx.x, head = blockIdx.y;
     const int dim = threadIdx.x;
     float o = 0.0f, ls = 0.0f;
     for (int z = 0; z < splits; z++) {
-        const uint64_t cell = (static_cast<uint64_t>(z) * a.rows + row) * sp.heads + head;
+        const uint64_t cell = (static_cast<uint64_t>(z) * sp.srows + blockIdx.x) * sp.heads + head;
         o += sp.so[cell * D + dim];
         ls += sp.sl[cell];
     }

@@ -53,6 +53,8 @@ static hipError_t prefill_more_d(const PrefillArgs &a, int heads, const PrefillS
     const dim3 grid(static_cast<unsigned>((a.rows + ROWS - 1) / ROWS), heads);
     const int splits = prefill_splits(a, static_cast<uint64_t>(grid.x) * grid.y, heads, ps);
     if (splits > 1) return launch_prefill_split<D, 1, NW, false>(a, heads, ps, grid, splits, s);
+    const PairRows pr = prefill_pairs(a, grid.x, static_cast<uint64_t>(grid.x) * grid.y, ROWS, heads, ps);
+    if (pr.srows) return launch_prefill_paired<D, 1, NW, false>(a, heads, ps, grid, pr, s);
     return launch(prefill_attn<D, 1, false, NW>, grid, dim3(64 * NW), s, a);
 }
 

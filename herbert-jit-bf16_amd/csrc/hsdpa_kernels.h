@@ -85,12 +85,14 @@ struct PrefillArgs {
 // The split form of the causal kernel (see prefill_split_max): workspace for
 // its partial maxima, outputs and sums, and what the launcher needs to choose
 // the number of splits. units: the most (split, 32-row group, head) cells the
-// workspace holds. No split when units is 0.
+// workspace holds (so and sl: 32 rows of each); smax holds kSplitMaxCells
+// floats per unit. No split when units is 0.
 struct PrefillSplit {
     float *smax, *so, *sl;
     uint64_t units;
     int cus;
 };
+constexpr uint64_t kSplitMaxCells = 128;
 
 // Constants of the kernels the host needs to size grids and workspaces.
 constexpr int kKeyTile = 32;          // keys per MFMA key block
@@ -195,6 +197,10 @@ hipError_t launch_decode(const DecodeArgs &a, int head_dim, int kv_heads, hipStr
 hipError_t launch_prefill(const PrefillArgs &a, int head_dim, int heads, const PrefillSplit &ps, hipStream_t s);
 // the key splits launch_prefill would choose (1: the one-workgroup kernel)
 int prefill_split_count(const PrefillArgs &a, int head_dim, int heads, const PrefillSplit &ps);
+struct PairRows;
+// the rows with partials of the paired form launch_prefill would choose
+// (srows 0: not paired)
+PairRows prefill_pair_rows(const PrefillArgs &a, int head_dim, int heads, const PrefillSplit &ps);
 // the head dimensions other than 64, 128 and 256 (hsdpa_attn_more.hip)
 hipError_t launch_decode_more(const DecodeArgs &a, int head_dim, int kv_heads, hipStream_t s);
 // the Fused form of the decode passes, head dimensions 32 to 256 (hsdpa_fused.hip)
@@ -232,6 +238,60 @@ inline int prefill_splits(const PrefillArgs &a, uint64_t wgs, int heads, const P
     const uint64_t cells = (a.rows + 31) / 32 * static_cast<uint64_t>(heads);
     if (s > ps.units / cells) s = ps.units / cells;
     return s >= 2 ? static_cast<int>(s) : 1;
+}
+
+// The paired form of the causal kernel, for a grid of R row groups (rpw rows
+// each) x head groups that the compute units hold in one round: row group r
+// sees causal_tiles(r) key tiles, more the later it lies, and the round lasts
+// as long as its longest workgroup. Row groups i and j = R - 1 - i (i < j) are
+// paired: j's last h = (T_j - T_i) / 2 tiles go to i's workgroup, which walks
+// them after its own row group, so that the two workgroups walk T_i + h and
+// T_j - h tiles. The split row groups (the last ones) pass partial outputs to
+// a combine: slot 0 the head, slot 1 the tail.
+constexpr uint64_t kPairMinTiles = 4;
+
+__host__ __device__ inline uint64_t causal_tiles(uint64_t past, uint64_t rows, uint64_t r, uint64_t rpw)
+{
+    const uint64_t e = (r + 1) * rpw < rows ? (r + 1) * rpw : rows;
+    return (past + e + kKeyTile - 1) / kKeyTile;
+}
+
+__host__ __device__ inline uint64_t pair_share(uint64_t ti, uint64_t tj)
+{
+    const uint64_t h = (tj - ti) / 2;
+    return h >= kPairMinTiles ? h : 0;
+}
+
+// The rows with partials of a paired call: [r0, r0 + srows); srows 0 when the
+// call is not paired. Paired when one round of the grid holds it, its longest
+// row group sees at least kPairMinLongest tiles (below, the two extra launches
+// and the second range's first loads cost more than the balance saves: 1000
+// rows at D 64, 32 tiles, 56.7 -> 60.9 us), pairing shortens its longest
+// workgroup by at least an eighth, and the partials fit the workspace.
+constexpr uint64_t kPairMinLongest = 64;
+struct PairRows {
+    uint64_t r0, srows;
+};
+
+inline PairRows prefill_pairs(const PrefillArgs &a, uint64_t R, uint64_t wgs, uint64_t rpw, int heads,
+                              const PrefillSplit &ps)
+{
+    const PairRows none{0, 0};
+    if (ps.units == 0 || ps.cus <= 0 || R < 2 || wgs > static_cast<uint64_t>(ps.cus)) return none;
+    uint64_t longest = R % 2 ? causal_tiles(a.past, a.rows, R / 2, rpw) : 0, split = 0;
+    for (uint64_t i = 0; i < R - 1 - i; i++) {
+        const uint64_t ti = causal_tiles(a.past, a.rows, i, rpw), tj = causal_tiles(a.past, a.rows, R - 1 - i, rpw);
+        const uint64_t h = pair_share(ti, tj);
+        const uint64_t w = ti + h > tj - h ? ti + h : tj - h;
+        if (w > longest) longest = w;
+        if (h) split = i + 1;
+    }
+    const uint64_t tmax = causal_tiles(a.past, a.rows, R - 1, rpw);
+    if (split == 0 || tmax < kPairMinLongest || 8 * longest > 7 * tmax) return none;
+    const uint64_t r0 = (R - split) * rpw, srows = a.rows - r0;
+    const uint64_t h = static_cast<uint64_t>(heads);
+    if (2 * srows * h > ps.units * 32 || 2 * a.rows * h > ps.units * kSplitMaxCells) return none;
+    return PairRows{r0, srows};
 }
 
 }  // namespace hsdpa

@@ -336,15 +336,23 @@ hipError_t launch_decode(const DecodeArgs &a, int head_dim, int kv_heads, hipStr
 // The causal kernel's grid: (row groups, head groups) of HPW query heads x
 // 32 * 8 / HPW rows at the tuned head dimensions (HPW the largest of 8, 4, 2
 // that divides the group size), one head x 32 NW rows at the others.
+static int prefill_hpw(const PrefillArgs &a, int head_dim)
+{
+    if (head_dim == 64 || head_dim == 128 || head_dim == 256)
+        return a.gqa % 8 == 0 ? 8 : a.gqa % 4 == 0 ? 4 : a.gqa % 2 == 0 ? 2 : 1;
+    return 1;
+}
+
+static uint64_t prefill_rows_per_wg(const PrefillArgs &a, int head_dim)
+{
+    if (head_dim == 64 || head_dim == 128 || head_dim == 256) return 32 * (8 / prefill_hpw(a, head_dim));
+    return 32 * (head_dim > 256 ? 4 : 8);
+}
+
 static dim3 prefill_grid(const PrefillArgs &a, int head_dim, int heads)
 {
-    if (head_dim == 64 || head_dim == 128 || head_dim == 256) {
-        const int hpw = a.gqa % 8 == 0 ? 8 : a.gqa % 4 == 0 ? 4 : a.gqa % 2 == 0 ? 2 : 1;
-        const uint64_t rows_per_wg = 32 * (8 / hpw);
-        return dim3(static_cast<unsigned>((a.rows + rows_per_wg - 1) / rows_per_wg), heads / hpw);
-    }
-    const uint64_t rows_per_wg = 32 * (head_dim > 256 ? 4 : 8);
-    return dim3(static_cast<unsigned>((a.rows + rows_per_wg - 1) / rows_per_wg), heads);
+    const uint64_t rows_per_wg = prefill_rows_per_wg(a, head_dim);
+    return dim3(static_cast<unsigned>((a.rows + rows_per_wg - 1) / rows_per_wg), heads / prefill_hpw(a, head_dim));
 }
 
 int prefill_split_count(const PrefillArgs &a, int head_dim, int heads, const PrefillSplit &ps)
@@ -353,12 +361,21 @@ int prefill_split_count(const PrefillArgs &a, int head_dim, int heads, const Pre
     return prefill_splits(a, static_cast<uint64_t>(g.x) * g.y, heads, ps);
 }
 
+PairRows prefill_pair_rows(const PrefillArgs &a, int head_dim, int heads, const PrefillSplit &ps)
+{
+    const dim3 g = prefill_grid(a, head_dim, heads);
+    if (prefill_splits(a, static_cast<uint64_t>(g.x) * g.y, heads, ps) > 1) return PairRows{0, 0};
+    return prefill_pairs(a, g.x, static_cast<uint64_t>(g.x) * g.y, prefill_rows_per_wg(a, head_dim), heads, ps);
+}
+
 template <int D, int HPW>
 static hipError_t prefill_dh(const PrefillArgs &a, int heads, const PrefillSplit &ps, hipStream_t s)
 {
     const dim3 grid = prefill_grid(a, D, heads);
     const int splits = prefill_splits(a, static_cast<uint64_t>(grid.x) * grid.y, heads, ps);
     if (splits > 1) return launch_prefill_split<D, HPW, 8>(a, heads, ps, grid, splits, s);
+    const PairRows pr = prefill_pairs(a, grid.x, static_cast<uint64_t>(grid.x) * grid.y, 32 * (8 / HPW), heads, ps);
+    if (pr.srows) return launch_prefill_paired<D, HPW, 8>(a, heads, ps, grid, pr, s);
     if (scale_is_pow2(a.scale)) return launch(prefill_attn<D, HPW, true>, grid, dim3(512), s, a);
     return launch(prefill_attn<D, HPW, false>, grid, dim3(512), s, a);
 }

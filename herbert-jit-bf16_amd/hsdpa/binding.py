@@ -25,7 +25,7 @@ STATUS = {
 STATIC_SCRATCH_BYTES = 32 << 20
 FORMS = {"chained": 0, "fused": 1}
 KERNELS = {0: "none", 1: "decode", 2: "few_rows", 3: "causal", 4: "causal_split", 5: "decode_rows",
-           6: "causal_short"}
+           6: "causal_short", 7: "causal_paired"}
 EXPORTS = ["hsdpa_plan_create", "hsdpa_plan_destroy", "hsdpa_workspace_bytes", "hsdpa_attention",
            "hsdpa_status_string", "hsdpa_version", "hsdpa_kv_check", "hsdpa_kv_append",
            "hsdpa_head_norm_rope", "hsdpa_output_gate", "hsdpa_kv_restore", "hsdpa_kv_take",

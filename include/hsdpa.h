@@ -160,7 +160,8 @@ typedef enum hsdpa_kernels {
     HSDPA_KERNELS_CAUSAL = 3,         /* the causal kernel, one workgroup per row group */
     HSDPA_KERNELS_CAUSAL_SPLIT = 4,   /* the causal kernel split over the keys (maxima, P.V, combine) */
     HSDPA_KERNELS_DECODE_ROWS = 5,    /* one decode per row, in turn */
-    HSDPA_KERNELS_CAUSAL_SHORT = 6    /* a short chunk: each 32-row block's keys split among its waves */
+    HSDPA_KERNELS_CAUSAL_SHORT = 6,   /* a short chunk: each 32-row block's keys split among its waves */
+    HSDPA_KERNELS_CAUSAL_PAIRED = 7   /* the causal kernel's light and heavy row groups paired (maxima, P.V, combine) */
 } hsdpa_kernels;
 
 typedef struct hsdpa_route {

@@ -110,13 +110,15 @@ def test_workspace_follows_max_rows_and_form():
 def test_route_names_the_kernels():
     """hsdpa_attention_route reports what a call would run, with no device:
     the decode passes for one row, (row, head) columns for a few rows, the
-    causal kernel or its split form otherwise; under the Fused form the rows
+    causal kernel or its split or paired form otherwise; under the Fused form the rows
     outside full chunks of 8 take the Fused numerics on the decode kernels."""
     p = hsdpa.Plan(16, 8, 256, 40000)
     assert p.route(1, 32767)["main"] == "decode"
     assert p.route(4, 100)["main"] == "few_rows"
-    r = p.route(4096, 8192)
-    assert r["main"] == "causal" and r["launches"] == 1 and r["tail"] == "none"
+    r = p.route(4096, 8192)       # one round of row groups, the longest paired with the shortest
+    assert r["main"] == "causal_paired" and r["launches"] == 3 and r["tail"] == "none"
+    r = p.route(8192, 0)          # two rounds: the heaviest row groups first
+    assert r["main"] == "causal" and r["launches"] == 1
     r = p.route(256, 32768)
     assert r["main"] == "causal_split" and r["splits"] > 1 and r["launches"] == 3
     f = hsdpa.Plan(16, 8, 256, 40000, form="fused")
@@ -127,7 +129,7 @@ def test_route_names_the_kernels():
     assert (r["main_rows"], r["main_form"], r["tail_rows"], r["tail"], r["tail_form"]) == \
         (8, "chained", 5, "few_rows", "fused")
     r = f.route(4096 + 3, 8192)
-    assert (r["main"], r["tail"], r["tail_rows"], r["tail_form"]) == ("causal", "few_rows", 3, "fused")
+    assert (r["main"], r["tail"], r["tail_rows"], r["tail_form"]) == ("causal_paired", "few_rows", 3, "fused")
     # above head_dim 256 the Fused form falls back to Chained
     assert hsdpa.Plan(4, 2, 288, 100, form="fused").route(1, 10)["main_form"] == "chained"
     # a group size with no equal split into groups of at most 16 (17) takes padded

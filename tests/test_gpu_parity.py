@@ -33,6 +33,17 @@ SMALL = [
     ("decode_d256_n40001_chunked", 16, 2, 256, 1, 40000, "decode"),
     ("decode_d128_kv8_n9000_chunked", 64, 8, 128, 1, 8999, "decode"),
     ("decode_d128_g16_n20001_chunked", 64, 4, 128, 1, 20000, "decode"),   # two P column blocks
+    # one round of causal workgroups whose longest row groups are paired with
+    # the shortest (the heavy row group's last tiles walked by the light one's
+    # workgroup): odd row-group counts (a middle row group alone), partial last
+    # row groups, the other head dimensions
+    ("prefill_paired_d64_r2200_g1", 24, 24, 64, 2200, 0, "causal_paired"),
+    ("prefill_paired_d128_r3000", 16, 2, 128, 3000, 0, "causal_paired"),
+    ("prefill_paired_d256_r2200_p1000_odd", 16, 2, 256, 2200, 1000, "causal_paired"),
+    ("prefill_paired_d256_r4000_p300", 16, 2, 256, 4000, 300, "causal_paired"),
+    ("prefill_paired_d96_r2200_g1", 24, 24, 96, 2200, 0, "causal_paired"),
+    ("prefill_paired_d384_r2200_g1", 12, 12, 384, 2200, 0, "causal_paired"),
+    ("prefill_d64_r1000_g1_short_rows", 40, 40, 64, 1000, 0, "causal"),    # 32 tiles: too few to pair
     # short chunks after long caches: the causal kernel split over the keys
     ("prefill_split_d256_r64_p3000", 16, 2, 256, 64, 3000, "causal_split"),
     ("prefill_split_d256_r300_p9000", 16, 2, 256, 300, 9000, "causal_split"),
