@@ -52,20 +52,22 @@ MFMA_BF16_PEAK_TFS = 2500.0  # MI355X dense bf16 MFMA, TFLOP/s
 # Summary and commands: profiles/pmc_traffic_bench_configs.md
 TRAFFIC_BYTES = {
     "chained": {
-        "decode_1k": (2 * (563.4 + 596.3 + 67.2) + (34.0 + 64.5 + 4.0)) * 1024,
-        "decode_32k": (2 * (16467.7 + 17509.3 + 1090.5) + (2112.0 + 2056.0 + 8.0)) * 1024,
-        "prefill_512": (2 * 8603.6 + 4096.0) * 1024,
-        "prefill_4096_after_8192": (2 * 165007.9 + 36352.0) * 1024,
-        "decode_128k_outliers": (2 * (65622.8 + 69784.3 + 1090.5) + (8320.2 + 2568.0 + 8.0)) * 1024,
+        "decode_1k": (2 * (563.4 + 597.3 + 64.0) + (34.0 + 64.5 + 4.0)) * 1024,
+        "decode_32k": (2 * (16467.2 + 17514.8 + 1087.5) + (2112.0 + 2056.0 + 8.0)) * 1024,
+        "prefill_512": (2 * 8603.7 + 4096.0) * 1024,
+        "prefill_4096_after_8192": (2 * (72934.8 + 150274.6 + 31013.0) + (376.0 + 87262.9 + 15360.0)) * 1024,
+        "decode_128k_outliers": (2 * (65627.8 + 69775.6 + 1087.5) + (8320.1 + 2568.0 + 8.0)) * 1024,
     },
     "fused": {
-        "decode_1k": (2 * (569.8 + 623.0 + 75.5) + (36.0 + 65.0 + 4.0)) * 1024,
-        "decode_32k": (2 * (16485.5 + 17542.2 + 1130.6) + (2240.0 + 2064.0 + 8.0)) * 1024,
-        "decode_128k_outliers": (2 * (65639.3 + 72584.0 + 1130.6) + (8832.4 + 16912.0 + 8.0)) * 1024,
+        "decode_1k": (2 * (569.6 + 623.0 + 75.5) + (36.0 + 65.0 + 4.0)) * 1024,
+        "decode_32k": (2 * (16476.8 + 17537.6 + 1130.0) + (2240.0 + 2064.0 + 8.0)) * 1024,
+        "decode_128k_outliers": (2 * (65639.2 + 72587.3 + 1130.0) + (8832.3 + 16912.0 + 8.0)) * 1024,
     },
 }
+
 PREFILL_KERNELS = {"prefill_512": "prefill_kd (one workgroup per 32-row block; its keys split among 8 waves)",
-                   "prefill_4096_after_8192": "prefill_attn"}
+                   "prefill_4096_after_8192": "prefill_split_max + prefill_split_pv + prefill_split_combine "
+                                              "(row groups paired: the longest with the shortest)"}
 
 
 def log(*a):
