@@ -1487,7 +1487,10 @@ __global__ __launch_bounds__(64 * KS, 1) void prefill_kd(PrefillArgs a)
     constexpr int QS = D / 16 / KS;                             // Q chunks each wave loads
     constexpr int KT_U16 = kKeyTile * SK;                       // one wave's K tile
     constexpr int Q_U16 = (D / 16) * 64 * 8;                    // Q in the lanes' operand layout
-    constexpr int P_U16 = MT * 4 * 64 * 8;                      // [tile][half][hi, lo][lane] x 8 bf16
+    // the P operands of two rounds at a time (the round being multiplied and
+    // the one being posted): [tile % PR][half][hi, lo][lane] x 8 bf16
+    constexpr int PR = MT < 2 * KS ? MT : 2 * KS;
+    constexpr int P_U16 = PR * 4 * 64 * 8;
     constexpr int VS_U16 = 2 * kKeyTile * SVS;                  // one wave's two V slices
     constexpr int PASS1 = KS * KT_U16 + Q_U16, PASS2 = P_U16 + KS * VS_U16;
     __shared__ __attribute__((aligned(16))) uint16_t lds[PASS1 > PASS2 ? PASS1 : PASS2];
@@ -1549,17 +1552,26 @@ __global__ __launch_bounds__(64 * KS, 1) void prefill_kd(PrefillArgs a)
             tile_lstore_padded<D, 64>(kt, SK, l, kr);
             wave_sync();
             if (i + 1 < TPW) tile_gload<D, 64, false>(kg, t0 + KS * kKeyTile, nblk, l, kr);
-            u32x4 ka[D / 16];
-#pragma unroll
-            for (int sq = 0; sq < D / 16; sq++) ka[sq] = load16(kt + arow + 16 * sq);
-            __builtin_amdgcn_sched_barrier(0);
+            // the tile's K operands read before its MFMAs: all at once into two
+            // accumulation chains, or, where more than 16 tiles' scores are
+            // kept, in two halves into one chain (registers)
+            constexpr bool WIDE = MT > 16;
+            constexpr int KA = WIDE ? D / 32 : D / 16;
             f32x16 acc0 = {}, acc1 = {};
 #pragma unroll
-            for (int sq = 0; sq < D / 16; sq += 2) {
-                acc0 = mfma(ka[sq], qb[sq], acc0);
-                acc1 = mfma(ka[sq + 1], qb[sq + 1], acc1);
+            for (int s0 = 0; s0 < D / 16; s0 += KA) {
+                u32x4 ka[KA];
+#pragma unroll
+                for (int sq = 0; sq < KA; sq++) ka[sq] = load16(kt + arow + 16 * (s0 + sq));
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int sq = 0; sq < KA; sq += 2) {
+                    acc0 = mfma(ka[sq], qb[s0 + sq], acc0);
+                    if constexpr (WIDE) acc0 = mfma(ka[sq + 1], qb[s0 + sq + 1], acc0);
+                    else acc1 = mfma(ka[sq + 1], qb[s0 + sq + 1], acc1);
+                }
             }
-            const f32x16 acc = acc0 + acc1;
+            const f32x16 acc = WIDE ? acc0 : acc0 + acc1;
             sc[i] = acc;
             const bool full = t < nfull;
             const int vis = static_cast<int>(static_cast<int64_t>(lim) - static_cast<int64_t>(t0));
@@ -1612,8 +1624,8 @@ __global__ __launch_bounds__(64 * KS, 1) void prefill_kd(PrefillArgs a)
         const int t = wave + KS * r;
         u32x4 hi, lo;
         split_pack_hw(ev + 8 * h, hi, lo);
-        store16(pbuf + ((t * 2 + h) * 2 + 0) * 512 + 8 * l, hi);
-        store16(pbuf + ((t * 2 + h) * 2 + 1) * 512 + 8 * l, lo);
+        store16(pbuf + (((t % PR) * 2 + h) * 2 + 0) * 512 + 8 * l, hi);
+        store16(pbuf + (((t % PR) * 2 + h) * 2 + 1) * 512 + 8 * l, lo);
     };
     auto exps_q = [&](int r, int q) {
 #pragma unroll
@@ -1623,7 +1635,7 @@ __global__ __launch_bounds__(64 * KS, 1) void prefill_kd(PrefillArgs a)
     u32x4 p[4], av[2][DPW];
     auto read_p = [&](int t) {
 #pragma unroll
-        for (int j = 0; j < 4; j++) p[j] = load16(pbuf + (t * 4 + j) * 512 + 8 * l);
+        for (int j = 0; j < 4; j++) p[j] = load16(pbuf + ((t % PR) * 4 + j) * 512 + 8 * l);
     };
     // tile t's V slice (vq[t % VPF]) to its staging rows, its V^T operands
     // read back, the slice VPF tiles on requested in its registers

@@ -212,9 +212,8 @@ hipError_t launch_decode_fused(const DecodeArgs &a, int head_dim, int kv_heads, 
 // spread the keys over more workgroups).
 constexpr int kShortWaves = 4;
 constexpr int kShortMaxTiles = 32;
-// up to this many key tiles per row block at head dimensions 128 and 256, O is
-// accumulated by dimensions (prefill_kd); beyond, and at 64, by keys (prefill_ks)
-constexpr int kShortKdTiles = 16;
+// at head dimensions 128 and 256 O is accumulated by dimensions (prefill_kd), at
+// 64 by keys (prefill_ks)
 inline bool prefill_short_ok(int d) { return d == 64 || d == 128 || d == 256; }
 hipError_t launch_prefill_short(const PrefillArgs &a, int head_dim, int heads, hipStream_t s);
 // the current device's copy of the static scratch of hsdpa_attention_static

@@ -19,26 +19,32 @@ template <int D, bool POW2>
 static hipError_t prefill_short_dp(const PrefillArgs &a, int heads, hipStream_t s)
 {
     const uint64_t ntiles = (a.past + a.rows + kKeyTile - 1) / kKeyTile;
-    // up to kShortKdTiles tiles at D = 128 and 256: O by dimensions, no partial
-    // outputs between the waves, every workgroup running the launch's tile
-    // count rounded up to 8, 12 or 16 (a chunk reaches this kernel only with
-    // more than 4 tiles: the split it replaces takes at least 4 per split);
-    // beyond (their exponentials no longer fit the LDS), and at D = 64: O by
-    // keys. At D = 256 the row block's keys go to 8 waves, two per SIMD (one
-    // or two tiles each, 32 dimensions of O), in rounds of 8 tiles: 512 rows
-    // with no cache 20.5 -> 16.7 us, 481 after 30 23.0 -> 16.7, 100 after 220
-    // 18.5 -> 14.8 against 4 waves.
-    if constexpr (D == 256) {
-        if (ntiles <= 8) return prefill_kd_mt<D, 8, POW2, 8>(a, heads, s);
-        if (ntiles <= 16) return prefill_kd_mt<D, 16, POW2, 8>(a, heads, s);
+    // D = 128 and 256: O by dimensions, no partial outputs between the waves,
+    // every workgroup running the launch's tile count rounded up to 8, 12, 16,
+    // 24 or 32 (a chunk reaches this kernel only with more than 4 tiles: the
+    // split it replaces takes at least 4 per split; the host sends none with
+    // more than kShortMaxTiles). The P operands of two rounds at a time in the
+    // LDS, so the tile count is bounded by the scores kept in registers: 512
+    // rows after 512 39.5 -> 29.3 us, 256 after 768 38.0 -> 26.7, 1024 rows
+    // with no cache 72.8 -> 55.0 against O by keys (prefill_ks) at D = 256.
+    // At D = 256 the row block's keys go to 8 waves, two per SIMD (one to four
+    // tiles each, 32 dimensions of O), in rounds of 8 tiles: 512 rows with no
+    // cache 20.5 -> 16.7 us, 481 after 30 23.0 -> 16.7, 100 after 220 18.5 ->
+    // 14.8 against 4 waves. D = 64: O by keys.
+    if constexpr (D == 64) {
+        const dim3 grid(static_cast<unsigned>((a.rows + 31) / 32), static_cast<unsigned>(heads));
+        return launch(prefill_ks<D, kShortWaves, kShortMaxTiles / kShortWaves, POW2>, grid, dim3(64 * kShortWaves),
+                      s, a);
+    } else {
+        constexpr int KS = D == 256 ? 8 : kShortWaves;
+        if (ntiles <= 8) return prefill_kd_mt<D, 8, POW2, KS>(a, heads, s);
+        if constexpr (D == 128)
+            if (ntiles <= 12) return prefill_kd_mt<D, 12, POW2, KS>(a, heads, s);
+        if (ntiles <= 16) return prefill_kd_mt<D, 16, POW2, KS>(a, heads, s);
+        if (ntiles <= 24) return prefill_kd_mt<D, 24, POW2, KS>(a, heads, s);
+        if (ntiles <= static_cast<uint64_t>(kShortMaxTiles)) return prefill_kd_mt<D, 32, POW2, KS>(a, heads, s);
+        return hipErrorInvalidValue;
     }
-    if constexpr (D == 128) {
-        if (ntiles <= 8) return prefill_kd_mt<D, 8, POW2>(a, heads, s);
-        if (ntiles <= 12) return prefill_kd_mt<D, 12, POW2>(a, heads, s);
-        if (ntiles <= static_cast<uint64_t>(kShortKdTiles)) return prefill_kd_mt<D, kShortKdTiles, POW2>(a, heads, s);
-    }
-    const dim3 grid(static_cast<unsigned>((a.rows + 31) / 32), static_cast<unsigned>(heads));
-    return launch(prefill_ks<D, kShortWaves, kShortMaxTiles / kShortWaves, POW2>, grid, dim3(64 * kShortWaves), s, a);
 }
 
 template <int D>

@@ -60,12 +60,16 @@ SMALL = [
     ("prefill_short_d256_r7_p257_g40", 80, 2, 256, 7, 257, "causal_short"),       # one partial row block
     ("prefill_short_d64_r500_p0", 8, 2, 64, 500, 0, "causal_short"),
     ("prefill_short_d256_r33_p0", 16, 2, 256, 33, 0, "causal"),                   # fills no split: one-workgroup kernel
-    # up to 16 key tiles at D 128 and 256 the waves split the dimensions for
-    # P.V, every workgroup running the launch's tile count in rounds of 4
+    # at D 128 and 256 the waves split the dimensions for P.V, every workgroup
+    # running the launch's tile count in rounds of 4 (D 128) or 8 (D 256)
     ("prefill_short_d128_r200_p50_g4_8_tiles", 16, 4, 128, 200, 50, "causal_short"),
     ("prefill_short_d256_r150_p90_8_tiles", 16, 2, 256, 150, 90, "causal_short"),
     ("prefill_short_d128_r300_p60_12_tiles", 16, 2, 128, 300, 60, "causal_short"),
     ("prefill_short_d256_r481_p30_16_tiles_partial_block", 16, 2, 256, 481, 30, "causal_short"),
+    # beyond 16 tiles the P operands of two rounds at a time: 24 and 32 tiles
+    ("prefill_short_d256_r256_p500_24_tiles", 16, 2, 256, 256, 500, "causal_short"),
+    ("prefill_short_d128_r300_p400_g4_24_tiles", 16, 4, 128, 300, 400, "causal_short"),
+    ("prefill_short_d128_r512_p400_32_tiles", 16, 2, 128, 512, 400, "causal_short"),
 ]
 
 
