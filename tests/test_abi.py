@@ -119,6 +119,13 @@ def test_route_names_the_kernels():
     assert r["main"] == "causal_paired" and r["launches"] == 3 and r["tail"] == "none"
     r = p.route(8192, 0)          # two rounds: the heaviest row groups first
     assert r["main"] == "causal" and r["launches"] == 1
+    # pairing needs one round of row groups whose longest sees at least 64 key
+    # tiles and gains at least an eighth
+    assert hsdpa.Plan(16, 8, 256, 4096).route(4096, 0)["main"] == "causal_paired"   # 1..128 tiles
+    assert hsdpa.Plan(16, 8, 256, 3000).route(3000, 0)["main"] == "causal_paired"   # 94 row groups
+    assert hsdpa.Plan(40, 1, 64, 1000).route(1000, 0)["main"] == "causal"           # 32 tiles at most
+    assert hsdpa.Plan(64, 8, 256, 5120).route(1024, 4096)["main"] == "causal"       # 129..160: < 1/8
+    assert hsdpa.Plan(32, 8, 256, 4096).route(4096, 0)["main"] == "causal"          # 512 row groups
     r = p.route(256, 32768)
     assert r["main"] == "causal_split" and r["splits"] > 1 and r["launches"] == 3
     f = hsdpa.Plan(16, 8, 256, 40000, form="fused")
