@@ -786,8 +786,10 @@ __global__ __launch_bounds__(64 * W, D > 256 ? 1 : 8 / W) void decode_pv(DecodeA
         //    operand read is issued before the first MFMA: reading each just
         //    before its MFMA waits out the LDS latency once per MFMA. With
         //    LOOP the next chunk's V registers are live here, so the operands
-        //    come in two halves of the tiles.
-        constexpr int PH = LOOP && TPP % 2 == 0 ? 2 : 1, TPH = TPP / PH;
+        //    come in two halves of the tiles, in quarters at D = 256 (the
+        //    halves spilled 29 registers under the Fused form: 128K keys on
+        //    16/2 heads 77.5 -> 71.2 us Fused, 48K 30.0 -> 29.2 us Chained).
+        constexpr int PH = LOOP && D == 256 && TPP % 4 == 0 ? 4 : LOOP && TPP % 2 == 0 ? 2 : 1, TPH = TPP / PH;
 #pragma unroll
         for (int ph = 0; ph < PH; ph++) {
             u32x4 bp[TPH][NCB], av[TPH][DBW];
