@@ -52,16 +52,16 @@ MFMA_BF16_PEAK_TFS = 2500.0  # MI355X dense bf16 MFMA, TFLOP/s
 # Summary and commands: profiles/pmc_traffic_bench_configs.md
 TRAFFIC_BYTES = {
     "chained": {
-        "decode_1k": (2 * (563.4 + 597.3 + 64.0) + (34.0 + 64.5 + 4.0)) * 1024,
-        "decode_32k": (2 * (16467.2 + 17514.8 + 1087.5) + (2112.0 + 2056.0 + 8.0)) * 1024,
-        "prefill_512": (2 * 8603.7 + 4096.0) * 1024,
-        "prefill_4096_after_8192": (2 * (72934.8 + 150274.6 + 31013.0) + (376.0 + 87262.9 + 15360.0)) * 1024,
-        "decode_128k_outliers": (2 * (65627.8 + 69775.6 + 1087.5) + (8320.1 + 2568.0 + 8.0)) * 1024,
+        "decode_1k": (2 * (563.2 + 597.1 + 64.0) + (34.0 + 64.5 + 4.0)) * 1024,
+        "decode_32k": (2 * (16467.1 + 17514.8 + 1087.5) + (2112.0 + 2056.0 + 8.0)) * 1024,
+        "prefill_512": (2 * 8605.7 + 4096.0) * 1024,
+        "prefill_4096_after_8192": (2 * (72935.2 + 148967.7 + 31013.3) + (376.0 + 87272.0 + 15360.0)) * 1024,
+        "decode_128k_outliers": (2 * (65628.0 + 69775.4 + 1087.5) + (8320.2 + 2056.0 + 8.0)) * 1024,
     },
     "fused": {
-        "decode_1k": (2 * (569.6 + 623.0 + 75.5) + (36.0 + 65.0 + 4.0)) * 1024,
-        "decode_32k": (2 * (16476.8 + 17537.6 + 1130.0) + (2240.0 + 2064.0 + 8.0)) * 1024,
-        "decode_128k_outliers": (2 * (65639.2 + 72587.3 + 1130.0) + (8832.3 + 16912.0 + 8.0)) * 1024,
+        "decode_1k": (2 * (569.6 + 623.0 + 71.0) + (36.0 + 65.0 + 4.0)) * 1024,
+        "decode_32k": (2 * (16476.8 + 17537.5 + 1130.5) + (2240.0 + 2064.0 + 8.0)) * 1024,
+        "decode_128k_outliers": (2 * (65639.3 + 69805.8 + 1130.5) + (8832.4 + 5648.0 + 8.0)) * 1024,
     },
 }
 
