@@ -145,6 +145,36 @@ def test_configs_full(torch_cuda, name):
     print(name, r, flush=True)
 
 
+# Both forms of the score scaling on every kernel family at D 256 (whose
+# default 1/16 is a power of two, folded into the exponential's constants): a
+# general scale, and a power of two other than the default.
+SCALED = [
+    # name, heads, kv_heads, head_dim, rows, past, the kernels the call must take
+    ("decode_32k", 16, 2, 256, 1, 32767, "decode"),
+    ("few_r4", 16, 2, 256, 4, 3000, "few_rows"),
+    ("short_16_tiles", 16, 4, 256, 512, 0, "causal_short"),
+    ("short_24_tiles", 16, 2, 256, 256, 500, "causal_short"),
+    ("short_32_tiles", 16, 2, 256, 1024, 0, "causal_short"),
+    ("split", 16, 2, 256, 256, 4000, "causal_split"),
+    ("paired", 16, 2, 256, 2200, 1000, "causal_paired"),
+    ("causal", 16, 2, 256, 19, 37, "causal"),
+]
+
+
+@pytest.mark.parametrize("scale", [0.0731, 0.125])
+@pytest.mark.parametrize("case", SCALED, ids=[c[0] for c in SCALED])
+def test_scales(torch_cuda, case, scale):
+    name, h, kvh, d, rows, past, kernels = case
+    w = W.make(name, heads=h, kv_heads=kvh, head_dim=d, rows=rows, past=past, seed=23, scale=scale)
+    plan = hsdpa.Plan(w.heads, w.gqa, w.head_dim, w.capacity)
+    assert plan.route(rows, past)["main"] == kernels, plan.route(rows, past)
+    print(f"case {name} scale {scale}", flush=True)
+    out = run_hsdpa(w, plan)
+    ref = oracle.attention(w)
+    r = assert_parity(out, ref, w, f"{name} scale {scale}")
+    print(name, scale, r, flush=True)
+
+
 GROUPS = [
     # more than 16 query heads per KV head: the decode kernels take them in 2, 3
     # or 4 equal groups; a group size with no such split (17), or more than 64
