@@ -90,3 +90,51 @@ def test_graph_replays_with_work_between(torch_cuda):
         hsdpa.attention_torch(plan, *bo[:3], bo[3], other.rows, other.past, other.scale, ws, st)
         torch.cuda.synchronize()
         assert torch.equal(bo[3].cpu(), want_o), f"after replay {replay}: eager call"
+
+
+def test_graph_replays_prefill_forms(torch_cuda):
+    """The prefill forms that launch several kernels or keep state in their
+    workspace, captured in one graph on one workspace: the paired form (maxima,
+    P.V, combine), the split form, and a short chunk of 29 key tiles (its P
+    operands two rounds at a time). Each replay, with an eager call on the
+    same workspace in between, equals the calls run alone."""
+    torch = torch_cuda
+    cap = 3000
+    ws_ = [W.make("graph_paired", heads=16, kv_heads=2, head_dim=128, rows=3000, past=0, capacity=cap, seed=41),
+           W.make("graph_split", heads=16, kv_heads=2, head_dim=128, rows=64, past=2000, capacity=cap, seed=42),
+           W.make("graph_short", heads=16, kv_heads=2, head_dim=128, rows=512, past=400, capacity=cap, seed=43)]
+    plan = hsdpa.Plan(16, 8, 128, cap)
+    assert [plan.route(w.rows, w.past)["main"] for w in ws_] == ["causal_paired", "causal_split", "causal_short"]
+    want = [alone(torch, plan, w) for w in ws_]
+    bufs = [dev_tensors(torch, w) for w in ws_]
+    ws = torch.empty(plan.workspace_bytes, dtype=torch.uint8, device="cuda")
+    st = torch.cuda.Stream()
+    st.wait_stream(torch.cuda.current_stream())
+
+    def step():
+        for w, b in zip(ws_, bufs):
+            hsdpa.attention_torch(plan, *b[:3], b[3], w.rows, w.past, w.scale, ws, st)
+
+    with torch.cuda.stream(st):
+        step()                                      # warm-up outside the capture
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=st):
+        step()
+    torch.cuda.synchronize()
+    for replay in range(3):
+        for b in bufs:
+            b[3].fill_(-1)
+        torch.cuda.synchronize()
+        with torch.cuda.stream(st):
+            graph.replay()
+        torch.cuda.synchronize()
+        for w, b, x in zip(ws_, bufs, want):
+            assert torch.equal(b[3].cpu(), x), f"replay {replay}: {w.name}"
+        # the paired call again, eagerly, on the same workspace
+        b = bufs[0]
+        b[3].fill_(-1)
+        st.wait_stream(torch.cuda.current_stream())
+        hsdpa.attention_torch(plan, *b[:3], b[3], ws_[0].rows, ws_[0].past, ws_[0].scale, ws, st)
+        torch.cuda.synchronize()
+        assert torch.equal(b[3].cpu(), want[0]), f"after replay {replay}: eager paired call"
