@@ -276,7 +276,7 @@ namespace {
 // How the decode passes cover a call: `sub` groups of `g` columns per KV
 // head, keys per workgroup and workgroups per group of each pass.
 struct DecodeCfg {
-    int sub, g, keys_qk, keys_pv, nwg_qk, nwg_pv, xcd;
+    int sub, g, keys_qk, keys_pv, nwg_qk, nwg_pv, xcd, qk_all;
 };
 
 // Whether `rows` rows run on the decode kernels: one row whose g query heads
@@ -296,7 +296,7 @@ int decode_sub(const hsdpa_plan *p, uint64_t rows)
 
 // The decode passes' grids for `rows` rows over n visible keys (decode_sub
 // already > 0).
-DecodeCfg decode_cfg(const hsdpa_plan *p, uint64_t rows, uint64_t n, int sub)
+DecodeCfg decode_cfg(const hsdpa_plan *p, uint64_t rows, uint64_t n, int sub, bool fused)
 {
     DecodeCfg c{};
     const int d = static_cast<int>(p->spec.head_dim);
@@ -304,6 +304,16 @@ DecodeCfg decode_cfg(const hsdpa_plan *p, uint64_t rows, uint64_t n, int sub)
     c.sub = sub;
     c.g = hsdpa::decode_group_cols(static_cast<int>(cols), sub);
     const uint64_t groups = p->kv_heads * static_cast<uint64_t>(sub);
+    const uint64_t nqk1 = (n + hsdpa::kDecodeKeysQK - 1) / hsdpa::kDecodeKeysQK;
+    const uint64_t cu1 = static_cast<uint64_t>(p->cus);
+    // pass 1 of the Chained form on the tuned head dimensions may score all of
+    // a KV head's groups in each workgroup: its grid then has kv_heads rows of
+    // workgroups, not one per group, and two tiles per wave at least (below)
+    c.qk_all = !fused && hsdpa::decode_rows_ok(d) && hsdpa::decode_loop_ok(d) &&
+                       hsdpa::decode_qk_groups(sub, p->kv_heads * nqk1, cu1)
+                   ? 1
+                   : 0;
+    const uint64_t groups_qk = c.qk_all ? p->kv_heads : groups;
     // pass 1: a tile per wave, or several in turn (the next one in flight)
     // once one tile per wave would need more than one workgroup per compute
     // unit: at least two, and as many as one round of two workgroups per
@@ -315,14 +325,12 @@ DecodeCfg decode_cfg(const hsdpa_plan *p, uint64_t rows, uint64_t n, int sub)
     // looped kernel runs one workgroup per CU at a time; the smaller count on
     // a tie): a partial last round costs a whole one (40K keys: 3 tiles in
     // one round, 27.8 us, against 2 tiles in two rounds, 29.2 us).
-    const uint64_t nqk1 = (n + hsdpa::kDecodeKeysQK - 1) / hsdpa::kDecodeKeysQK;
-    const uint64_t cu1 = static_cast<uint64_t>(p->cus);
-    const uint64_t rounds = (groups * nqk1 + 2 * cu1 - 1) / (2 * cu1);
-    uint64_t rq = !hsdpa::decode_loop_ok(d) ? 1 : groups * nqk1 > cu1 && rounds < 2 ? 2 : rounds;
+    const uint64_t rounds = (groups_qk * nqk1 + 2 * cu1 - 1) / (2 * cu1);
+    uint64_t rq = !hsdpa::decode_loop_ok(d) ? 1 : groups_qk * nqk1 > cu1 && rounds < 2 ? 2 : rounds;
     if (rq > 1) {
         uint64_t best = rq, cost = ~0ull;
         for (uint64_t r = rq; r <= 2 * rq; r++) {
-            const uint64_t wgs = groups * ((nqk1 + r - 1) / r);
+            const uint64_t wgs = groups_qk * ((nqk1 + r - 1) / r);
             const uint64_t cc = (wgs + cu1 - 1) / cu1 * r;
             if (cc < cost) {
                 cost = cc;
@@ -499,7 +507,7 @@ static hsdpa_status run_part(const hsdpa_plan *plan, const hsdpa_call *call, con
     const uint16_t *gp = gate ? gate + part.row0 * gate_row : nullptr;
     const int sub = decode_sub(plan, rows);
     if (sub > 0) {
-        const DecodeCfg c = decode_cfg(plan, rows, n, sub);
+        const DecodeCfg c = decode_cfg(plan, rows, n, sub, part.fused);
         if (kernels) *kernels = rows == 1 ? HSDPA_KERNELS_DECODE : HSDPA_KERNELS_FEW_ROWS;
         if (splits) *splits = 1;
         if (launches) *launches += 3;
@@ -534,6 +542,7 @@ static hsdpa_status run_part(const hsdpa_plan *plan, const hsdpa_call *call, con
         a.nwg_qk = c.nwg_qk;
         a.nwg_pv = c.nwg_pv;
         a.xcd = c.xcd;
+        a.qk_all = c.qk_all;
         a.scale = call->scale;
         a.gate = gp;
         const hipError_t e = part.fused ? hsdpa::launch_decode_fused(a, d, static_cast<int>(plan->kv_heads), st)

@@ -388,19 +388,28 @@ template <int MR> struct DecodeIds {
 // FUSED: also store the maximum of every 16-key block of each column (bmax):
 // the Fused form evaluates a block's exponentials at the running maximum of
 // the blocks up to it. TWO (with LOOP): exactly two tiles per wave.
-template <int D, bool LOOP, int MR = 0, bool FUSED = false, bool TWO = false>
+template <int D, bool LOOP, int MR = 0, bool FUSED = false, bool TWO = false, bool MG = false>
 __global__ __launch_bounds__(256) void decode_qk(DecodeArgs a)
 {
     constexpr int KS = D / 32;
     constexpr int C = D / 8, KM = swz_group<D>() - 1;          // chunks per row, swizzle mask
+    // MG: every group of the KV head in this workgroup (at most kDecodeMaxSub),
+    // its Q columns staged in LDS in the lanes' operand layout, so that each K
+    // tile is loaded and staged once for all of them (several rows after a
+    // cache, or more than 16 query heads per KV head)
+    constexpr int NG = MG ? kDecodeMaxSub : 1;
+    static_assert(!(MG && FUSED), "the Fused form scores one group per workgroup");
     __shared__ __attribute__((aligned(16))) uint16_t kt[4][kKeyTile * D];
-    __shared__ float red[4][16];
+    __shared__ __attribute__((aligned(16))) u32x4 qs[MG ? kDecodeMaxSub * KS * 64 : 1];
+    __shared__ float red[NG][4][16];
     // blockIdx.y: the KV head; id.z: which of its a.sub groups of g columns
     // (one unless a KV head has more than 16)
-    const DecodeIds<MR> id(a);
-    if (MR == 2 && id.wg >= a.nwg_qk) return;              // grid padding
-    const int kvh = MR == 2 ? static_cast<int>(blockIdx.y) * a.sub + id.z
-                            : static_cast<int>(blockIdx.y * gridDim.z + blockIdx.z);
+    const DecodeIds<MG ? 1 : MR> id(a);
+    if (!MG && MR == 2 && id.wg >= a.nwg_qk) return;       // grid padding
+    const int ng = MG ? a.sub : 1;
+    const int kvh0 = MG ? static_cast<int>(blockIdx.y) * a.sub
+                        : MR == 2 ? static_cast<int>(blockIdx.y) * a.sub + id.z
+                                  : static_cast<int>(blockIdx.y * gridDim.z + blockIdx.z);
     const int wg = id.wg;
     const int wave = threadIdx.x >> 6, l = threadIdx.x & 63, i = l & 15, G = l >> 4;
     const uint64_t j0 = static_cast<uint64_t>(wg) * a.keys_qk;
@@ -408,25 +417,42 @@ __global__ __launch_bounds__(256) void decode_qk(DecodeArgs a)
     const bool colv = i < a.g;
     // Rows past the visible keys (loaded from row 0) and columns past g are
     // computed and discarded: an MFMA output element depends only on its own
-    // A row and B column.
-    const uint16_t *qp;
-    uint64_t lim = a.n;                 // keys below lim are visible to this lane's column
-    if constexpr (MR) {
-        // a padded column (past rows * G) computes column 0's scores, never stored
-        const int cg = id.z * a.g + (colv ? i : 0), c = cg < a.cols ? cg : 0, row = c / a.G;
-        qp = a.q + static_cast<uint64_t>(row) * a.q_row +
-             static_cast<uint64_t>(static_cast<int>(blockIdx.y) * a.G + c - row * a.G) * a.q_head + 8 * G;
-        lim = a.past + static_cast<uint64_t>(row) + 1;
-    } else {
-        qp = a.q + static_cast<uint64_t>(kvh * a.g + (colv ? i : 0)) * a.q_head + 8 * G;
-    }
+    // A row and B column. Column i of group z: its Q row and the keys visible
+    // to it (keys below lim).
+    auto qsrc = [&](int z, uint64_t &lim) {
+        lim = a.n;
+        if constexpr (MR) {
+            // a padded column (past rows * G) computes column 0's scores, never stored
+            const int cg = z * a.g + (colv ? i : 0), c = cg < a.cols ? cg : 0, row = c / a.G;
+            lim = a.past + static_cast<uint64_t>(row) + 1;
+            return a.q + static_cast<uint64_t>(row) * a.q_row +
+                   static_cast<uint64_t>(static_cast<int>(blockIdx.y) * a.G + c - row * a.G) * a.q_head + 8 * G;
+        } else {
+            return a.q + static_cast<uint64_t>((MG ? kvh0 + z : kvh0) * a.g + (colv ? i : 0)) * a.q_head + 8 * G;
+        }
+    };
     u32x4 qb[KS];
+    uint64_t lim1 = a.n;
+    if constexpr (MG) {
+        for (int z = wave; z < ng; z += 4) {
+            uint64_t lz;
+            const uint16_t *qp = qsrc(z, lz);
 #pragma unroll
-    for (int s = 0; s < KS; s++) qb[s] = load16(qp + 32 * s);
+            for (int s = 0; s < KS; s++) qs[(z * KS + s) * 64 + l] = load16(qp + 32 * s);
+        }
+        __syncthreads();
+    } else {
+        const uint16_t *qp = MR ? qsrc(id.z, lim1) : qsrc(0, lim1);
+#pragma unroll
+        for (int s = 0; s < KS; s++) qb[s] = load16(qp + 32 * s);
+    }
     const uint16_t *kbase = a.k + static_cast<uint64_t>(blockIdx.y) * a.kv_stride;
     uint16_t *my = kt[wave];
-    float m = kNegInf;
-    // One 32-key tile of the wave: staged through its LDS rows, scored, stored.
+    float m[NG];
+#pragma unroll
+    for (int z = 0; z < NG; z++) m[z] = kNegInf;
+    // One 32-key tile of the wave: staged through its LDS rows, scored for
+    // each group, stored.
     auto tile = [&](uint64_t t0, const u32x4 (&kr)[Tile<D, 64>::kPer]) {
 #pragma unroll
         for (int c0 = 0; c0 < Tile<D, 64>::kPer; c0++) {
@@ -446,52 +472,67 @@ __global__ __launch_bounds__(256) void decode_qk(DecodeArgs a)
                 const int row = 16 * b + i;
                 ka[b][s] = load16(my + row * D + 8 * ((4 * s + G) ^ (row & KM)));
             }
-        f32x4 acc[2] = {};
 #pragma unroll
-        for (int s = 0; s < KS; s++)
-#pragma unroll
-            for (int b = 0; b < 2; b++) acc[b] = mfma16(ka[b][s], qb[s], acc[b]);
-        if (colv && t0 < j1) {
-            float *sp = a.scores + static_cast<uint64_t>(kvh * a.g + i) * a.npad + t0 + 4 * G;
-#pragma unroll
-            for (int b = 0; b < 2; b++) {
-                float4 v4;
-                float *v = reinterpret_cast<float *>(&v4);
-#pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    const uint64_t key = t0 + 16 * b + 4 * G + r;
-                    const bool valid = key < j1 && (!MR || key < lim);
-                    const float s = acc[b][r] * a.scale;
-                    v[r] = valid ? s : kNegInf;
-                    if (valid) m = s > m ? s : m;
+        for (int z = 0; z < NG; z++) {
+            if (z >= ng) break;
+            const int kvh = MG ? kvh0 + z : kvh0;
+            uint64_t lim = lim1;
+            if constexpr (MG) {
+                if constexpr (MR) {
+                    const int cg = z * a.g + (colv ? i : 0), c = cg < a.cols ? cg : 0;
+                    lim = a.past + static_cast<uint64_t>(c / a.G) + 1;
                 }
-                *reinterpret_cast<float4 *>(sp + 16 * b) = v4;
+#pragma unroll
+                for (int s = 0; s < KS; s++) qb[s] = qs[(z * KS + s) * 64 + l];
             }
-        }
-        if constexpr (FUSED) {
-            // block b of the tile: keys t0 + 16 b + 4 G + r over the four lane
-            // groups G of column i (the same scaled values as stored above)
+            f32x4 acc[2] = {};
 #pragma unroll
-            for (int b = 0; b < 2; b++) {
-                float bm = kNegInf;
+            for (int s = 0; s < KS; s++)
 #pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    const uint64_t key = t0 + 16 * b + 4 * G + r;
-                    const float s = acc[b][r] * a.scale;
-                    if (key < j1 && (!MR || key < lim)) bm = s > bm ? s : bm;
+                for (int b = 0; b < 2; b++) acc[b] = mfma16(ka[b][s], qb[s], acc[b]);
+            if (colv && t0 < j1) {
+                float *sp = a.scores + static_cast<uint64_t>(kvh * a.g + i) * a.npad + t0 + 4 * G;
+#pragma unroll
+                for (int b = 0; b < 2; b++) {
+                    float4 v4;
+                    float *v = reinterpret_cast<float *>(&v4);
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        const uint64_t key = t0 + 16 * b + 4 * G + r;
+                        const bool valid = key < j1 && (!MR || key < lim);
+                        const float s = acc[b][r] * a.scale;
+                        v[r] = valid ? s : kNegInf;
+                        if (valid) m[z] = s > m[z] ? s : m[z];
+                    }
+                    *reinterpret_cast<float4 *>(sp + 16 * b) = v4;
                 }
-                const float o16 = __shfl_xor(bm, 16);
-                bm = o16 > bm ? o16 : bm;
-                const float o32 = __shfl_xor(bm, 32);
-                bm = o32 > bm ? o32 : bm;
-                if (colv && G == 0 && t0 + 16 * b < j1)
-                    a.bmax[static_cast<uint64_t>(kvh * a.g + i) * a.nblk + (t0 + 16 * b) / 16] = bm;
+            }
+            if constexpr (FUSED) {
+                // block b of the tile: keys t0 + 16 b + 4 G + r over the four lane
+                // groups G of column i (the same scaled values as stored above)
+#pragma unroll
+                for (int b = 0; b < 2; b++) {
+                    float bm = kNegInf;
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        const uint64_t key = t0 + 16 * b + 4 * G + r;
+                        const float s = acc[b][r] * a.scale;
+                        if (key < j1 && (!MR || key < lim)) bm = s > bm ? s : bm;
+                    }
+                    const float o16 = __shfl_xor(bm, 16);
+                    bm = o16 > bm ? o16 : bm;
+                    const float o32 = __shfl_xor(bm, 32);
+                    bm = o32 > bm ? o32 : bm;
+                    if (colv && G == 0 && t0 + 16 * b < j1)
+                        a.bmax[static_cast<uint64_t>(kvh * a.g + i) * a.nblk + (t0 + 16 * b) / 16] = bm;
+                }
             }
         }
     };
+    constexpr bool NT = MG || MR != 2;     // streams no other workgroup rereads
     if constexpr (!LOOP) {
         u32x4 kr[Tile<D, 64>::kPer];
-        tile_gload<D, 64, MR != 2>(kbase, j0 + kKeyTile * wave, j1, l, kr);
+        tile_gload<D, 64, NT>(kbase, j0 + kKeyTile * wave, j1, l, kr);
         // Every load is in flight before the first use waits on one: left to
         // itself the scheduler interleaves them and keeps only a few outstanding.
         __builtin_amdgcn_sched_barrier(0);
@@ -504,8 +545,8 @@ __global__ __launch_bounds__(256) void decode_qk(DecodeArgs a)
         // runs faster with one tile in flight (two: 0.8 us slower at 64K and
         // 128K)
         u32x4 kr0[Tile<D, 64>::kPer], kr1[Tile<D, 64>::kPer];
-        tile_gload<D, 64, MR != 2>(kbase, j0 + kKeyTile * wave, j1, l, kr0);
-        tile_gload<D, 64, MR != 2>(kbase, j0 + 4 * kKeyTile + kKeyTile * wave, j1, l, kr1);
+        tile_gload<D, 64, NT>(kbase, j0 + kKeyTile * wave, j1, l, kr0);
+        tile_gload<D, 64, NT>(kbase, j0 + 4 * kKeyTile + kKeyTile * wave, j1, l, kr1);
         __builtin_amdgcn_sched_barrier(0);
         tile(j0 + kKeyTile * wave, kr0);
         __builtin_amdgcn_sched_barrier(0);
@@ -516,30 +557,36 @@ __global__ __launch_bounds__(256) void decode_qk(DecodeArgs a)
         // falls past j1 and reads row 0 (clamped, unused)
         const int rounds = a.keys_qk / (4 * kKeyTile);
         u32x4 kr0[Tile<D, 64>::kPer], kr1[Tile<D, 64>::kPer];
-        tile_gload<D, 64, MR != 2>(kbase, j0 + kKeyTile * wave, j1, l, kr0);
+        tile_gload<D, 64, NT>(kbase, j0 + kKeyTile * wave, j1, l, kr0);
         for (int it = 0; it < rounds; it += 2) {
             const uint64_t t0 = j0 + 4 * kKeyTile * it + kKeyTile * wave;
-            tile_gload<D, 64, MR != 2>(kbase, t0 + 4 * kKeyTile, j1, l, kr1);
+            tile_gload<D, 64, NT>(kbase, t0 + 4 * kKeyTile, j1, l, kr1);
             __builtin_amdgcn_sched_barrier(0);
             tile(t0, kr0);
             if (it + 1 < rounds) {
-                tile_gload<D, 64, MR != 2>(kbase, t0 + 8 * kKeyTile, j1, l, kr0);
+                tile_gload<D, 64, NT>(kbase, t0 + 8 * kKeyTile, j1, l, kr0);
                 __builtin_amdgcn_sched_barrier(0);
                 tile(t0 + 4 * kKeyTile, kr1);
             }
         }
     }
-    float mo = __shfl_xor(m, 16);
-    m = mo > m ? mo : m;
-    mo = __shfl_xor(m, 32);
-    m = mo > m ? mo : m;
-    if (G == 0) red[wave][i] = m;
-    __syncthreads();
-    if (threadIdx.x < 16 && static_cast<int>(threadIdx.x) < a.g) {
-        float r = red[0][threadIdx.x];
 #pragma unroll
-        for (int w = 1; w < 4; w++) r = red[w][threadIdx.x] > r ? red[w][threadIdx.x] : r;
-        a.wgmax[(static_cast<uint64_t>(kvh) * a.g + threadIdx.x) * a.nwg_qk + wg] = r;
+    for (int z = 0; z < NG; z++) {
+        float mz = m[z];
+        float mo = __shfl_xor(mz, 16);
+        mz = mo > mz ? mo : mz;
+        mo = __shfl_xor(mz, 32);
+        mz = mo > mz ? mo : mz;
+        if (G == 0) red[z][wave][i] = mz;
+    }
+    __syncthreads();
+    // thread z 16 + i: column i of group z
+    const int z = static_cast<int>(threadIdx.x) / 16, ic = static_cast<int>(threadIdx.x) % 16;
+    if (z < ng && ic < a.g) {
+        float r = red[z][0][ic];
+#pragma unroll
+        for (int w = 1; w < 4; w++) r = red[z][w][ic] > r ? red[z][w][ic] : r;
+        a.wgmax[(static_cast<uint64_t>(kvh0 + (MG ? z : 0)) * a.g + ic) * a.nwg_qk + wg] = r;
     }
 }
 

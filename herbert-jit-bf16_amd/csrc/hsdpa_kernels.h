@@ -54,6 +54,7 @@ struct DecodeArgs {
     // y are (row, head) pairs, column c serving row c / G and query head
     // y G + c % G, whose visible keys are [0, past + row].
     int xcd;                // 1: the groups of a key range numbered onto one XCD (several groups)
+    int qk_all;             // 1: pass 1 scores all sub groups of a KV head in each workgroup
     int rows;               // 1 for a decode step
     int G;                  // query heads per KV head
     int cols;               // columns per KV head that hold a (row, head) pair: rows * G; sub * g may
@@ -179,6 +180,21 @@ inline bool decode_wide_ok(int d) { return d <= 256 && (d / 16 >= 8 || 8 % (d / 
 // so few rows.
 constexpr int kDecodeMaxRows = 8;
 constexpr int kDecodeMaxCols = 4 * kDecodeMaxGroup;     // columns per KV head
+// pass 1 scores up to this many groups of a KV head in one workgroup
+constexpr int kDecodeMaxSub = 4;
+// Whether pass 1 of a Chained decode call on the tuned head dimensions takes
+// all of a KV head's groups in each workgroup (its grid then has no group
+// axis): 2 to kDecodeMaxSub groups, where a tile per wave of these workgroups
+// (kv_wgs = kv_heads x the 128-key blocks) would still take more than one
+// round of the compute units, so that every wave scores at least two tiles.
+// On 2 KV heads at head_dim 256 from 24K keys on (24K: 8 rows 48.0 -> 42.7 us,
+// 32 query heads per KV head 31.6 -> 31.1 us; 32K: 8 rows 59.6 -> 53.7 us);
+// below it, one workgroup per group fills the compute units better (8K: 8 rows
+// 21.9 us per group, 24.1 all groups; 16K: 2 groups of 16 heads 20.3 and 21.9).
+inline bool decode_qk_groups(int sub, uint64_t kv_wgs, uint64_t cus)
+{
+    return sub >= 2 && sub <= kDecodeMaxSub && kv_wgs > cus;
+}
 inline bool decode_rows_ok(int d) { return d == 64 || d == 128 || d == 256; }
 
 // Pass 2 in chunks (one round of workgroups over a long cache) is built for

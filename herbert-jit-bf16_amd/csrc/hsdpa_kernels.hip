@@ -290,9 +290,19 @@ static hipError_t decode_dm(const DecodeArgs &a, int kv_heads, hipStream_t s)
     const auto pad8 = [](int n) { return static_cast<unsigned>((n + 7) / 8 * 8); };
     const dim3 gqk = xcd ? dim3(pad8(a.nwg_qk) * a.sub, kv_heads, 1) : dim3(a.nwg_qk, kv_heads, a.sub);
     const dim3 gpv = xcd ? dim3(pad8(a.nwg_pv) * a.sub, kv_heads, 1) : dim3(a.nwg_pv, kv_heads, a.sub);
-    hipError_t e = a.keys_qk == 8 * kKeyTile ? launch(decode_qk<D, true, MR, false, true>, gqk, dim3(256), s, a)
-                   : a.keys_qk > 4 * kKeyTile  ? launch(decode_qk<D, true, MR>, gqk, dim3(256), s, a)
-                                               : launch(decode_qk<D, false, MR>, gqk, dim3(256), s, a);
+    hipError_t e;
+    if (a.qk_all) {
+        // pass 1 scores all the KV head's groups in one workgroup, two or more
+        // tiles per wave (decode_qk_groups)
+        const dim3 g1(a.nwg_qk, kv_heads, 1);
+        if (a.keys_qk <= 4 * kKeyTile) return hipErrorInvalidValue;
+        e = a.keys_qk == 8 * kKeyTile ? launch(decode_qk<D, true, MR, false, true, true>, g1, dim3(256), s, a)
+                                      : launch(decode_qk<D, true, MR, false, false, true>, g1, dim3(256), s, a);
+    } else {
+        e = a.keys_qk == 8 * kKeyTile ? launch(decode_qk<D, true, MR, false, true>, gqk, dim3(256), s, a)
+            : a.keys_qk > 4 * kKeyTile  ? launch(decode_qk<D, true, MR>, gqk, dim3(256), s, a)
+                                        : launch(decode_qk<D, false, MR>, gqk, dim3(256), s, a);
+    }
     if (e != hipSuccess) return e;
     if (a.g <= 8) {
         if (a.keys_pv == 4 * kKeyTile) e = launch(decode_pv<D, 4, 1, false, MR>, gpv, dim3(256), s, a);

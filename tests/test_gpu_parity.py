@@ -103,6 +103,11 @@ FEW = [
     ("few_r8_d128_g16_causal_kernel", 32, 2, 128, 8, 500),  # 128 columns
     ("few_r2_d128_g32_p700", 32, 1, 128, 2, 700),          # 64 columns: four groups of 16
     ("few_r5_d256_g3_p333", 6, 2, 256, 5, 333),            # 15 columns: one group, two P blocks
+    # pass 1 scoring every group of a KV head in one workgroup (more than one
+    # round of such workgroups): four groups, two tiles per wave; two groups,
+    # three tiles per wave at D 128
+    ("few_r8_d256_g8_p20000", 16, 2, 256, 8, 20000),
+    ("few_r4_d128_g8_p33000", 16, 2, 128, 4, 33000),
     # long caches at D 64 and 128: pass 2 in chunks
     ("few_r4_d128_g8_p40000_chunked", 16, 2, 128, 4, 40000),
     ("few_r2_d128_g8_p70000_chunked", 16, 2, 128, 2, 70000),
@@ -190,6 +195,8 @@ GROUPS = [
     ("decode_g24_d256_two_groups_8_wave", 48, 2, 256, 1, 33000, "decode"),
     ("decode_g20_d256_loop", 40, 2, 256, 1, 70000, "decode"),
     ("decode_g17_d128_padded", 17, 1, 128, 1, 900, "decode"),                 # 2 groups of 9, one padded
+    # 3 groups of 12, one padded, all scored in each pass-1 workgroup
+    ("decode_g34_d128_padded_all_groups", 34, 1, 128, 1, 40000, "decode"),
     ("decode_g17_d256_padded_2kv_long", 34, 2, 256, 1, 40000, "decode"),
     ("decode_g80_d64_five_groups", 80, 1, 64, 1, 300, "decode"),              # 5 groups of 16
     ("decode_g80_d64_five_groups_long", 80, 1, 64, 1, 6000, "decode"),
