@@ -276,7 +276,7 @@ namespace {
 // How the decode passes cover a call: `sub` groups of `g` columns per KV
 // head, keys per workgroup and workgroups per group of each pass.
 struct DecodeCfg {
-    int sub, g, keys_qk, keys_pv, nwg_qk, nwg_pv, xcd, qk_all;
+    int sub, g, keys_qk, keys_pv, nwg_qk, nwg_pv, xcd, qk_all, pv_all;
 };
 
 // Whether `rows` rows run on the decode kernels: one row whose g query heads
@@ -361,6 +361,10 @@ DecodeCfg decode_cfg(const hsdpa_plan *p, uint64_t rows, uint64_t n, int sub, bo
     }
     c.nwg_qk = static_cast<int>((n + c.keys_qk - 1) / c.keys_qk);
     c.nwg_pv = static_cast<int>((n + c.keys_pv - 1) / c.keys_pv);
+    // where pass 1 takes all of a KV head's groups and pass 2 runs 256-key
+    // workgroups (D = 256; at D = 64 and 128 it takes chunks there), pass 2
+    // takes them all too: each V tile loaded once instead of once per group
+    c.pv_all = c.qk_all && c.keys_pv == hsdpa::kDecodeKeysPV && d == 256 ? 1 : 0;
     // several groups: a key range's groups on one XCD, whose L2 then serves
     // the later ones (a few rows: 3-8 rows after 32K 11-14 % faster; one row
     // where pass 2 takes several rounds of workgroups, not chunks: 48 heads on
@@ -543,6 +547,7 @@ static hsdpa_status run_part(const hsdpa_plan *plan, const hsdpa_call *call, con
         a.nwg_pv = c.nwg_pv;
         a.xcd = c.xcd;
         a.qk_all = c.qk_all;
+        a.pv_all = c.pv_all;
         a.scale = call->scale;
         a.gate = gp;
         const hipError_t e = part.fused ? hsdpa::launch_decode_fused(a, d, static_cast<int>(plan->kv_heads), st)

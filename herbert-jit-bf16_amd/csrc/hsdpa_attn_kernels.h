@@ -911,6 +911,141 @@ __global__ __launch_bounds__(64 * W, D > 256 ? 1 : 8 / W) void decode_pv(DecodeA
 }
 
 // ---------------------------------------------------------------------------
+// Decode pass 2 over every group of a KV head in one workgroup (2 to
+// kDecodeMaxSub groups of 9 to 16 columns; 8 waves, 256 keys, as decode_pv's
+// 8-wave form with two P column blocks). The V tiles are loaded and staged in
+// LDS once, and each wave reads its V^T operands into registers once; then,
+// for each group in turn, the exact maximum of its columns, the exponentials
+// (hi + lo P columns in LDS) and P.V, the next group's scores and maxima
+// requested before this group's products. The partials go where decode_pv
+// puts them, so the combine is the same. Every column carries its row's
+// causal limit (a few rows; one row sees all keys). Grid (nwg_pv, kv_heads).
+// ---------------------------------------------------------------------------
+template <int D>
+__global__ __launch_bounds__(512, 1) void decode_pv_all(DecodeArgs a)
+{
+    constexpr int W = 8, NCB = 2, THREADS = 64 * W, KEYS = W * kKeyTile, PS = KEYS + 8;
+    constexpr int DB = D / 16, DBW = DB / W, nh = 8 * NCB;
+    static_assert(DB % W == 0, "each wave takes whole dimension blocks");
+    constexpr int T = THREADS / nh, BATCH = 8;                  // lanes per column's maxima
+    __shared__ __attribute__((aligned(16))) uint16_t vt[W][kKeyTile * D];
+    __shared__ __attribute__((aligned(16))) uint16_t pc[2 * kDecodeMaxGroup * PS];
+    __shared__ float smax[kDecodeMaxGroup];
+    __shared__ float lpart[W][kDecodeMaxGroup];
+    const int wg = static_cast<int>(blockIdx.x), tid = threadIdx.x;
+    const int kvh0 = static_cast<int>(blockIdx.y) * a.sub, ng = a.sub;
+    const int wave = tid >> 6, l = tid & 63, j = l & 15, G = l >> 4;
+    const uint64_t j0 = static_cast<uint64_t>(wg) * KEYS;
+    const uint64_t j1 = j0 + KEYS < a.n ? j0 + KEYS : a.n;
+    const uint16_t *vbase = a.v + static_cast<uint64_t>(blockIdx.y) * a.kv_stride;
+    const int key_e = tid % KEYS;
+    const uint64_t gk = j0 + key_e;
+    const bool kv_e = gk < j1;
+    const int jh = tid / T, u = tid % T;
+    float sv[kDecodeMaxGroup / 2], mx[BATCH];
+    // group z's scores of this thread's key (columns tid / KEYS + 2 i) and the
+    // first batch of its columns' pass-1 maxima
+    auto load_group = [&](int z) {
+        const int kvh = kvh0 + z;
+#pragma unroll
+        for (int i = 0; i < kDecodeMaxGroup / 2; i++) {
+            const int h = tid / KEYS + 2 * i;
+            const int hc = h < a.g ? h : 0;
+            sv[i] = a.scores[static_cast<uint64_t>(kvh * a.g + hc) * a.npad + (kv_e ? gk : 0)];
+        }
+        const float *msrc = a.wgmax + (static_cast<uint64_t>(kvh) * a.g + (jh < a.g ? jh : 0)) * a.nwg_qk;
+#pragma unroll
+        for (int b = 0; b < BATCH; b++) {
+            const int w = u + b * T;
+            mx[b] = msrc[w < a.nwg_qk ? w : 0];
+        }
+    };
+    load_group(0);
+    u32x4 vr[Tile<D, 64>::kPer];
+    tile_gload<D, 64, true>(vbase, j0 + kKeyTile * wave, j1, l, vr);
+    __builtin_amdgcn_sched_barrier(0);                          // all loads issued first
+    u32x4 av[W][DBW];                                           // this wave's V^T operands, all tiles
+    // one group: FIRST also stages V and reads the V^T operands
+    auto group = [&](int z, auto first_t) {
+        constexpr bool FIRST = decltype(first_t)::value;
+        const int kvh = kvh0 + z;
+        float m = kNegInf;
+#pragma unroll
+        for (int b = 0; b < BATCH; b++) m = (u + b * T < a.nwg_qk && mx[b] > m) ? mx[b] : m;
+        const float *msrc = a.wgmax + (static_cast<uint64_t>(kvh) * a.g + (jh < a.g ? jh : 0)) * a.nwg_qk;
+        for (int w0 = u + BATCH * T; w0 < a.nwg_qk; w0 += BATCH * T) {
+#pragma unroll
+            for (int b = 0; b < BATCH; b++) {
+                const int w = w0 + b * T;
+                mx[b] = msrc[w < a.nwg_qk ? w : 0];
+            }
+#pragma unroll
+            for (int b = 0; b < BATCH; b++) m = (w0 + b * T < a.nwg_qk && mx[b] > m) ? mx[b] : m;
+        }
+        m = group_max_hi(m, T);
+        // the previous group's P operand reads and partial sums are done
+        // before this barrier, so its slots may be rewritten after it
+        if (u == T - 1 && jh < a.g) smax[jh] = m;
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < kDecodeMaxGroup / 2; i++) {
+            const int h = tid / KEYS + 2 * i;
+            if (h >= a.g) break;
+            // column h's row sees keys [0, past + row]
+            const int row = (z * a.g + h) / a.G;
+            const bool vis = kv_e && gk <= a.past + static_cast<uint64_t>(row);
+            const float e = vis ? exp_poly(sv[i] - smax[h]) : 0.0f;
+            const uint32_t hb = bf16_rne(e);
+            pc[h * PS + key_e] = static_cast<uint16_t>(hb);
+            pc[(nh + h) * PS + key_e] = static_cast<uint16_t>(bf16_rne(e - __uint_as_float(hb << 16)));
+            const float sum = wave_sum_hi(e);
+            if (l == 63) lpart[wave][h] = sum;
+        }
+        if (z + 1 < ng) load_group(z + 1);
+        if constexpr (FIRST) tile_mask_lstore_v16<D, 64>(vt[wave], j0 + kKeyTile * wave, j1, l, vr);
+        __syncthreads();
+        if constexpr (FIRST) {
+#pragma unroll
+            for (int t = 0; t < W; t++)
+#pragma unroll
+                for (int db = 0; db < DBW; db++) av[t][db] = vt16_operand<D>(vt[t], 16 * (wave * DBW + db), l);
+        }
+        u32x4 bp[W][NCB];
+#pragma unroll
+        for (int t = 0; t < W; t++)
+#pragma unroll
+            for (int c = 0; c < NCB; c++) bp[t][c] = load16(pc + (16 * c + j) * PS + kKeyTile * t + 8 * G);
+        __builtin_amdgcn_sched_barrier(0);
+        f32x4 o[NCB][DBW] = {};
+#pragma unroll
+        for (int t = 0; t < W; t++)
+#pragma unroll
+            for (int db = 0; db < DBW; db++)
+#pragma unroll
+                for (int c = 0; c < NCB; c++) o[c][db] = mfma16(av[t][db], bp[t][c], o[c][db]);
+        // O(column) = O(hi block) + O(lo block)
+        const uint64_t pbase = (static_cast<uint64_t>(kvh) * a.nwg_pv + wg) * a.g;
+#pragma unroll
+        for (int db = 0; db < DBW; db++) {
+            if (j < a.g) {
+                float *dst = a.part_o + (pbase + j) * D + 16 * (wave * DBW + db) + 4 * G;
+                *reinterpret_cast<float4 *>(dst) = float4{o[0][db][0] + o[1][db][0], o[0][db][1] + o[1][db][1],
+                                                          o[0][db][2] + o[1][db][2], o[0][db][3] + o[1][db][3]};
+            }
+        }
+        if (tid < a.g) {
+            // columns of parity p were summed by waves 4 p .. 4 p + 3, 64 keys each
+            const int p0 = (tid % (THREADS / KEYS)) * (KEYS / 64);
+            float L = 0.0f;
+            for (int w = 0; w < KEYS / 64; w++) L += lpart[p0 + w][tid];
+            a.part_l[pbase + tid] = L;
+        }
+    };
+    group(0, std::true_type{});
+    for (int z = 1; z < ng; z++) group(z, std::false_type{});
+}
+
+// ---------------------------------------------------------------------------
 // Decode pass 3: out[h] = bf16(sum_w O_w / sum_w l_w).
 // grid (heads, D/64), 512 threads: 64 dimensions x 8 interleaved partial
 // subsets; every thread issues all its loads before adding (one round trip

@@ -55,6 +55,7 @@ struct DecodeArgs {
     // y G + c % G, whose visible keys are [0, past + row].
     int xcd;                // 1: the groups of a key range numbered onto one XCD (several groups)
     int qk_all;             // 1: pass 1 scores all sub groups of a KV head in each workgroup
+    int pv_all;             // 1: pass 2 (256-key workgroups) takes all sub groups in each workgroup
     int rows;               // 1 for a decode step
     int G;                  // query heads per KV head
     int cols;               // columns per KV head that hold a (row, head) pair: rows * G; sub * g may

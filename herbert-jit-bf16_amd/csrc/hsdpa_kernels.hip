@@ -304,7 +304,15 @@ static hipError_t decode_dm(const DecodeArgs &a, int kv_heads, hipStream_t s)
                                         : launch(decode_qk<D, false, MR>, gqk, dim3(256), s, a);
     }
     if (e != hipSuccess) return e;
-    if (a.g <= 8) {
+    if (a.pv_all) {
+        // pass 2 over all the KV head's groups in one workgroup
+        if constexpr (D == 256) {
+            if (a.keys_pv != kDecodeKeysPV) return hipErrorInvalidValue;
+            e = launch(decode_pv_all<D>, dim3(a.nwg_pv, kv_heads, 1), dim3(512), s, a);
+        } else {
+            return hipErrorInvalidValue;
+        }
+    } else if (a.g <= 8) {
         if (a.keys_pv == 4 * kKeyTile) e = launch(decode_pv<D, 4, 1, false, MR>, gpv, dim3(256), s, a);
         else if (a.keys_pv <= kDecodeKeysPV) e = launch(decode_pv<D, 8, 1, false, MR>, gpv, dim3(512), s, a);
         else if constexpr (!MR || D < 256) e = launch(decode_pv<D, 8, 1, true, MR>, gpv, dim3(512), s, a);
