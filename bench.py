@@ -248,6 +248,8 @@ CONFIG_TEXT = {
                             "channels per KV head x20, 1% of value rows x8",
 }
 DECODE_KERNELS = "decode step (decode_qk + decode_pv + decode_combine)"
+# up to 1024 keys (one row, one group): pass 2 writes the outputs itself
+DECODE_DIRECT = "decode step (decode_qk + decode_direct, no combine launch)"
 
 
 def bench_config(torch, hsdpa, W, name, kind, steps, warmup, form="chained"):
@@ -265,6 +267,7 @@ def bench_config(torch, hsdpa, W, name, kind, steps, warmup, form="chained"):
     if not torch.equal(eager, replay):
         print(f"{name}: graph replay differs from the eager call", file=sys.stderr)
         sys.exit(3)
+    launches = plan.route(w.rows, w.past)["launches"]
     del q, ks, vs, out, ws
     torch.cuda.empty_cache()
     text = f"{name}: {CONFIG_TEXT[name]}, bf16 q/K/V/out, f32 accumulation, scale 1/16"
@@ -280,7 +283,7 @@ def bench_config(torch, hsdpa, W, name, kind, steps, warmup, form="chained"):
                 "config": {"workload": text, "algorithmic_bytes": nbytes, "kv_caches_rotated": copies},
                 "roofline": {"bound": "hbm", "achieved": round(val, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                              "frac": round(val / HBM_PEAK_GBS, 4), "traffic": round(tr) if tr else None,
-                             "kernel": DECODE_KERNELS}}
+                             "kernel": DECODE_DIRECT if launches == 2 else DECODE_KERNELS}}
     flops = w.prefill_flops()
     val = flops / (ms * 1e-3) / 1e12
     log(f"{name}: {ms*1e3:.2f} us/step, {val:.1f} TFLOP/s ({val/MFMA_BF16_PEAK_TFS:.1%} of MFMA peak)")

@@ -276,7 +276,7 @@ namespace {
 // How the decode passes cover a call: `sub` groups of `g` columns per KV
 // head, keys per workgroup and workgroups per group of each pass.
 struct DecodeCfg {
-    int sub, g, keys_qk, keys_pv, nwg_qk, nwg_pv, xcd, qk_all, pv_all;
+    int sub, g, keys_qk, keys_pv, nwg_qk, nwg_pv, xcd, qk_all, pv_all, direct;
 };
 
 // Whether `rows` rows run on the decode kernels: one row whose g query heads
@@ -365,6 +365,8 @@ DecodeCfg decode_cfg(const hsdpa_plan *p, uint64_t rows, uint64_t n, int sub, bo
     // workgroups (D = 256; at D = 64 and 128 it takes chunks there), pass 2
     // takes them all too: each V tile loaded once instead of once per group
     c.pv_all = c.qk_all && c.keys_pv == hsdpa::kDecodeKeysPV && d == 256 ? 1 : 0;
+    // a short cache: pass 2 writes the outputs itself, no combine launch
+    c.direct = !fused && hsdpa::decode_direct_ok(d, static_cast<int>(rows), sub, c.g, n) ? 1 : 0;
     // several groups: a key range's groups on one XCD, whose L2 then serves
     // the later ones (a few rows: 3-8 rows after 32K 11-14 % faster; one row
     // where pass 2 takes several rounds of workgroups, not chunks: 48 heads on
@@ -514,7 +516,7 @@ static hsdpa_status run_part(const hsdpa_plan *plan, const hsdpa_call *call, con
         const DecodeCfg c = decode_cfg(plan, rows, n, sub, part.fused);
         if (kernels) *kernels = rows == 1 ? HSDPA_KERNELS_DECODE : HSDPA_KERNELS_FEW_ROWS;
         if (splits) *splits = 1;
-        if (launches) *launches += 3;
+        if (launches) *launches += c.direct ? 2 : 3;
         if (!launch) return HSDPA_OK;
         hsdpa::DecodeArgs a{};
         a.q = q;
@@ -548,6 +550,7 @@ static hsdpa_status run_part(const hsdpa_plan *plan, const hsdpa_call *call, con
         a.xcd = c.xcd;
         a.qk_all = c.qk_all;
         a.pv_all = c.pv_all;
+        a.direct = c.direct;
         a.scale = call->scale;
         a.gate = gp;
         const hipError_t e = part.fused ? hsdpa::launch_decode_fused(a, d, static_cast<int>(plan->kv_heads), st)

@@ -1046,6 +1046,142 @@ __global__ __launch_bounds__(512, 1) void decode_pv_all(DecodeArgs a)
 }
 
 // ---------------------------------------------------------------------------
+// Decode pass 2 and the combine in one launch for short caches (one row, g <=
+// 8 query heads per KV head in one group, n <= kDirectKeys). Workgroup (s,
+// kvh) computes dimensions [DS s, DS s + DS) of the g outputs over all n keys
+// (DS = kDirectSlice). Every load is issued first: the g heads' scores and
+// pass-1 maxima, and the V slice (n rows of 2 DS bytes). Then the exact
+// maxima (wave h reduces head h's),
+// the g x n exponentials as P columns [hi of 8 heads | lo of 8 heads] in LDS
+// (as decode_pv; each slice's workgroup computes all of them, at most 16 per
+// thread), the V slice to LDS, P.V with the 32-key tiles dealt to the 8 waves,
+// the waves' partial outputs summed in LDS in wave order, and
+// out = bf16(O / l), gated like the combine's. Grid (D / DS, kv_heads).
+// ---------------------------------------------------------------------------
+template <int D, int DS = kDirectSlice>
+__global__ __launch_bounds__(512, 1) void decode_direct(DecodeArgs a)
+{
+    constexpr int W = 8, THREADS = 64 * W, DBS = DS / 16, NK = kDirectKeys, PS = NK + 8;
+    constexpr int R = NK / 256, CH = NK * DS / 8 / THREADS, NT = NK / kKeyTile;
+    static_assert(D % DS == 0 && NK % 256 == 0 && CH * THREADS * 8 == NK * DS, "slices and rounds");
+    __shared__ __attribute__((aligned(16))) uint16_t vs[NK * DS];
+    __shared__ __attribute__((aligned(16))) uint16_t pc[16 * PS];
+    __shared__ float smax[8];
+    __shared__ float lpart[W][8];
+    __shared__ float ored[W][DBS][4][64];
+    const int tid = threadIdx.x, wave = tid >> 6, l = tid & 63, j = l & 15, G = l >> 4;
+    const int kvh = static_cast<int>(blockIdx.y), d0 = static_cast<int>(blockIdx.x) * DS;
+    const uint64_t n = a.n;
+    const int g = a.g;
+    // thread t: keys t % 256 + 256 r, heads t / 256 + 2 i (the same for a
+    // whole wave, so the head loops end alike in every lane)
+    const int kb = tid % 256, hp = tid / 256;
+    float sv[R][4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int h = hp + 2 * i;
+        if (h >= g) break;
+        const float *src = a.scores + static_cast<uint64_t>(kvh * g + h) * a.npad;
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const uint64_t key = static_cast<uint64_t>(kb + 256 * r);
+            sv[r][i] = src[key < n ? key : 0];
+        }
+    }
+    // wave h: head h's pass-1 maxima (nwg_qk <= NK / 128 <= 64 entries)
+    const float mxv = wave < g && l < a.nwg_qk
+                          ? a.wgmax[static_cast<uint64_t>(kvh * g + wave) * a.nwg_qk + l]
+                          : kNegInf;
+    // the V slice: chunk c = tid + THREADS i is key c / (DS / 8), bytes
+    // 16 (c % (DS / 8)).. of the slice; keys past the cache read row 0 and are
+    // stored as zeros
+    const uint16_t *vbase = a.v + static_cast<uint64_t>(kvh) * a.kv_stride + d0;
+    u32x4 vr[CH];
+#pragma unroll
+    for (int c = 0; c < CH; c++) {
+        const int idx = tid + THREADS * c, key = idx / (DS / 8), part = idx % (DS / 8);
+        vr[c] = load16(vbase + static_cast<uint64_t>(static_cast<uint64_t>(key) < n ? key : 0) * D + 8 * part);
+    }
+    __builtin_amdgcn_sched_barrier(0);                          // all loads issued first
+    const float m = group_max_hi(mxv, 64);
+    if (l == 63 && wave < g) smax[wave] = m;
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int h = hp + 2 * i;
+        if (h >= g) break;
+        float le = 0.0f;
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const int key = kb + 256 * r;
+            const float e = static_cast<uint64_t>(key) < n ? exp_poly(sv[r][i] - smax[h]) : 0.0f;
+            const uint32_t hb = bf16_rne(e);
+            pc[h * PS + key] = static_cast<uint16_t>(hb);
+            pc[(8 + h) * PS + key] = static_cast<uint16_t>(bf16_rne(e - __uint_as_float(hb << 16)));
+            le += e;
+        }
+        const float sum = wave_sum_hi(le);
+        if (l == 63) lpart[wave][h] = sum;
+    }
+#pragma unroll
+    for (int c = 0; c < CH; c++) {
+        const int idx = tid + THREADS * c, key = idx / (DS / 8), part = idx % (DS / 8), kk = key % kKeyTile;
+        store16(vs + (key / kKeyTile) * (kKeyTile * DS) + kk * DS + 8 * swz16<DS>(kk, part),
+                static_cast<uint64_t>(key) < n ? vr[c] : u32x4{0, 0, 0, 0});
+    }
+    __syncthreads();
+    // O^T = V^T . P^T over the tiles t = wave, wave + 8, ..; lane (j, G)
+    // holds column j (hi of head j, lo of head j - 8), dimensions 4 G .. 4 G + 3
+    // of each 16-dimension block
+    const int nt = static_cast<int>((n + kKeyTile - 1) / kKeyTile);
+    f32x4 o[DBS] = {};
+#pragma unroll
+    for (int k = 0; k < NT / W; k++) {
+        const int t = wave + W * k;
+        if (t < nt) {
+            const u32x4 bp = load16(pc + j * PS + kKeyTile * t + 8 * G);
+#pragma unroll
+            for (int db = 0; db < DBS; db++)
+                o[db] = mfma16(vt16_operand<DS>(vs + t * (kKeyTile * DS), 16 * db, l), bp, o[db]);
+        }
+    }
+#pragma unroll
+    for (int db = 0; db < DBS; db++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) ored[wave][db][r][l] = o[db][r];
+    __syncthreads();
+    if (wave == 0) {
+        const int h = j & 7;
+        float L = 0.0f;
+        // heads of parity p were summed by waves 4 p .. 4 p + 3
+#pragma unroll
+        for (int w = 0; w < 4; w++) L += lpart[4 * (h & 1) + w][h < g ? h : 0];
+#pragma unroll
+        for (int db = 0; db < DBS; db++) {
+            f32x4 s = {};
+#pragma unroll
+            for (int w = 0; w < W; w++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) s[r] += ored[w][db][r][l];
+            uint16_t ob[4];
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const float os = s[r] + __shfl_xor(s[r], 8);    // hi column + lo column
+                ob[r] = static_cast<uint16_t>(cvt_out(os / L));
+            }
+            if (j < 8 && j < g) {
+                const uint64_t at = static_cast<uint64_t>(kvh * g + j) * D + d0 + 16 * db + 4 * G;
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    if (a.gate) ob[r] = gate_bf16(ob[r], a.gate[at + r]);
+                    a.out[at + r] = ob[r];
+                }
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Decode pass 3: out[h] = bf16(sum_w O_w / sum_w l_w).
 // grid (heads, D/64), 512 threads: 64 dimensions x 8 interleaved partial
 // subsets; every thread issues all its loads before adding (one round trip

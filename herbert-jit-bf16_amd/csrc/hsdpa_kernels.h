@@ -56,6 +56,7 @@ struct DecodeArgs {
     int xcd;                // 1: the groups of a key range numbered onto one XCD (several groups)
     int qk_all;             // 1: pass 1 scores all sub groups of a KV head in each workgroup
     int pv_all;             // 1: pass 2 (256-key workgroups) takes all sub groups in each workgroup
+    int direct;             // 1: pass 2 writes the outputs itself (decode_direct_ok), no combine
     int rows;               // 1 for a decode step
     int G;                  // query heads per KV head
     int cols;               // columns per KV head that hold a (row, head) pair: rows * G; sub * g may
@@ -197,6 +198,19 @@ inline bool decode_qk_groups(int sub, uint64_t kv_wgs, uint64_t cus)
     return sub >= 2 && sub <= kDecodeMaxSub && kv_wgs > cus;
 }
 inline bool decode_rows_ok(int d) { return d == 64 || d == 128 || d == 256; }
+// Short caches: pass 2 over every key in each workgroup, which writes the
+// outputs itself (no combine launch): one row, one group of at most 8 query
+// heads per KV head, at most kDirectKeys visible keys, the tuned head
+// dimensions, the Chained form.
+constexpr int kDirectKeys = 1024;
+// dimensions per workgroup of that pass: 16, one MFMA block (twice the
+// workgroups of 32-dimension slices, 1024 keys on 8/2 heads at D = 256 10.96
+// -> 9.95 us)
+constexpr int kDirectSlice = 16;
+inline bool decode_direct_ok(int d, int rows, int sub, int g, uint64_t n)
+{
+    return decode_rows_ok(d) && rows == 1 && sub == 1 && g <= 8 && n <= static_cast<uint64_t>(kDirectKeys);
+}
 
 // Pass 2 in chunks (one round of workgroups over a long cache) is built for
 // the tuned head dimensions, at D = 256 for one row in groups of up to 8

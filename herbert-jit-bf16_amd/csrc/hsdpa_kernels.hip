@@ -304,6 +304,11 @@ static hipError_t decode_dm(const DecodeArgs &a, int kv_heads, hipStream_t s)
                                         : launch(decode_qk<D, false, MR>, gqk, dim3(256), s, a);
     }
     if (e != hipSuccess) return e;
+    if (a.direct) {
+        // a short cache: pass 2 writes the outputs (decode_direct_ok)
+        if constexpr (MR == 0) return launch(decode_direct<D>, dim3(D / kDirectSlice, kv_heads), dim3(512), s, a);
+        else return hipErrorInvalidValue;
+    }
     if (a.pv_all) {
         // pass 2 over all the KV head's groups in one workgroup
         if constexpr (D == 256) {

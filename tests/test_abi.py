@@ -115,6 +115,14 @@ def test_route_names_the_kernels():
     p = hsdpa.Plan(16, 8, 256, 40000)
     assert p.route(1, 32767)["main"] == "decode"
     assert p.route(4, 100)["main"] == "few_rows"
+    # up to 1024 visible keys (one row, one group of at most 8 heads) pass 2
+    # writes the outputs itself: two launches; past that, or with more heads
+    # per KV head, three
+    assert p.route(1, 1023)["launches"] == 2 and p.route(1, 0)["launches"] == 2
+    assert p.route(1, 1024)["launches"] == 3
+    assert hsdpa.Plan(32, 16, 256, 4096).route(1, 100)["launches"] == 3
+    assert hsdpa.Plan(16, 8, 256, 4096, form="fused").route(1, 100)["launches"] == 3
+    assert hsdpa.Plan(16, 8, 96, 4096).route(1, 100)["launches"] == 3
     r = p.route(4096, 8192)       # one round of row groups, the longest paired with the shortest
     assert r["main"] == "causal_paired" and r["launches"] == 3 and r["tail"] == "none"
     r = p.route(8192, 0)          # two rounds: the heaviest row groups first

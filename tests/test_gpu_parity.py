@@ -18,6 +18,13 @@ SMALL = [
     ("decode_d256_n37", 8, 2, 256, 1, 36, "decode"),
     ("decode_d128_n300", 16, 4, 128, 1, 299, "decode"),
     ("decode_d64_g1", 4, 4, 64, 1, 77, "decode"),
+    # up to 1024 keys pass 2 writes the outputs itself (no combine): both
+    # sides of 1024, one partial tile, one head per KV head, odd groups
+    ("decode_direct_d256_n1024_g8", 16, 2, 256, 1, 1023, "decode"),
+    ("decode_combine_d128_n1025_g8", 16, 2, 128, 1, 1024, "decode"),
+    ("decode_direct_d64_n33_g8", 8, 1, 64, 1, 32, "decode"),
+    ("decode_direct_d128_n32_g1", 4, 4, 128, 1, 31, "decode"),
+    ("decode_direct_d256_n700_g3_kv5", 15, 5, 256, 1, 699, "decode"),
     ("prefill_d256_r2_g40", 80, 2, 256, 2, 0, "causal"),              # 80 columns: past the decode kernels
     ("prefill_d256_r19_p37", 8, 2, 256, 19, 37, "causal"),
     ("prefill_d128_r70_p5", 8, 8, 128, 70, 5, "causal"),
