@@ -279,19 +279,22 @@ struct DecodeCfg {
     int sub, g, keys_qk, keys_pv, nwg_qk, nwg_pv, xcd, qk_all, pv_all, direct;
 };
 
-// Whether `rows` rows run on the decode kernels: one row whose g query heads
-// split into at most 4 groups of at most 16, or up to 8 rows as (row, head)
-// columns at head dimensions 64, 128 and 256 within the plan's columns; at
+// Whether `rows` rows over n visible keys run on the decode kernels: one row
+// whose g query heads split into at most 4 groups of at most 16, or up to 16
+// rows as (row, head) columns at head dimensions 64, 128 and 256 within the
+// plan's columns (past 8 rows or 64 columns, within decode_wide_ok_n); at
 // those head dimensions, columns no equal split fits take padded groups
-// (decode_groups_pad).
-int decode_sub(const hsdpa_plan *p, uint64_t rows)
+// (decode_groups_pad). n = 0: any n (the most a call of `rows` rows may take).
+int decode_sub(const hsdpa_plan *p, uint64_t rows, uint64_t n)
 {
     const uint64_t cols = rows * p->spec.gqa;
     const int d = static_cast<int>(p->spec.head_dim);
     const int even = cols <= static_cast<uint64_t>(4 * hsdpa::kDecodeMaxGroup) ? hsdpa::decode_groups(static_cast<int>(cols)) : 0;
     if (rows == 1 && even) return even;
     if (rows > hsdpa::kDecodeMaxRows || !hsdpa::decode_rows_ok(d) || cols > p->dec_cols) return 0;
-    return even ? even : hsdpa::decode_groups_pad(static_cast<int>(cols));
+    const int sub = even ? even : hsdpa::decode_groups_pad(static_cast<int>(cols));
+    if (sub && n && !hsdpa::decode_wide_ok_n(d, static_cast<int>(rows), static_cast<int>(cols), sub, n)) return 0;
+    return sub;
 }
 
 // The decode passes' grids for `rows` rows over n visible keys (decode_sub
@@ -397,7 +400,10 @@ uint64_t decode_nwg_pv_max(const hsdpa_plan *p, uint64_t rows, int sub)
 }
 
 // Whether a call of `rows` rows can reach the causal kernels.
-bool reaches_causal(const hsdpa_plan *p, uint64_t rows) { return decode_sub(p, rows) == 0; }
+bool reaches_causal(const hsdpa_plan *p, uint64_t rows)
+{
+    return decode_sub(p, rows, std::max<uint64_t>(p->spec.kv_capacity, rows)) == 0;
+}
 
 // The Fused form's rows outside full chunks of 8: the last rows % 8 (the
 // reference's passes of 256 rows are multiples of 8, so only the last pass
@@ -431,7 +437,7 @@ hsdpa_status hsdpa_plan_create(const hsdpa_spec *spec, hsdpa_plan **out)
     // no device current, the MI355X's 256
     int cus = 0;
     p->cus = check_device(&cus) == HSDPA_OK && cus > 0 ? cus : 256;
-    // decode columns: the query heads of one row, or up to 8 rows of them
+    // decode columns: the query heads of one row, or up to 16 rows of them
     const int gi = static_cast<int>(std::min<uint64_t>(g, 1u << 20));
     const bool pad_ok = hsdpa::decode_rows_ok(static_cast<int>(d)) && hsdpa::decode_groups_pad(gi) > 0;
     uint64_t cols = hsdpa::decode_groups(gi) || pad_ok ? g : 0;
@@ -446,7 +452,7 @@ hsdpa_status hsdpa_plan_create(const hsdpa_spec *spec, hsdpa_plan **out)
     // serves, its columns counting the padding of the last group
     uint64_t part = 0, cols_used = 0, cols_pad = 0;
     for (uint64_t r = 1; r <= std::min<uint64_t>(hsdpa::kDecodeMaxRows, p->max_rows); r++) {
-        const int sub = decode_sub(p, r);
+        const int sub = decode_sub(p, r, 0);
         if (sub == 0) continue;
         const uint64_t padded = static_cast<uint64_t>(sub) * hsdpa::decode_group_cols(static_cast<int>(r * g), sub);
         cols_used = std::max(cols_used, r * g);
@@ -511,7 +517,7 @@ static hsdpa_status run_part(const hsdpa_plan *plan, const hsdpa_call *call, con
     const uint16_t *q = call->q ? call->q + part.row0 * s.q_row : nullptr;
     uint16_t *outp = call->output ? call->output + part.row0 * s.out_row : nullptr;
     const uint16_t *gp = gate ? gate + part.row0 * gate_row : nullptr;
-    const int sub = decode_sub(plan, rows);
+    const int sub = decode_sub(plan, rows, past + rows);
     if (sub > 0) {
         const DecodeCfg c = decode_cfg(plan, rows, n, sub, part.fused);
         if (kernels) *kernels = rows == 1 ? HSDPA_KERNELS_DECODE : HSDPA_KERNELS_FEW_ROWS;
@@ -629,7 +635,7 @@ static hsdpa_status run_attention(const hsdpa_plan *plan, const hsdpa_call *call
     if (stt == HSDPA_OK && tail) {
         // the tail's kernels decide its numerics: the decode kernels compute the
         // Fused weights, the causal ones the Chained
-        const bool together = decode_sub(plan, tail) > 0;
+        const bool together = decode_sub(plan, tail, call->past + rows) > 0;
         uint32_t kern = HSDPA_KERNELS_NONE, sp = 1;
         if (together) {
             stt = run_part(plan, call, Part{main, tail, true}, gate, gate_row, st, launch, &kern, &sp, &r.launches);

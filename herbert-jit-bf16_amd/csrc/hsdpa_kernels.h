@@ -177,13 +177,25 @@ inline int decode_groups_pad(int cols)
 inline int decode_group_cols(int cols, int sub) { return (cols + sub - 1) / sub; }
 inline bool decode_wide_ok(int d) { return d <= 256 && (d / 16 >= 8 || 8 % (d / 16) == 0); }
 // A few rows after a cache run on the decode kernels (one column per (row,
-// head) pair, up to 4 groups of 16 columns per KV head) for the tuned head
+// head) pair, up to 8 groups of 16 columns per KV head) for the tuned head
 // dimensions; the causal kernel computes 32-row tiles, most of them wasted on
 // so few rows.
-constexpr int kDecodeMaxRows = 8;
-constexpr int kDecodeMaxCols = 4 * kDecodeMaxGroup;     // columns per KV head
+constexpr int kDecodeMaxRows = 16;
+constexpr int kDecodeMaxCols = 8 * kDecodeMaxGroup;     // columns per KV head
 // pass 1 scores up to this many groups of a KV head in one workgroup
-constexpr int kDecodeMaxSub = 4;
+constexpr int kDecodeMaxSub = 8;
+// Past 8 rows or 64 columns (up to 16 rows, 128 columns) the few-rows decode
+// beats the split causal kernel only while its groups times the visible keys
+// stay small: 16/2 heads at D = 256, 9 and 16 rows after 32K 110 -> 49 and 114
+// -> 66 us, 9 rows after 128K (5 groups) 204 -> 162 us, but 16 rows after 128K
+// (8 groups) 218 -> 235 us; 32/4 heads at D = 128, 9 and 16 rows after 8K 57
+// -> 43 and 60 -> 40 us, but 9 rows after 32K 84 -> 102 us.
+inline bool decode_wide_ok_n(int d, int rows, int cols, int sub, uint64_t n)
+{
+    if (rows <= 8 && cols <= 4 * kDecodeMaxGroup) return true;
+    const uint64_t budget = d == 256 ? uint64_t{768} << 10 : uint64_t{64} << 10;
+    return static_cast<uint64_t>(sub) * n <= budget;
+}
 // Whether pass 1 of a Chained decode call on the tuned head dimensions takes
 // all of a KV head's groups in each workgroup (its grid then has no group
 // axis): 2 to kDecodeMaxSub groups, where a tile per wave of these workgroups

@@ -177,8 +177,9 @@ typedef struct hsdpa_route {
 hsdpa_status hsdpa_attention_route(const hsdpa_plan *plan, uint64_t rows, uint64_t past, hsdpa_route *out);
 
 /* The whole attention node: every query head of every row, the decode kernels
- * when rows == 1 (and for up to 8 rows at head_dim 64, 128 and 256 while
- * rows * gqa <= 64), causal prefill otherwise, enqueued on `stream` (a hipStream_t;
+ * when rows == 1 (and for up to 16 rows at head_dim 64, 128 and 256 while
+ * rows * gqa <= 128, past 8 rows or 64 columns only over short enough caches),
+ * causal prefill otherwise, enqueued on `stream` (a hipStream_t;
  * NULL is the default stream). Validation happens on the host before any
  * launch; nothing is allocated. HSDPA_ERR_HIP after a launch was enqueued
  * leaves the output rows unspecified. */

@@ -155,9 +155,22 @@ def test_route_names_the_kernels():
     # ...and keeps the causal kernel (and the Chained numerics) at the others
     r = hsdpa.Plan(17, 17, 96, 100, form="fused").route(1, 10)
     assert r["main"] == "causal" and r["main_form"] == "chained"
-    # one row per decode where the tail does not fit the decode columns
-    r = hsdpa.Plan(32, 16, 128, 1000, form="fused").route(13, 100)
+    # one row per decode where the tail does not fit the decode columns (5 rows
+    # of 32 heads: 160 columns, past 128)
+    r = hsdpa.Plan(64, 32, 128, 1000, form="fused").route(13, 100)
     assert r["tail"] == "decode_rows" and r["tail_form"] == "fused" and r["launches"] == 1 + 5 * 3
+    # up to 16 rows within 128 columns take the few-rows kernels together
+    r = hsdpa.Plan(32, 16, 128, 1000, form="fused").route(13, 100)
+    assert r["main"] == "few_rows" and r["tail"] == "few_rows" and r["tail_form"] == "fused"
+    assert hsdpa.Plan(16, 8, 256, 40000).route(16, 30000)["main"] == "few_rows"
+    assert hsdpa.Plan(16, 8, 256, 40000).route(17, 30000)["main"] != "few_rows"
+    # past 8 rows or 64 columns only while groups x keys stay within the bound:
+    # 8 groups x 128K keys at D 256, 8 groups x 32K keys at D 128 go causal
+    assert hsdpa.Plan(16, 8, 256, 140000).route(16, 131000)["main"] == "causal_split"
+    assert hsdpa.Plan(16, 8, 256, 140000).route(9, 131000)["main"] == "few_rows"
+    assert hsdpa.Plan(32, 8, 128, 40000).route(16, 32000)["main"] == "causal_split"
+    assert hsdpa.Plan(32, 8, 128, 40000).route(16, 6000)["main"] == "few_rows"
+    assert hsdpa.Plan(32, 8, 128, 40000).route(8, 32000)["main"] == "few_rows"
 
 
 def _call(plan, rows=1, past=0, scale=0.0625, sink=0.0, ws_bytes=None, q=0x10000, k=0x20000, v=0x30000,

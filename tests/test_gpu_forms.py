@@ -55,8 +55,10 @@ FUSED = [
     ("fused_prefill_r13_p100", 16, 2, 256, 13, 100, ("few_rows", "chained"), ("few_rows", "fused")),
     ("fused_prefill_r300_p9000", 16, 2, 256, 300, 9000, ("causal_split", "chained"), ("few_rows", "fused")),
     ("fused_prefill_r70_p5_d128", 8, 8, 128, 70, 5, ("causal", "chained"), ("few_rows", "fused")),
-    ("fused_prefill_r9_g16", 32, 2, 128, 9, 50, ("causal", "chained"), ("decode", "fused")),
-    ("fused_prefill_r13_g16", 32, 2, 128, 13, 100, ("causal", "chained"), ("decode_rows", "fused")),
+    ("fused_prefill_r9_g16", 32, 2, 128, 9, 50, ("few_rows", "chained"), ("decode", "fused")),
+    ("fused_prefill_r13_g16", 32, 2, 128, 13, 100, ("few_rows", "chained"), ("few_rows", "fused")),
+    ("fused_prefill_r9_g32", 64, 2, 128, 9, 50, ("causal", "chained"), ("decode", "fused")),
+    ("fused_prefill_r13_g32", 64, 2, 128, 13, 100, ("causal", "chained"), ("decode_rows", "fused")),
     # padded groups (a group size with no equal split into groups of at most 16)
     ("fused_d128_g17_padded", 17, 1, 128, 1, 900, ("decode", "fused"), None),
     ("fused_d256_g17_padded_2kv_long", 34, 2, 256, 1, 40000, ("decode", "fused"), None),

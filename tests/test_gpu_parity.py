@@ -25,7 +25,7 @@ SMALL = [
     ("decode_direct_d64_n33_g8", 8, 1, 64, 1, 32, "decode"),
     ("decode_direct_d128_n32_g1", 4, 4, 128, 1, 31, "decode"),
     ("decode_direct_d256_n700_g3_kv5", 15, 5, 256, 1, 699, "decode"),
-    ("prefill_d256_r2_g40", 80, 2, 256, 2, 0, "causal"),              # 80 columns: past the decode kernels
+    ("prefill_d256_r2_g80", 160, 2, 256, 2, 0, "causal"),             # 160 columns: past the decode kernels
     ("prefill_d256_r19_p37", 8, 2, 256, 19, 37, "causal"),
     ("prefill_d128_r70_p5", 8, 8, 128, 70, 5, "causal"),
     ("prefill_d64_r33_p100_g2", 8, 4, 64, 33, 100, "causal"),
@@ -107,7 +107,7 @@ FEW = [
     ("few_r2_d256_g16_p2000", 32, 2, 256, 2, 2000),
     ("few_r4_d128_g4_p0", 8, 2, 128, 4, 0),                # row r sees keys 0..r only
     ("few_r7_d256_g8_p0", 16, 2, 256, 7, 0),
-    ("few_r8_d128_g16_causal_kernel", 32, 2, 128, 8, 500),  # 128 columns
+    ("few_r8_d128_g16_p500", 32, 2, 128, 8, 500),           # 128 columns: 8 groups
     ("few_r2_d128_g32_p700", 32, 1, 128, 2, 700),          # 64 columns: four groups of 16
     ("few_r5_d256_g3_p333", 6, 2, 256, 5, 333),            # 15 columns: one group, two P blocks
     # pass 1 scoring every group of a KV head in one workgroup (more than one
@@ -115,6 +115,14 @@ FEW = [
     # three tiles per wave at D 128
     ("few_r8_d256_g8_p20000", 16, 2, 256, 8, 20000),
     ("few_r4_d128_g8_p33000", 16, 2, 128, 4, 33000),
+    # 9 to 16 rows: up to 8 groups of 16 columns (the last one padded), all
+    # groups per workgroup over long caches, one workgroup per group otherwise
+    # (within the groups x keys bound past 8 rows or 64 columns)
+    ("few_r12_d256_g8_p20000", 16, 2, 256, 12, 20000),
+    ("few_r16_d256_g8_p1500", 16, 2, 256, 16, 1500),
+    ("few_r9_d64_g8_p700", 16, 2, 64, 9, 700),
+    ("few_r16_d128_g8_p6000", 16, 2, 128, 16, 6000),
+    ("few_r11_d128_g4_p0", 16, 4, 128, 11, 0),             # 44 columns, row r sees keys 0..r
     # long caches at D 64 and 128: pass 2 in chunks
     ("few_r4_d128_g8_p40000_chunked", 16, 2, 128, 4, 40000),
     ("few_r2_d128_g8_p70000_chunked", 16, 2, 128, 2, 70000),
