@@ -27,8 +27,8 @@ timed under the reference's Fused form ("configs_fused").
 
 Also timed: the whole attention chain of a gated Qwen3.5 layer (q/k norm and
 RoPE, KV append, attention, output gate) fused into one call against the same
-nodes called one by one; the decode at 1K, 8K, 32K and 128K keys; and 2, 4 and
-8 rows after the 32K cache (`--no-sweep` skips these two).
+nodes called one by one; the decode at 1K, 8K, 32K and 128K keys; and 2, 4, 8
+and 16 rows after the 32K cache (`--no-sweep` skips these two).
 """
 from __future__ import annotations
 
@@ -441,7 +441,7 @@ def main():
         # a few rows after the 32K cache (speculative verification): (row, head)
         # columns on the decode kernels
         few = {}
-        for rows in (2, 4, 8):
+        for rows in (2, 4, 8, 16):
             wf = W.make(f"few_{rows}", heads=16, kv_heads=2, head_dim=256, rows=rows, past=32768 - rows, seed=3)
             q, ks, vs, out = device_buffers(torch, wf, copies=16)
             plan_f = hsdpa.Plan(wf.heads, wf.gqa, wf.head_dim, wf.capacity)
