@@ -2366,6 +2366,16 @@ __global__ __launch_bounds__(64 * NW, 1) void prefill_split_pv(PrefillArgs a, Sp
 // grid (rows with partials, heads), D threads: one output element each.
 template <int D>
 __global__ __launch_bounds__(D) void prefill_split_combine(PrefillArgs a, SplitArgs sp, int splits);
+// The wide combine's shape: DL lanes of 4 dimensions each, SUBS subsets of
+// the splits; it takes more than kCombineNarrowSplits splits (2 splits of the
+// paired form: 21.0 us with a thread per dimension, 35.6 us this way).
+template <int D> struct CombineShape {
+    static constexpr int DL = D / 4, SUBS = 256 / DL > 0 ? 256 / DL : 1, THREADS = DL * SUBS;
+};
+constexpr int kCombineNarrowSplits = 4;
+template <int D>
+__global__ __launch_bounds__(CombineShape<D>::THREADS) void prefill_split_combine_wide(PrefillArgs a, SplitArgs sp,
+                                                                                       int splits);
 
 // A positive power of two in [2^-20, 2^20]: scaling by it is exact for the
 // scores and for the folded exponential constants.
@@ -2394,7 +2404,10 @@ static hipError_t launch_prefill_split(const PrefillArgs &a, int heads, const Pr
         if (e == hipSuccess) e = launch(prefill_split_pv<D, HPW, false, NW>, gs, dim3(64 * NW), s, a, sp);
     }
     if (e != hipSuccess) return e;
-    return launch(prefill_split_combine<D>, dim3(static_cast<unsigned>(a.rows), heads), dim3(D), s, a, sp, splits);
+    const dim3 gc(static_cast<unsigned>(a.rows), heads);
+    return splits > kCombineNarrowSplits
+               ? launch(prefill_split_combine_wide<D>, gc, dim3(CombineShape<D>::THREADS), s, a, sp, splits)
+               : launch(prefill_split_combine<D>, gc, dim3(D), s, a, sp, splits);
 }
 
 // The paired form on the causal kernel's grid (row groups, head groups); pr
@@ -2430,6 +2443,73 @@ __global__ __launch_bounds__(D) void prefill_split_combine(PrefillArgs a, SplitA
     uint16_t ob = static_cast<uint16_t>(cvt_out(o / ls));
     if (a.gate) ob = gate_bf16(ob, a.gate[row * a.gate_row + head * D + dim]);
     a.out[row * a.out_row + head * D + dim] = ob;
+}
+
+// The combine for many splits (more than kCombineNarrowSplits).
+template <int D>
+__global__ __launch_bounds__(CombineShape<D>::THREADS) void prefill_split_combine_wide(PrefillArgs a, SplitArgs sp,
+                                                                                       int splits)
+{
+    // lane t of subset u: dimensions 4 t .. 4 t + 3 of the splits u, u + SUBS,
+    // .., B of them requested at a time; the subsets' sums then added in
+    // subset order (with at most SUBS splits, the plain split order). One
+    // 4-byte load per split in turn left too few bytes in flight: 128 splits
+    // of 17 rows after 32K keys (36 MB of partials) took 36.6 us.
+    constexpr int DL = CombineShape<D>::DL, SUBS = CombineShape<D>::SUBS, B = 8;
+    __shared__ float4 ored[SUBS][DL];
+    __shared__ float lred[SUBS];
+    const uint64_t row = sp.r0 + blockIdx.x, head = blockIdx.y;
+    const int t = static_cast<int>(threadIdx.x) % DL, u = static_cast<int>(threadIdx.x) / DL;
+    float o[4] = {0.0f, 0.0f, 0.0f, 0.0f}, ls = 0.0f;
+    for (int z0 = u; z0 < splits; z0 += SUBS * B) {
+        float4 xo[B];
+        float xl[B];
+#pragma unroll
+        for (int b = 0; b < B; b++) {
+            const int z = z0 + SUBS * b;
+            if (z < splits) {
+                const uint64_t cell = (static_cast<uint64_t>(z) * sp.srows + blockIdx.x) * sp.heads + head;
+                xo[b] = *reinterpret_cast<const float4 *>(sp.so + cell * D + 4 * t);
+                xl[b] = sp.sl[cell];
+            }
+        }
+#pragma unroll
+        for (int b = 0; b < B; b++)
+            if (z0 + SUBS * b < splits) {
+                o[0] += xo[b].x;
+                o[1] += xo[b].y;
+                o[2] += xo[b].z;
+                o[3] += xo[b].w;
+                ls += xl[b];
+            }
+    }
+    ored[u][t] = float4{o[0], o[1], o[2], o[3]};
+    if (t == 0) lred[u] = ls;
+    __syncthreads();
+    if (u != 0) return;
+    float4 sum = ored[0][t];
+    float L = lred[0];
+    for (int v = 1; v < SUBS; v++) {
+        const float4 x = ored[v][t];
+        sum.x += x.x;
+        sum.y += x.y;
+        sum.z += x.z;
+        sum.w += x.w;
+        L += lred[v];
+    }
+    const float sv[4] = {sum.x, sum.y, sum.z, sum.w};
+    uint16_t ob[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) ob[r] = static_cast<uint16_t>(cvt_out(sv[r] / L));
+    if (a.gate) {
+        const uint2 gw = *reinterpret_cast<const uint2 *>(a.gate + row * a.gate_row + head * D + 4 * t);
+        const uint16_t gv[4] = {static_cast<uint16_t>(gw.x), static_cast<uint16_t>(gw.x >> 16),
+                                static_cast<uint16_t>(gw.y), static_cast<uint16_t>(gw.y >> 16)};
+#pragma unroll
+        for (int r = 0; r < 4; r++) ob[r] = gate_bf16(ob[r], gv[r]);
+    }
+    *reinterpret_cast<uint2 *>(a.out + row * a.out_row + head * D + 4 * t) =
+        uint2{ob[0] | (static_cast<uint32_t>(ob[1]) << 16), ob[2] | (static_cast<uint32_t>(ob[3]) << 16)};
 }
 
 }  // namespace hsdpa
