@@ -1057,18 +1057,27 @@ __global__ __launch_bounds__(512, 1) void decode_pv_all(DecodeArgs a)
 // thread), the V slice to LDS, P.V with the 32-key tiles dealt to the 8 waves,
 // the waves' partial outputs summed in LDS in wave order, and
 // out = bf16(O / l), gated like the combine's. Grid (D / DS, kv_heads).
+// FUSED (the Fused form, as decode_pv's FUSED over one chunk of all the keys):
+// wave h takes head h's block maxima from pass 1, one 16-key block per lane,
+// their running maxima M_b by a prefix maximum (exact in any order), the
+// corrections P(M_{b-1} - M_b) and each block's product C_b of the later
+// blocks' corrections (left to right, from lane broadcasts); e = P(s - M_b) * C_b, and
+// out = bf16(O * fl(1/l)).
 // ---------------------------------------------------------------------------
-template <int D, int DS = kDirectSlice>
+template <int D, bool FUSED = false, int DS = kDirectSlice>
 __global__ __launch_bounds__(512, 1) void decode_direct(DecodeArgs a)
 {
     constexpr int W = 8, THREADS = 64 * W, DBS = DS / 16, NK = kDirectKeys, PS = NK + 8;
-    constexpr int R = NK / 256, CH = NK * DS / 8 / THREADS, NT = NK / kKeyTile;
+    constexpr int R = NK / 256, CH = NK * DS / 8 / THREADS, NT = NK / kKeyTile, NB = NK / 16;
     static_assert(D % DS == 0 && NK % 256 == 0 && CH * THREADS * 8 == NK * DS, "slices and rounds");
+    static_assert(!FUSED || NB == 64, "one block of 16 keys per lane of a wave");
     __shared__ __attribute__((aligned(16))) uint16_t vs[NK * DS];
     __shared__ __attribute__((aligned(16))) uint16_t pc[16 * PS];
     __shared__ float smax[8];
     __shared__ float lpart[W][8];
     __shared__ float ored[W][DBS][4][64];
+    constexpr int FB = FUSED ? 8 * NB : 1;
+    __shared__ float fmb[FB], fcf[FB];
     const int tid = threadIdx.x, wave = tid >> 6, l = tid & 63, j = l & 15, G = l >> 4;
     const int kvh = static_cast<int>(blockIdx.y), d0 = static_cast<int>(blockIdx.x) * DS;
     const uint64_t n = a.n;
@@ -1088,10 +1097,15 @@ __global__ __launch_bounds__(512, 1) void decode_direct(DecodeArgs a)
             sv[r][i] = src[key < n ? key : 0];
         }
     }
-    // wave h: head h's pass-1 maxima (nwg_qk <= NK / 128 <= 64 entries)
-    const float mxv = wave < g && l < a.nwg_qk
-                          ? a.wgmax[static_cast<uint64_t>(kvh * g + wave) * a.nwg_qk + l]
-                          : kNegInf;
+    // wave h: head h's pass-1 maxima (nwg_qk <= NK / 128 <= 64 entries), or
+    // (FUSED) its block maxima, one 16-key block per lane (blocks past the
+    // cache: -inf, leaving the running maximum as it is)
+    const int nbv = static_cast<int>((n + 15) / 16);
+    const float mxv = FUSED ? (wave < g && l < nbv ? a.bmax[static_cast<uint64_t>(kvh * g + wave) * a.nblk + l]
+                                                   : kNegInf)
+                            : (wave < g && l < a.nwg_qk
+                                   ? a.wgmax[static_cast<uint64_t>(kvh * g + wave) * a.nwg_qk + l]
+                                   : kNegInf);
     // the V slice: chunk c = tid + THREADS i is key c / (DS / 8), bytes
     // 16 (c % (DS / 8)).. of the slice; keys past the cache read row 0 and are
     // stored as zeros
@@ -1103,8 +1117,32 @@ __global__ __launch_bounds__(512, 1) void decode_direct(DecodeArgs a)
         vr[c] = load16(vbase + static_cast<uint64_t>(static_cast<uint64_t>(key) < n ? key : 0) * D + 8 * part);
     }
     __builtin_amdgcn_sched_barrier(0);                          // all loads issued first
-    const float m = group_max_hi(mxv, 64);
-    if (l == 63 && wave < g) smax[wave] = m;
+    if constexpr (FUSED) {
+        // running maxima: an inclusive prefix maximum over the wave's lanes
+        float mb = mxv;
+#pragma unroll
+        for (int off = 1; off < 64; off *= 2) {
+            const float o = __shfl_up(mb, off);
+            if (l >= off) mb = fmaxnn(mb, o);
+        }
+        const float mprev = __shfl_up(mb, 1);
+        const float cor = l > 0 ? exp_poly(mprev - mb) : 1.0f;
+        // C_l = the corrections of blocks l + 1 .. NB - 1 multiplied left to
+        // right, each broadcast from its lane in turn
+        float c = 1.0f;
+#pragma unroll
+        for (int k = 1; k < NB; k++) {
+            const float ck = lane_value(cor, k);
+            c = k > l ? c * ck : c;
+        }
+        if (wave < g) {
+            fmb[wave * NB + l] = mb;
+            fcf[wave * NB + l] = c;
+        }
+    } else {
+        const float m = group_max_hi(mxv, 64);
+        if (l == 63 && wave < g) smax[wave] = m;
+    }
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < 4; i++) {
@@ -1114,7 +1152,13 @@ __global__ __launch_bounds__(512, 1) void decode_direct(DecodeArgs a)
 #pragma unroll
         for (int r = 0; r < R; r++) {
             const int key = kb + 256 * r;
-            const float e = static_cast<uint64_t>(key) < n ? exp_poly(sv[r][i] - smax[h]) : 0.0f;
+            float e;
+            if constexpr (FUSED) {
+                const int fb = h * NB + key / 16;
+                e = static_cast<uint64_t>(key) < n ? exp_poly(sv[r][i] - fmb[fb]) * fcf[fb] : 0.0f;
+            } else {
+                e = static_cast<uint64_t>(key) < n ? exp_poly(sv[r][i] - smax[h]) : 0.0f;
+            }
             const uint32_t hb = bf16_rne(e);
             pc[h * PS + key] = static_cast<uint16_t>(hb);
             pc[(8 + h) * PS + key] = static_cast<uint16_t>(bf16_rne(e - __uint_as_float(hb << 16)));
@@ -1167,7 +1211,7 @@ __global__ __launch_bounds__(512, 1) void decode_direct(DecodeArgs a)
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 const float os = s[r] + __shfl_xor(s[r], 8);    // hi column + lo column
-                ob[r] = static_cast<uint16_t>(cvt_out(os / L));
+                ob[r] = static_cast<uint16_t>(cvt_out(FUSED ? os * (1.0f / L) : os / L));
             }
             if (j < 8 && j < g) {
                 const uint64_t at = static_cast<uint64_t>(kvh * g + j) * D + d0 + 16 * db + 4 * G;

@@ -34,6 +34,11 @@ static hipError_t fused_dm(const DecodeArgs &a, int kv_heads, hipStream_t s)
                    : a.keys_qk > 4 * kKeyTile  ? launch(decode_qk<D, true, MR, true>, gqk, dim3(256), s, a)
                                                : launch(decode_qk<D, false, MR, true>, gqk, dim3(256), s, a);
     if (e != hipSuccess) return e;
+    if (a.direct) {
+        // a short cache: pass 2 over every key writes the outputs (decode_direct_ok)
+        if constexpr (MR == 0) return launch(decode_direct<D, true>, dim3(D / kDirectSlice, kv_heads), dim3(512), s, a);
+        else return hipErrorInvalidValue;
+    }
     if (a.g <= 8) {
         if (a.keys_pv == 4 * kKeyTile) e = launch(decode_pv<D, 4, 1, false, MR, true>, gpv, dim3(256), s, a);
         else if (a.keys_pv <= kDecodeKeysPV) e = launch(decode_pv<D, 8, 1, false, MR, true>, gpv, dim3(512), s, a);

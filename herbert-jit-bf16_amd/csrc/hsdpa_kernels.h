@@ -213,7 +213,7 @@ inline bool decode_rows_ok(int d) { return d == 64 || d == 128 || d == 256; }
 // Short caches: pass 2 over every key in each workgroup, which writes the
 // outputs itself (no combine launch): one row, one group of at most 8 query
 // heads per KV head, at most kDirectKeys visible keys, the tuned head
-// dimensions, the Chained form.
+// dimensions, either form.
 constexpr int kDirectKeys = 1024;
 // dimensions per workgroup of that pass: 16, one MFMA block (twice the
 // workgroups of 32-dimension slices, 1024 keys on 8/2 heads at D = 256 10.96

@@ -121,7 +121,8 @@ def test_route_names_the_kernels():
     assert p.route(1, 1023)["launches"] == 2 and p.route(1, 0)["launches"] == 2
     assert p.route(1, 1024)["launches"] == 3
     assert hsdpa.Plan(32, 16, 256, 4096).route(1, 100)["launches"] == 3
-    assert hsdpa.Plan(16, 8, 256, 4096, form="fused").route(1, 100)["launches"] == 3
+    assert hsdpa.Plan(16, 8, 256, 4096, form="fused").route(1, 100)["launches"] == 2
+    assert hsdpa.Plan(16, 8, 256, 4096, form="fused").route(1, 1024)["launches"] == 3
     assert hsdpa.Plan(16, 8, 96, 4096).route(1, 100)["launches"] == 3
     r = p.route(4096, 8192)       # one round of row groups, the longest paired with the shortest
     assert r["main"] == "causal_paired" and r["launches"] == 3 and r["tail"] == "none"

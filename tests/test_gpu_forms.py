@@ -30,6 +30,8 @@ FUSED = [
     ("fused_d256_n15", 8, 2, 256, 1, 14, ("decode", "fused"), None),
     ("fused_d256_n17", 8, 2, 256, 1, 16, ("decode", "fused"), None),
     ("fused_d256_n300", 8, 2, 256, 1, 299, ("decode", "fused"), None),
+    # up to 1024 keys pass 2 takes every key and writes the outputs: 64 blocks
+    ("fused_d128_n1024_g8", 16, 2, 128, 1, 1023, ("decode", "fused"), None),
     ("fused_d128_n5000_g4", 16, 4, 128, 1, 4999, ("decode", "fused"), None),
     ("fused_d64_g1_n777", 4, 4, 64, 1, 776, ("decode", "fused"), None),
     ("fused_d32_n1000", 8, 2, 32, 1, 999, ("decode", "fused"), None),
