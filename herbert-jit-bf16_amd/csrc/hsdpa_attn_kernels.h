@@ -644,11 +644,11 @@ __global__ __launch_bounds__(64 * W, D > 256 ? 1 : 8 / W) void decode_pv(DecodeA
     __shared__ float lpart[W][kDecodeMaxGroup];
     __shared__ __attribute__((aligned(16))) float ored[PARTS > 1 ? (PARTS - 1) * WPP * NCB * DBW * 4 * 64 : 1];
     // FUSED: per (column, block of the chunk): block maximum, running maximum,
-    // correction, suffix product of the later corrections; per column: the
-    // chunk's and the workgroup's products
+    // product of the later blocks' corrections; per column: the chunk's and
+    // the workgroup's products
     constexpr int NB = KEYS / 16;
     constexpr int FN = FUSED ? kDecodeMaxGroup * NB : 1, FH = FUSED ? kDecodeMaxGroup : 1;
-    __shared__ float fbm[FN], fmb[FN], fcor[FN], fcf[FN], fx[FH], fxw[FH];
+    __shared__ float fbm[FN], fmb[FN], fcf[FN], fx[FH], fxw[FH];
     const DecodeIds<MR> id(a);
     if (MR == 2 && id.wg >= a.nwg_pv) return;              // grid padding
     const int kvh = MR == 2 ? static_cast<int>(blockIdx.y) * a.sub + id.z       // as in decode_qk
@@ -750,29 +750,39 @@ __global__ __launch_bounds__(64 * W, D > 256 ? 1 : 8 / W) void decode_pv(DecodeA
                 if ((l & 15) == 0) fbm[h * NB + key_e / 16] = x;
             }
             __syncthreads();
-            // (b) per (column, block): the running maximum M_b and the
-            //     correction P(M_{b-1} - M_b), M_{-1} the maximum entering the chunk
+            // (b) per (column, block), in the NB lanes of each column: the
+            //     running maximum M_b (a prefix maximum, exact in any order;
+            //     M_{-1} the maximum entering the chunk), the correction
+            //     P(M_{b-1} - M_b), and C_b = the product of the later blocks'
+            //     corrections, multiplied left to right from the column's lanes
+            //     (from LDS one after another these scans waited out a read
+            //     each); the chunk's product X rescales what came before it
             if (tid < a.g * NB) {
                 const int h = tid / NB, b = tid - h * NB;
-                float mp = smax[h];
-                for (int k = 0; k < b; k++) mp = fbm[h * NB + k] > mp ? fbm[h * NB + k] : mp;
-                const float mb = fbm[h * NB + b] > mp ? fbm[h * NB + b] : mp;
-                fmb[tid] = mb;
-                fcor[tid] = exp_poly(mp - mb);
-            }
-            __syncthreads();
-            // (c) C_b = the product of the later blocks' corrections; the
-            //     chunk's product X rescales what came before it
-            if (tid < a.g * NB) {
-                const int h = tid / NB, b = tid - h * NB;
+                const float m0 = smax[h];
+                float mb = fbm[tid] > m0 ? fbm[tid] : m0;
+#pragma unroll
+                for (int off = 1; off < NB; off *= 2) {
+                    const float o = __shfl_up(mb, off, NB);
+                    if (b >= off && o > mb) mb = o;
+                }
+                const float mprev = __shfl_up(mb, 1, NB);
+                const float mp = b > 0 ? mprev : m0;
+                const float cor = exp_poly(mp - mb);
                 float c = 1.0f;
-                for (int k = b + 1; k < NB; k++) c = c * fcor[h * NB + k];
+#pragma unroll
+                for (int k = 1; k < NB; k++) {
+                    const float ck = __shfl(cor, k, NB);
+                    c = k > b ? c * ck : c;
+                }
+                const float mlast = __shfl(mb, NB - 1, NB);
+                fmb[tid] = mb;
                 fcf[tid] = c;
                 if (b == 0) {
-                    const float x = fcor[h * NB] * c;
+                    const float x = cor * c;
                     fx[h] = x;
                     fxw[h] = c0 == j0 ? x : fxw[h] * x;
-                    smax[h] = fmb[h * NB + NB - 1];
+                    smax[h] = mlast;
                 }
             }
             __syncthreads();
