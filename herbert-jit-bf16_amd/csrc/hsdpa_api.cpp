@@ -369,7 +369,7 @@ DecodeCfg decode_cfg(const hsdpa_plan *p, uint64_t rows, uint64_t n, int sub, bo
     // takes them all too: each V tile loaded once instead of once per group
     c.pv_all = c.qk_all && c.keys_pv == hsdpa::kDecodeKeysPV && d == 256 ? 1 : 0;
     // a short cache: pass 2 writes the outputs itself, no combine launch
-    c.direct = hsdpa::decode_direct_ok(d, static_cast<int>(rows), sub, c.g, n) ? 1 : 0;
+    c.direct = hsdpa::decode_direct_ok(d, static_cast<int>(rows), sub, c.g, n, fused) ? 1 : 0;
     // several groups: a key range's groups on one XCD, whose L2 then serves
     // the later ones (a few rows: 3-8 rows after 32K 11-14 % faster; one row
     // where pass 2 takes several rounds of workgroups, not chunks: 48 heads on

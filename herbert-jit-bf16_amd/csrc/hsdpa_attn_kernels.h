@@ -1056,48 +1056,51 @@ __global__ __launch_bounds__(512, 1) void decode_pv_all(DecodeArgs a)
 }
 
 // ---------------------------------------------------------------------------
-// Decode pass 2 and the combine in one launch for short caches (one row, g <=
-// 8 query heads per KV head in one group, n <= kDirectKeys). Workgroup (s,
-// kvh) computes dimensions [DS s, DS s + DS) of the g outputs over all n keys
-// (DS = kDirectSlice). Every load is issued first: the g heads' scores and
-// pass-1 maxima, and the V slice (n rows of 2 DS bytes). Then the exact
-// maxima (wave h reduces head h's),
-// the g x n exponentials as P columns [hi of 8 heads | lo of 8 heads] in LDS
-// (as decode_pv; each slice's workgroup computes all of them, at most 16 per
-// thread), the V slice to LDS, P.V with the 32-key tiles dealt to the 8 waves,
-// the waves' partial outputs summed in LDS in wave order, and
-// out = bf16(O / l), gated like the combine's. Grid (D / DS, kv_heads).
-// FUSED (the Fused form, as decode_pv's FUSED over one chunk of all the keys):
-// wave h takes head h's block maxima from pass 1, one 16-key block per lane,
-// their running maxima M_b by a prefix maximum (exact in any order), the
-// corrections P(M_{b-1} - M_b) and each block's product C_b of the later
-// blocks' corrections (left to right, from lane broadcasts); e = P(s - M_b) * C_b, and
-// out = bf16(O * fl(1/l)).
+// Decode pass 2 and the combine in one launch for short caches (one group of
+// g <= 8 NCB columns per KV head: the query heads of one row, or MR the (row,
+// head) columns of a few rows, each with its row's causal limit; n <=
+// kDirectKeys). Workgroup (s, kvh) computes dimensions [DS s, DS s + DS) of
+// the g outputs over all n keys (DS = kDirectSlice). Every load is issued
+// first: the columns' scores and pass-1 maxima, and the V slice (n rows of 2 DS
+// bytes). Then the exact maxima (wave w reduces columns w and w + 8, 32 lanes
+// each), the g x n exponentials as P columns in LDS (as decode_pv: [hi of 8 |
+// lo of 8] for NCB = 1, a hi and a lo block of 16 for NCB = 2; each slice's
+// workgroup computes all of them), the V slice to LDS, P.V with the 32-key
+// tiles dealt to the 8 waves, the waves' partial outputs summed in LDS in wave
+// order, and out = bf16(O / l), gated like the combine's. Grid (D / DS,
+// kv_heads).
+// FUSED (the Fused form, one row, NCB = 1, as decode_pv's FUSED over one chunk
+// of all the keys): wave h takes head h's block maxima from pass 1, one 16-key
+// block per lane, their running maxima M_b by a prefix maximum (exact in any
+// order), the corrections P(M_{b-1} - M_b) and each block's product C_b of the
+// later blocks' corrections (left to right, from lane broadcasts);
+// e = P(s - M_b) * C_b, and out = bf16(O * fl(1/l)).
 // ---------------------------------------------------------------------------
-template <int D, bool FUSED = false, int DS = kDirectSlice>
+template <int D, bool FUSED = false, int NCB = 1, bool MR = false, int DS = kDirectSlice>
 __global__ __launch_bounds__(512, 1) void decode_direct(DecodeArgs a)
 {
     constexpr int W = 8, THREADS = 64 * W, DBS = DS / 16, NK = kDirectKeys, PS = NK + 8;
     constexpr int R = NK / 256, CH = NK * DS / 8 / THREADS, NT = NK / kKeyTile, NB = NK / 16;
+    constexpr int CM = 8 * NCB, HI = CM / 2;                     // columns; per thread parity
     static_assert(D % DS == 0 && NK % 256 == 0 && CH * THREADS * 8 == NK * DS, "slices and rounds");
-    static_assert(!FUSED || NB == 64, "one block of 16 keys per lane of a wave");
+    static_assert(!FUSED || (NB == 64 && NCB == 1 && !MR), "the Fused form: one row, one block of 16 keys per lane");
     __shared__ __attribute__((aligned(16))) uint16_t vs[NK * DS];
-    __shared__ __attribute__((aligned(16))) uint16_t pc[16 * PS];
-    __shared__ float smax[8];
-    __shared__ float lpart[W][8];
-    __shared__ float ored[W][DBS][4][64];
+    __shared__ __attribute__((aligned(16))) uint16_t pc[2 * CM * PS];
+    __shared__ float smax[CM];
+    __shared__ float lpart[W][CM];
+    __shared__ float ored[W][NCB][DBS][4][64];
     constexpr int FB = FUSED ? 8 * NB : 1;
     __shared__ float fmb[FB], fcf[FB];
     const int tid = threadIdx.x, wave = tid >> 6, l = tid & 63, j = l & 15, G = l >> 4;
     const int kvh = static_cast<int>(blockIdx.y), d0 = static_cast<int>(blockIdx.x) * DS;
     const uint64_t n = a.n;
     const int g = a.g;
-    // thread t: keys t % 256 + 256 r, heads t / 256 + 2 i (the same for a
-    // whole wave, so the head loops end alike in every lane)
+    // thread t: keys t % 256 + 256 r, columns t / 256 + 2 i (the same for a
+    // whole wave, so the column loops end alike in every lane)
     const int kb = tid % 256, hp = tid / 256;
-    float sv[R][4];
+    float sv[R][HI];
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
+    for (int i = 0; i < HI; i++) {
         const int h = hp + 2 * i;
         if (h >= g) break;
         const float *src = a.scores + static_cast<uint64_t>(kvh * g + h) * a.npad;
@@ -1107,14 +1110,16 @@ __global__ __launch_bounds__(512, 1) void decode_direct(DecodeArgs a)
             sv[r][i] = src[key < n ? key : 0];
         }
     }
-    // wave h: head h's pass-1 maxima (nwg_qk <= NK / 128 <= 64 entries), or
-    // (FUSED) its block maxima, one 16-key block per lane (blocks past the
-    // cache: -inf, leaving the running maximum as it is)
+    // the pass-1 maxima of column wave + 8 (l / 32), lane l % 32 taking entry
+    // l % 32 (nwg_qk <= NK / 128 <= 32), or (FUSED) head `wave`'s block maxima,
+    // one 16-key block per lane (blocks past the cache: -inf, leaving the
+    // running maximum as it is)
+    const int mcol = wave + 8 * (l >> 5), ml = l & 31;
     const int nbv = static_cast<int>((n + 15) / 16);
     const float mxv = FUSED ? (wave < g && l < nbv ? a.bmax[static_cast<uint64_t>(kvh * g + wave) * a.nblk + l]
                                                    : kNegInf)
-                            : (wave < g && l < a.nwg_qk
-                                   ? a.wgmax[static_cast<uint64_t>(kvh * g + wave) * a.nwg_qk + l]
+                            : (mcol < g && ml < a.nwg_qk
+                                   ? a.wgmax[static_cast<uint64_t>(kvh * g + mcol) * a.nwg_qk + ml]
                                    : kNegInf);
     // the V slice: chunk c = tid + THREADS i is key c / (DS / 8), bytes
     // 16 (c % (DS / 8)).. of the slice; keys past the cache read row 0 and are
@@ -1150,28 +1155,31 @@ __global__ __launch_bounds__(512, 1) void decode_direct(DecodeArgs a)
             fcf[wave * NB + l] = c;
         }
     } else {
-        const float m = group_max_hi(mxv, 64);
-        if (l == 63 && wave < g) smax[wave] = m;
+        const float m = group_max_hi(mxv, 32);
+        if (ml == 31 && mcol < g) smax[mcol] = m;
     }
     __syncthreads();
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
+    for (int i = 0; i < HI; i++) {
         const int h = hp + 2 * i;
         if (h >= g) break;
+        // column h's row sees keys [0, past + row] (one row: all n)
+        const uint64_t lim = MR ? a.past + static_cast<uint64_t>(h / a.G) + 1 : n;
         float le = 0.0f;
 #pragma unroll
         for (int r = 0; r < R; r++) {
             const int key = kb + 256 * r;
+            const bool vis = static_cast<uint64_t>(key) < n && static_cast<uint64_t>(key) < lim;
             float e;
             if constexpr (FUSED) {
                 const int fb = h * NB + key / 16;
-                e = static_cast<uint64_t>(key) < n ? exp_poly(sv[r][i] - fmb[fb]) * fcf[fb] : 0.0f;
+                e = vis ? exp_poly(sv[r][i] - fmb[fb]) * fcf[fb] : 0.0f;
             } else {
-                e = static_cast<uint64_t>(key) < n ? exp_poly(sv[r][i] - smax[h]) : 0.0f;
+                e = vis ? exp_poly(sv[r][i] - smax[h]) : 0.0f;
             }
             const uint32_t hb = bf16_rne(e);
             pc[h * PS + key] = static_cast<uint16_t>(hb);
-            pc[(8 + h) * PS + key] = static_cast<uint16_t>(bf16_rne(e - __uint_as_float(hb << 16)));
+            pc[(CM + h) * PS + key] = static_cast<uint16_t>(bf16_rne(e - __uint_as_float(hb << 16)));
             le += e;
         }
         const float sum = wave_sum_hi(le);
@@ -1185,50 +1193,65 @@ __global__ __launch_bounds__(512, 1) void decode_direct(DecodeArgs a)
     }
     __syncthreads();
     // O^T = V^T . P^T over the tiles t = wave, wave + 8, ..; lane (j, G)
-    // holds column j (hi of head j, lo of head j - 8), dimensions 4 G .. 4 G + 3
-    // of each 16-dimension block
+    // holds P column j of each block (NCB = 1: hi of column j, lo of column
+    // j - 8; NCB = 2: block 0 hi, block 1 lo of column j), dimensions
+    // 4 G .. 4 G + 3 of each 16-dimension block
     const int nt = static_cast<int>((n + kKeyTile - 1) / kKeyTile);
-    f32x4 o[DBS] = {};
+    f32x4 o[NCB][DBS] = {};
 #pragma unroll
     for (int k = 0; k < NT / W; k++) {
         const int t = wave + W * k;
         if (t < nt) {
-            const u32x4 bp = load16(pc + j * PS + kKeyTile * t + 8 * G);
+            u32x4 bp[NCB];
 #pragma unroll
-            for (int db = 0; db < DBS; db++)
-                o[db] = mfma16(vt16_operand<DS>(vs + t * (kKeyTile * DS), 16 * db, l), bp, o[db]);
+            for (int c = 0; c < NCB; c++) bp[c] = load16(pc + (16 * c + j) * PS + kKeyTile * t + 8 * G);
+#pragma unroll
+            for (int db = 0; db < DBS; db++) {
+                const u32x4 av = vt16_operand<DS>(vs + t * (kKeyTile * DS), 16 * db, l);
+#pragma unroll
+                for (int c = 0; c < NCB; c++) o[c][db] = mfma16(av, bp[c], o[c][db]);
+            }
         }
     }
 #pragma unroll
-    for (int db = 0; db < DBS; db++)
+    for (int c = 0; c < NCB; c++)
 #pragma unroll
-        for (int r = 0; r < 4; r++) ored[wave][db][r][l] = o[db][r];
+        for (int db = 0; db < DBS; db++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) ored[wave][c][db][r][l] = o[c][db][r];
     __syncthreads();
     if (wave == 0) {
-        const int h = j & 7;
+        const int h = NCB == 1 ? (j & 7) : j;                   // this lane's column
+        const int hc = h < g ? h : 0;
         float L = 0.0f;
-        // heads of parity p were summed by waves 4 p .. 4 p + 3
+        // columns of parity p were summed by waves 4 p .. 4 p + 3
 #pragma unroll
-        for (int w = 0; w < 4; w++) L += lpart[4 * (h & 1) + w][h < g ? h : 0];
+        for (int w = 0; w < 4; w++) L += lpart[4 * (hc & 1) + w][hc];
+        // the column's (row, head) and where its output goes
+        const int row = MR ? hc / a.G : 0, head = kvh * a.G + hc - row * a.G;
+        const uint64_t obase = static_cast<uint64_t>(row) * a.out_row + static_cast<uint64_t>(head) * D + d0 + 4 * G;
+        const uint64_t gbase = static_cast<uint64_t>(row) * a.gate_row + static_cast<uint64_t>(head) * D + d0 + 4 * G;
 #pragma unroll
         for (int db = 0; db < DBS; db++) {
-            f32x4 s = {};
+            f32x4 sum[NCB] = {};
 #pragma unroll
             for (int w = 0; w < W; w++)
 #pragma unroll
-                for (int r = 0; r < 4; r++) s[r] += ored[w][db][r][l];
+                for (int c = 0; c < NCB; c++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++) sum[c][r] += ored[w][c][db][r][l];
             uint16_t ob[4];
 #pragma unroll
             for (int r = 0; r < 4; r++) {
-                const float os = s[r] + __shfl_xor(s[r], 8);    // hi column + lo column
+                // hi column + lo column
+                const float os = NCB == 1 ? sum[0][r] + __shfl_xor(sum[0][r], 8) : sum[0][r] + sum[NCB - 1][r];
                 ob[r] = static_cast<uint16_t>(cvt_out(FUSED ? os * (1.0f / L) : os / L));
             }
-            if (j < 8 && j < g) {
-                const uint64_t at = static_cast<uint64_t>(kvh * g + j) * D + d0 + 16 * db + 4 * G;
+            if (j < CM && h < g) {
 #pragma unroll
                 for (int r = 0; r < 4; r++) {
-                    if (a.gate) ob[r] = gate_bf16(ob[r], a.gate[at + r]);
-                    a.out[at + r] = ob[r];
+                    if (a.gate) ob[r] = gate_bf16(ob[r], a.gate[gbase + 16 * db + r]);
+                    a.out[obase + 16 * db + r] = ob[r];
                 }
             }
         }

@@ -36,7 +36,8 @@ static hipError_t fused_dm(const DecodeArgs &a, int kv_heads, hipStream_t s)
     if (e != hipSuccess) return e;
     if (a.direct) {
         // a short cache: pass 2 over every key writes the outputs (decode_direct_ok)
-        if constexpr (MR == 0) return launch(decode_direct<D, true>, dim3(D / kDirectSlice, kv_heads), dim3(512), s, a);
+        if constexpr (MR == 0)
+            return launch(decode_direct<D, true, 1, false>, dim3(D / kDirectSlice, kv_heads), dim3(512), s, a);
         else return hipErrorInvalidValue;
     }
     if (a.g <= 8) {

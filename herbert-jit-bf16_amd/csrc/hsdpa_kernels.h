@@ -211,17 +211,24 @@ inline bool decode_qk_groups(int sub, uint64_t kv_wgs, uint64_t cus)
 }
 inline bool decode_rows_ok(int d) { return d == 64 || d == 128 || d == 256; }
 // Short caches: pass 2 over every key in each workgroup, which writes the
-// outputs itself (no combine launch): one row, one group of at most 8 query
-// heads per KV head, at most kDirectKeys visible keys, the tuned head
-// dimensions, either form.
+// outputs itself (no combine launch): one group of at most 16 columns per KV
+// head (the query heads of one row, or the (row, head) columns of a few rows;
+// under the Fused form one row of at most 8 heads), at most kDirectKeys
+// visible keys, the tuned head dimensions. Past 8 columns (two P column
+// blocks) only while columns x keys <= kDirectWideWork: each workgroup
+// computes every column's exponentials (16 heads at 256 keys 11.97 -> 11.36
+// us, 3 rows of 4 heads after 100 keys 12.39 -> 11.17; 16 heads at 1024 keys
+// 12.86 -> 13.82, 4 rows of 4 heads after 500 keys at D = 128 11.65 -> 12.34).
 constexpr int kDirectKeys = 1024;
+constexpr uint64_t kDirectWideWork = 4096;
 // dimensions per workgroup of that pass: 16, one MFMA block (twice the
 // workgroups of 32-dimension slices, 1024 keys on 8/2 heads at D = 256 10.96
 // -> 9.95 us)
 constexpr int kDirectSlice = 16;
-inline bool decode_direct_ok(int d, int rows, int sub, int g, uint64_t n)
+inline bool decode_direct_ok(int d, int rows, int sub, int g, uint64_t n, bool fused)
 {
-    return decode_rows_ok(d) && rows == 1 && sub == 1 && g <= 8 && n <= static_cast<uint64_t>(kDirectKeys);
+    return decode_rows_ok(d) && sub == 1 && n <= static_cast<uint64_t>(kDirectKeys) &&
+           (fused ? rows == 1 && g <= 8 : g <= 8 || static_cast<uint64_t>(g) * n <= kDirectWideWork);
 }
 
 // Pass 2 in chunks (one round of workgroups over a long cache) is built for

@@ -305,9 +305,15 @@ static hipError_t decode_dm(const DecodeArgs &a, int kv_heads, hipStream_t s)
     }
     if (e != hipSuccess) return e;
     if (a.direct) {
-        // a short cache: pass 2 writes the outputs (decode_direct_ok)
-        if constexpr (MR == 0) return launch(decode_direct<D>, dim3(D / kDirectSlice, kv_heads), dim3(512), s, a);
-        else return hipErrorInvalidValue;
+        // a short cache: pass 2 writes the outputs (decode_direct_ok); one
+        // group, so never the XCD numbering
+        if constexpr (MR == 2) {
+            return hipErrorInvalidValue;
+        } else {
+            const dim3 grid(D / kDirectSlice, kv_heads);
+            return a.g <= 8 ? launch(decode_direct<D, false, 1, MR == 1>, grid, dim3(512), s, a)
+                            : launch(decode_direct<D, false, 2, MR == 1>, grid, dim3(512), s, a);
+        }
     }
     if (a.pv_all) {
         // pass 2 over all the KV head's groups in one workgroup

@@ -120,7 +120,11 @@ def test_route_names_the_kernels():
     # per KV head, three
     assert p.route(1, 1023)["launches"] == 2 and p.route(1, 0)["launches"] == 2
     assert p.route(1, 1024)["launches"] == 3
-    assert hsdpa.Plan(32, 16, 256, 4096).route(1, 100)["launches"] == 3
+    assert hsdpa.Plan(32, 16, 256, 4096).route(1, 100)["launches"] == 2       # 16 heads: two P blocks
+    assert hsdpa.Plan(64, 32, 256, 4096).route(1, 100)["launches"] == 3       # two groups
+    assert hsdpa.Plan(16, 8, 256, 4096).route(2, 100)["launches"] == 2        # 2 rows: 16 (row, head) columns
+    assert hsdpa.Plan(16, 8, 256, 4096).route(3, 100)["launches"] == 3
+    assert hsdpa.Plan(32, 16, 256, 4096).route(1, 1000)["launches"] == 3      # 16 columns x 1001 keys
     assert hsdpa.Plan(16, 8, 256, 4096, form="fused").route(1, 100)["launches"] == 2
     assert hsdpa.Plan(16, 8, 256, 4096, form="fused").route(1, 1024)["launches"] == 3
     assert hsdpa.Plan(16, 8, 96, 4096).route(1, 100)["launches"] == 3

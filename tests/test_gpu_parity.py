@@ -25,6 +25,8 @@ SMALL = [
     ("decode_direct_d64_n33_g8", 8, 1, 64, 1, 32, "decode"),
     ("decode_direct_d128_n32_g1", 4, 4, 128, 1, 31, "decode"),
     ("decode_direct_d256_n700_g3_kv5", 15, 5, 256, 1, 699, "decode"),
+    ("decode_direct_d256_g16_n200", 32, 2, 256, 1, 199, "decode"),               # two P column blocks
+    ("decode_direct_d128_g12_n300", 12, 1, 128, 1, 299, "decode"),
     ("prefill_d256_r2_g80", 160, 2, 256, 2, 0, "causal"),             # 160 columns: past the decode kernels
     ("prefill_d256_r19_p37", 8, 2, 256, 19, 37, "causal"),
     ("prefill_d128_r70_p5", 8, 8, 128, 70, 5, "causal"),
@@ -123,6 +125,11 @@ FEW = [
     ("few_r9_d64_g8_p700", 16, 2, 64, 9, 700),
     ("few_r16_d128_g8_p6000", 16, 2, 128, 16, 6000),
     ("few_r11_d128_g4_p0", 16, 4, 128, 11, 0),             # 44 columns, row r sees keys 0..r
+    # up to 16 columns after a short cache: one launch for pass 2 and the outputs
+    ("few_r2_d256_g8_p200_direct", 16, 2, 256, 2, 200),
+    ("few_r3_d128_g4_p0_direct", 16, 4, 128, 3, 0),
+    ("few_r2_d64_g8_p150_direct", 16, 2, 64, 2, 150),
+    ("few_r2_d128_g4_p900_direct", 8, 2, 128, 2, 900),      # 8 columns: one P block, 902 keys
     # long caches at D 64 and 128: pass 2 in chunks
     ("few_r4_d128_g8_p40000_chunked", 16, 2, 128, 4, 40000),
     ("few_r2_d128_g8_p70000_chunked", 16, 2, 128, 2, 70000),
