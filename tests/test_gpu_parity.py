@@ -121,6 +121,8 @@ FEW = [
     # groups per workgroup over long caches, one workgroup per group otherwise
     # (within the groups x keys bound past 8 rows or 64 columns)
     ("few_r12_d256_g8_p20000", 16, 2, 256, 12, 20000),
+    ("few_r14_d256_g8_p20000", 16, 2, 256, 14, 20000),     # 7 groups
+    ("few_r16_d256_g8_p24000", 16, 2, 256, 16, 24000),     # 8 groups
     ("few_r16_d256_g8_p1500", 16, 2, 256, 16, 1500),
     ("few_r9_d64_g8_p700", 16, 2, 64, 9, 700),
     ("few_r16_d128_g8_p6000", 16, 2, 128, 16, 6000),
