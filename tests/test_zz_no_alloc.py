@@ -43,6 +43,7 @@ CASES = [
     # name, plan (heads, gqa, head_dim, capacity, form, max_rows), first call (rows, past), second call
     ("decode_32k_then_1k", (16, 8, 256, 32768, "chained", 1), (1, 32767), (1, 1023)),
     ("fused_decode_40k_then_5k", (16, 8, 256, 40001, "fused", 1), (1, 40000), (1, 4999)),
+    ("fused_decode_3k_then_500", (16, 8, 256, 3000, "fused", 1), (1, 2999), (1, 499)),
     ("few_rows_d128_then_decode", (16, 8, 128, 20000, "chained", 4), (4, 19996), (1, 700)),
     ("split_prefill_d64_then_decode", (8, 2, 64, 4096, "chained", 0), (64, 3000), (1, 300)),
 ]
