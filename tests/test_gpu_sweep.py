@@ -3,7 +3,8 @@
 The named cases elsewhere pin each kernel at the shapes chosen for it; this
 sweep draws 80 calls at random (fixed seed) over group shapes (1 to 80 query
 heads per KV head), every kind of head_dim the reference accepts (32 to 512),
-1 to 512 rows after 0 to 12 000 cached positions, and both decode forms
+1 to 512 rows after 0 to 12 000 cached positions, and 24 more of up to 8 rows
+after 12 000 to 131 071 positions, under both decode forms
 (sdpa_form Chained and Fused, src/jit/target/x86/emit_sdpa/x86/decode.rs:
 212-293 and 501-669), so that routing and kernel choices meet shapes nobody
 picked. The host test checks, without a GPU, that the draw still reaches
@@ -47,6 +48,31 @@ def _draw():
 
 CASES = _draw()
 
+# long caches: 12 000 to 131 071 positions, up to 8 rows (the decode and
+# few-rows kernels' tile loops, chunked pass 2 and all-group forms)
+LONG_DIMS = [64, 128, 256, 256, 96, 512]
+LONG_ROWS = [1, 1, 1, 2, 3, 4, 5, 8]
+LONG_COUNT = 24
+LONG_MAX_WORK = 6e8
+
+
+def _draw_long():
+    rng = np.random.default_rng(SEED + 1)
+    out = []
+    while len(out) < LONG_COUNT:
+        h, kvh = GROUPS[rng.integers(len(GROUPS))]
+        d = int(LONG_DIMS[rng.integers(len(LONG_DIMS))])
+        rows = int(LONG_ROWS[rng.integers(len(LONG_ROWS))])
+        past = int(rng.integers(12000, 131072))
+        form = "fused" if rng.random() < 0.3 else "chained"
+        if rows * (past + rows) * h * d > LONG_MAX_WORK:
+            continue
+        out.append((f"l{len(out):02d}_h{h}k{kvh}_d{d}_r{rows}_p{past}_{form}", h, kvh, d, rows, past, form))
+    return out
+
+
+LONG_CASES = _draw_long()
+
 # (main kernels, main numerics, tail kernels, launches, split over keys) that
 # the draw reaches
 REACHED = {
@@ -67,6 +93,13 @@ REACHED = {
     ("few_rows", "chained", "none", 3, False),
     ("few_rows", "fused", "none", 3, False),
 }
+REACHED_LONG = {
+    ("causal_split", "chained", "none", 3, True),
+    ("decode", "chained", "none", 3, False),
+    ("decode", "fused", "none", 3, False),
+    ("few_rows", "chained", "none", 3, False),
+    ("few_rows", "fused", "none", 3, False),
+}
 
 
 def _plan(h, kvh, d, rows, past, form):
@@ -77,22 +110,24 @@ def _route_class(r):
     return (r["main"], r["main_form"], r["tail"], r["launches"], r["splits"] > 1)
 
 
-def test_sweep_reaches_every_route_class():
+@pytest.mark.parametrize("cases,reached", [(CASES, REACHED), (LONG_CASES, REACHED_LONG)], ids=["short", "long"])
+def test_sweep_reaches_every_route_class(cases, reached):
     seen = set()
-    for _, h, kvh, d, rows, past, form in CASES:
+    for _, h, kvh, d, rows, past, form in cases:
         seen.add(_route_class(_plan(h, kvh, d, rows, past, form).route(rows, past)))
-    assert REACHED <= seen, sorted(REACHED - seen)
+    assert reached <= seen, sorted(reached - seen)
 
 
 @pytest.mark.gpu
-def test_sweep_parity(torch_cuda):
+@pytest.mark.parametrize("cases,seed0", [(CASES, 31), (LONG_CASES, 131)], ids=["short", "long"])
+def test_sweep_parity(torch_cuda, cases, seed0):
     """Each call: no NaN, the per-row bound max |out - ref| <= 2^-6 max |V|,
     and at most max(2, 1 %) of its outputs past one ulp (a call of 128
     outputs cannot show a 99.9 % share, a wrong kernel misses by far more);
-    over the 80 calls together at least 99.9 % of outputs within one ulp."""
+    over the calls together at least 99.9 % of outputs within one ulp."""
     within = total = 0
-    for i, (name, h, kvh, d, rows, past, form) in enumerate(CASES):
-        w = W.make(name, heads=h, kv_heads=kvh, head_dim=d, rows=rows, past=past, seed=31 + i)
+    for i, (name, h, kvh, d, rows, past, form) in enumerate(cases):
+        w = W.make(name, heads=h, kv_heads=kvh, head_dim=d, rows=rows, past=past, seed=seed0 + i)
         plan = _plan(h, kvh, d, rows, past, form)
         print(f"case {name} route {_route_class(plan.route(rows, past))}", flush=True)
         out = run_hsdpa(w, plan)
