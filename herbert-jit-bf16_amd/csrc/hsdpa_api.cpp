@@ -297,6 +297,26 @@ int decode_sub(const hsdpa_plan *p, uint64_t rows, uint64_t n)
     return sub;
 }
 
+// Query heads per KV head beyond which a Fused plan is refused: its rows
+// would need more padded groups than one grid's z dimension holds.
+constexpr uint64_t kFusedMaxGqa = uint64_t{4096} * hsdpa::kDecodeMaxGroup;
+
+// The groups of one row under the Fused form (head_dim <= 256). The reference
+// serves such a row with its Fused head whatever its shape
+// (src/jit/sdpa.rs:491-510), so it always takes the decode kernels, which
+// compute the Fused weights: where decode_sub would send it to the causal
+// kernels (Chained numerics) -- a group size with no equal split at the head
+// dimensions other than 64, 128 and 256, more than 16 padded groups, or padded
+// groups over a cache longer than decode_wide_ok_n allows -- it takes
+// ceil(g / 16) padded groups on the kernels that map each column to its
+// (row, head) pair. n = 0: any n.
+int fused_row_sub(const hsdpa_plan *p, uint64_t n)
+{
+    const int sub = decode_sub(p, 1, n);
+    if (sub) return sub;
+    return static_cast<int>((p->spec.gqa + hsdpa::kDecodeMaxGroup - 1) / hsdpa::kDecodeMaxGroup);
+}
+
 // The decode passes' grids for `rows` rows over n visible keys (decode_sub
 // already > 0).
 DecodeCfg decode_cfg(const hsdpa_plan *p, uint64_t rows, uint64_t n, int sub, bool fused)
@@ -376,6 +396,8 @@ DecodeCfg decode_cfg(const hsdpa_plan *p, uint64_t rows, uint64_t n, int sub, bo
     // 2 KV heads at 128K, 126 -> 109 us; with chunks, or in one round, the
     // plain grid is faster)
     c.xcd = sub > 1 && (rows > 1 || (c.keys_pv <= hsdpa::kDecodeKeysPV && groups * nch > cu1)) ? 1 : 0;
+    // the other head dimensions' launchers number the groups on the plain grid
+    if (!hsdpa::decode_rows_ok(d)) c.xcd = 0;
     return c;
 }
 
@@ -399,16 +421,19 @@ uint64_t decode_nwg_pv_max(const hsdpa_plan *p, uint64_t rows, int sub)
     return one_round;
 }
 
-// Whether a call of `rows` rows can reach the causal kernels.
-bool reaches_causal(const hsdpa_plan *p, uint64_t rows)
-{
-    return decode_sub(p, rows, std::max<uint64_t>(p->spec.kv_capacity, rows)) == 0;
-}
-
 // The Fused form's rows outside full chunks of 8: the last rows % 8 (the
 // reference's passes of 256 rows are multiples of 8, so only the last pass
 // ends on a partial chunk), all rows of a call shorter than 8.
 uint64_t fused_tail(uint64_t rows) { return rows < 8 ? rows : rows % 8; }
+
+// Whether a call of `rows` rows can reach the causal kernels: under the Fused
+// form only its rows in full chunks of 8 can (the others take the decode
+// kernels, fused_row_sub).
+bool reaches_causal(const hsdpa_plan *p, uint64_t rows)
+{
+    if (p->form == HSDPA_FORM_FUSED) rows -= fused_tail(rows);
+    return rows > 0 && decode_sub(p, rows, std::max<uint64_t>(p->spec.kv_capacity, rows)) == 0;
+}
 
 // One sub-call of the node: rows [row0, row0 + rows) of the call, their
 // numerics (Fused or Chained) and their kernels.
@@ -432,11 +457,25 @@ hsdpa_status hsdpa_plan_create(const hsdpa_spec *spec, hsdpa_plan **out)
     const uint64_t cap = spec->kv_capacity;
     p->kv_heads = kvh;
     p->form = spec->form == HSDPA_FORM_FUSED && d <= 256 ? HSDPA_FORM_FUSED : HSDPA_FORM_CHAINED;
+    if (p->form == HSDPA_FORM_FUSED && g > kFusedMaxGqa) {
+        delete p;
+        return HSDPA_ERR_FORM;
+    }
     p->max_rows = spec->max_rows ? spec->max_rows : cap;
     // the grids (and so the workspace) follow the device's compute units; with
     // no device current, the MI355X's 256
     int cus = 0;
-    p->cus = check_device(&cus) == HSDPA_OK && cus > 0 ? cus : 256;
+    const bool on_gfx950 = check_device(&cus) == HSDPA_OK;
+    p->cus = on_gfx950 && cus > 0 ? cus : 256;
+    // the static scratch's address on this device, so that no call of
+    // hsdpa_attention_static (possibly under graph capture) looks it up
+    if (on_gfx950) {
+        void *scratch = nullptr;
+        if (hsdpa::static_scratch(&scratch) != hipSuccess) {
+            delete p;
+            return HSDPA_ERR_HIP;
+        }
+    }
     // decode columns: the query heads of one row, or up to 16 rows of them
     const int gi = static_cast<int>(std::min<uint64_t>(g, 1u << 20));
     const bool pad_ok = hsdpa::decode_rows_ok(static_cast<int>(d)) && hsdpa::decode_groups_pad(gi) > 0;
@@ -452,7 +491,7 @@ hsdpa_status hsdpa_plan_create(const hsdpa_spec *spec, hsdpa_plan **out)
     // serves, its columns counting the padding of the last group
     uint64_t part = 0, cols_used = 0, cols_pad = 0;
     for (uint64_t r = 1; r <= std::min<uint64_t>(hsdpa::kDecodeMaxRows, p->max_rows); r++) {
-        const int sub = decode_sub(p, r, 0);
+        const int sub = r == 1 && p->form == HSDPA_FORM_FUSED ? fused_row_sub(p, 0) : decode_sub(p, r, 0);
         if (sub == 0) continue;
         const uint64_t padded = static_cast<uint64_t>(sub) * hsdpa::decode_group_cols(static_cast<int>(r * g), sub);
         cols_used = std::max(cols_used, r * g);
@@ -481,7 +520,7 @@ hsdpa_status hsdpa_plan_create(const hsdpa_spec *spec, hsdpa_plan **out)
     // one round of the compute units (8 row blocks of 32 per workgroup), when
     // some call of the plan reaches the causal kernels
     bool causal = false;
-    for (uint64_t r = 1; r <= std::min<uint64_t>(hsdpa::kDecodeMaxRows + 1, p->max_rows) && !causal; r++)
+    for (uint64_t r = 1; r <= std::min<uint64_t>(hsdpa::kDecodeMaxRows + 8, p->max_rows) && !causal; r++)
         causal = reaches_causal(p, r);
     p->split_units = causal ? std::min<uint64_t>(hsdpa::kSplitUnits, 8 * static_cast<uint64_t>(p->cus)) : 0;
     const uint64_t cells = p->split_units * 32;
@@ -517,7 +556,7 @@ static hsdpa_status run_part(const hsdpa_plan *plan, const hsdpa_call *call, con
     const uint16_t *q = call->q ? call->q + part.row0 * s.q_row : nullptr;
     uint16_t *outp = call->output ? call->output + part.row0 * s.out_row : nullptr;
     const uint16_t *gp = gate ? gate + part.row0 * gate_row : nullptr;
-    const int sub = decode_sub(plan, rows, past + rows);
+    const int sub = part.fused && rows == 1 ? fused_row_sub(plan, n) : decode_sub(plan, rows, n);
     if (sub > 0) {
         const DecodeCfg c = decode_cfg(plan, rows, n, sub, part.fused);
         if (kernels) *kernels = rows == 1 ? HSDPA_KERNELS_DECODE : HSDPA_KERNELS_FEW_ROWS;
@@ -616,8 +655,7 @@ static hsdpa_status run_part(const hsdpa_plan *plan, const hsdpa_call *call, con
 // The attention node on validated arguments: under the Fused form the rows
 // outside full chunks of 8 take the Fused numerics on the decode kernels (as
 // one few-rows call where the decode kernels take them together, else one
-// decode per row), the others the Chained ones; a route that ends on the
-// causal kernels keeps the Chained numerics.
+// decode per row, fused_row_sub), the others the Chained ones.
 static hsdpa_status run_attention(const hsdpa_plan *plan, const hsdpa_call *call, const uint16_t *gate,
                                   uint64_t gate_row, hipStream_t st, bool launch, hsdpa_route *route)
 {
@@ -802,7 +840,7 @@ const char *hsdpa_status_string(hsdpa_status status)
     case HSDPA_ERR_NO_DEVICE: return "no gfx950 device is current";
     case HSDPA_ERR_BATCH: return "more rows than the reserve's max_batch or the plan's max_rows";
     case HSDPA_ERR_LAYOUT: return "the R16 copies of the KV cache are an AArch64 layout";
-    case HSDPA_ERR_FORM: return "unknown decode form";
+    case HSDPA_ERR_FORM: return "unknown decode form, or a Fused plan with more than 65536 query heads per KV head";
     case HSDPA_ERR_STATIC_SCRATCH: return "the plan's workspace exceeds the static scratch (HSDPA_STATIC_SCRATCH_BYTES)";
     }
     return "unknown status";

@@ -70,31 +70,39 @@ static hipError_t fused_tuned(const DecodeArgs &a, int kv_heads, hipStream_t s)
 }
 
 // The other head dimensions up to 256: one row, the configurations of
-// hsdpa_attn_more.hip.
-template <int D>
-static hipError_t fused_more(const DecodeArgs &a, int kv_heads, hipStream_t s)
+// hsdpa_attn_more.hip; MR = 1 for a group size with no equal split into
+// groups of at most 16 (padded groups: the Fused form serves every row on the
+// decode kernels, where the Chained form would take the causal kernel).
+template <int D, int MR>
+static hipError_t fused_more_m(const DecodeArgs &a, int kv_heads, hipStream_t s)
 {
-    if (a.rows != 1) return hipErrorInvalidValue;           // decode_rows_ok
     const dim3 gqk(a.nwg_qk, kv_heads, a.sub), gpv(a.nwg_pv, kv_heads, a.sub);
-    hipError_t e = a.keys_qk == 8 * kKeyTile ? launch(decode_qk<D, true, 0, true, true>, gqk, dim3(256), s, a)
-                   : a.keys_qk > 4 * kKeyTile  ? launch(decode_qk<D, true, 0, true>, gqk, dim3(256), s, a)
-                                               : launch(decode_qk<D, false, 0, true>, gqk, dim3(256), s, a);
+    hipError_t e = a.keys_qk == 8 * kKeyTile ? launch(decode_qk<D, true, MR, true, true>, gqk, dim3(256), s, a)
+                   : a.keys_qk > 4 * kKeyTile  ? launch(decode_qk<D, true, MR, true>, gqk, dim3(256), s, a)
+                                               : launch(decode_qk<D, false, MR, true>, gqk, dim3(256), s, a);
     if (e != hipSuccess) return e;
     constexpr bool WIDE = D / 16 >= 8 || 8 % (D / 16) == 0;        // decode_wide_ok
     if (a.keys_pv == 4 * kKeyTile) {
-        e = a.g <= 8 ? launch(decode_pv<D, 4, 1, false, 0, true>, gpv, dim3(256), s, a)
-                     : launch(decode_pv<D, 4, 2, false, 0, true>, gpv, dim3(256), s, a);
+        e = a.g <= 8 ? launch(decode_pv<D, 4, 1, false, MR, true>, gpv, dim3(256), s, a)
+                     : launch(decode_pv<D, 4, 2, false, MR, true>, gpv, dim3(256), s, a);
     } else {
         if constexpr (WIDE) {
-            e = a.g <= 8 ? launch(decode_pv<D, 8, 1, false, 0, true>, gpv, dim3(512), s, a)
-                         : launch(decode_pv<D, 8, 2, false, 0, true>, gpv, dim3(512), s, a);
+            e = a.g <= 8 ? launch(decode_pv<D, 8, 1, false, MR, true>, gpv, dim3(512), s, a)
+                         : launch(decode_pv<D, 8, 2, false, MR, true>, gpv, dim3(512), s, a);
         } else {
             return hipErrorInvalidValue;
         }
     }
     if (e != hipSuccess) return e;
-    return launch(decode_combine<D, false, true>, dim3(kv_heads * a.sub * a.g, (D + 63) / 64),
+    return launch(decode_combine<D, MR != 0, true>, dim3(kv_heads * a.sub * a.g, (D + 63) / 64),
                   dim3(64 * kCombineSubs), s, a);
+}
+
+template <int D>
+static hipError_t fused_more(const DecodeArgs &a, int kv_heads, hipStream_t s)
+{
+    if (a.rows != 1 || a.xcd) return hipErrorInvalidValue;  // decode_rows_ok; decode_cfg
+    return a.g * a.sub == a.cols ? fused_more_m<D, 0>(a, kv_heads, s) : fused_more_m<D, 1>(a, kv_heads, s);
 }
 
 hipError_t launch_decode_fused(const DecodeArgs &a, int head_dim, int kv_heads, hipStream_t s)

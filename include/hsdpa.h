@@ -80,7 +80,9 @@ typedef enum hsdpa_status {
     HSDPA_ERR_BATCH = 12,           /* kv append: rows > max_batch (the frame's bound);
                                        attention: rows > the plan's max_rows */
     HSDPA_ERR_LAYOUT = 13,          /* kv append: the R16 copies, an AArch64 layout (kv.rs:19-21) */
-    HSDPA_ERR_FORM = 14,            /* an unknown decode form (the knob's parse, knobs.rs:66-68) */
+    HSDPA_ERR_FORM = 14,            /* an unknown decode form (the knob's parse, knobs.rs:66-68),
+                                       or a Fused plan with more than 65 536 query heads per
+                                       KV head (more padded decode groups than a grid holds) */
     HSDPA_ERR_STATIC_SCRATCH = 15   /* hsdpa_attention_static: the plan's workspace exceeds
                                        HSDPA_STATIC_SCRATCH_BYTES */
 } hsdpa_status;
@@ -94,8 +96,10 @@ typedef enum hsdpa_status {
  * P(m_old - m_new), the sum's reciprocal at the end. Under Fused, like the
  * reference, the rows the engine serves with its prefill block (full chunks
  * of 8 rows) keep the Chained numerics; the other rows (a decode row, the
- * last rows % 8 of a chunk) take the Fused ones; above head_dim 256 the form
- * falls back to Chained (src/jit/sdpa.rs:491-510). */
+ * last rows % 8 of a chunk) take the Fused ones, on the decode kernels
+ * whatever the shape (padded groups where no equal split into groups of at
+ * most 16 query heads exists); above head_dim 256 the form falls back to
+ * Chained (src/jit/sdpa.rs:491-510). */
 typedef enum hsdpa_form {
     HSDPA_FORM_CHAINED = 0,
     HSDPA_FORM_FUSED = 1
@@ -192,10 +196,12 @@ hsdpa_status hsdpa_attention(const hsdpa_plan *plan, const hsdpa_call *call, voi
  * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc.
  * The scratch is one static array of HSDPA_STATIC_SCRATCH_BYTES per GPU,
  * held until the process ends; a plan whose hsdpa_workspace_bytes exceeds it
- * is refused (HSDPA_ERR_STATIC_SCRATCH) before any launch: a decode-only plan
- * (max_rows = 1) fits up to about 400K cached positions at 16 query heads on 2
- * KV heads of head_dim 256. The call allocates nothing (its first call on a
- * device looks up that device's copy of the array). Every call on a GPU shares
+ * is refused (HSDPA_ERR_STATIC_SCRATCH) before any launch: at 16 query heads on
+ * 2 KV heads of head_dim 256 (256 CUs), a decode-only plan (max_rows = 1) fits
+ * up to a capacity of 487 424 positions, max_rows = 8 up to 32 512. The call
+ * allocates nothing and looks nothing up: hsdpa_plan_create resolves the
+ * array's address on the device current at plan creation (a call on a device
+ * no plan was created on resolves it there, once). Every call on a GPU shares
  * that GPU's array: calls that overlap on one GPU (different streams, or
  * threads enqueueing at once) race on it; stream-ordered calls do not. */
 #define HSDPA_STATIC_SCRATCH_BYTES (32u << 20)

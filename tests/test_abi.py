@@ -45,7 +45,7 @@ def test_library_has_gfx950_code():
 
 def test_status_strings_and_version():
     lib = hsdpa.library()
-    for code in range(15):
+    for code in range(16):
         assert lib.hsdpa_status_string(code) != b"unknown status", code
     assert lib.hsdpa_version() >= 200
 
@@ -157,9 +157,23 @@ def test_route_names_the_kernels():
     r = hsdpa.Plan(17, 17, 128, 100, form="fused").route(1, 10)
     assert r["main"] == "decode" and r["main_form"] == "fused"
     assert hsdpa.Plan(160, 80, 256, 40000).route(1, 32767)["main"] == "decode"     # 80 heads: 5 groups of 16
-    # ...and keeps the causal kernel (and the Chained numerics) at the others
-    r = hsdpa.Plan(17, 17, 96, 100, form="fused").route(1, 10)
-    assert r["main"] == "causal" and r["main_form"] == "chained"
+    # ...and at the other head dimensions a Chained plan keeps the causal kernel
+    assert hsdpa.Plan(17, 17, 96, 100).route(1, 10)["main"] == "causal"
+    # while a Fused plan serves every row outside full chunks of 8 with the
+    # Fused numerics on padded decode groups, as the reference's Fused head
+    # does: a group size with no equal split at D 96, more than 256 heads per
+    # KV head, padded groups over a long cache
+    for spec, rows, past in [((17, 17, 96, 100), 1, 10), ((17, 17, 96, 4000), 1, 3000),
+                             ((300, 300, 64, 1000), 1, 500), ((100, 100, 128, 40000), 1, 32000),
+                             ((34, 17, 160, 100), 1, 50)]:
+        r = hsdpa.Plan(*spec, form="fused").route(rows, past)
+        assert r["main"] == "decode" and r["main_form"] == "fused", (spec, r)
+        assert hsdpa.Plan(*spec).route(rows, past)["main"] != "decode", spec
+    r = hsdpa.Plan(17, 17, 96, 100, form="fused").route(11, 50)
+    assert (r["main"], r["main_form"], r["tail"], r["tail_form"]) == ("causal", "chained", "decode_rows", "fused")
+    # beyond 65 536 query heads per KV head the Fused form has no decode grid
+    with pytest.raises(hsdpa.HsdpaError):
+        hsdpa.Plan(65537, 65537, 64, 10, form="fused")
     # one row per decode where the tail does not fit the decode columns (5 rows
     # of 32 heads: 160 columns, past 128)
     r = hsdpa.Plan(64, 32, 128, 1000, form="fused").route(13, 100)

@@ -454,3 +454,42 @@ def test_fused_gpu_scheme_meets_the_bar_and_online_flash_does_not():
         flash[0, h] = bf(O.astype(f32) * (f32(1.0) / f32(lsum)))
     assert compare(good, ref, w)["ulp1_share"] >= 0.999
     assert compare(flash, ref, w)["ulp1_share"] < 0.999
+
+
+def test_one_pass_decode_fails_the_chained_bar_at_32k():
+    """The default (Chained) form evaluates every exponential at the exact row
+    maximum (src/jit/target/x86/emit_sdpa/x86/decode.rs:212-293). A model of
+    the GPU's two-pass scheme (f32 scores, the exact maximum, P split hi + lo,
+    one division at the end) meets the bar against the Chained oracle at the
+    32K configuration. A one-pass split-KV decode, which would stream K and V
+    in one kernel (each key range at its own maximum m_w, its O and l rescaled
+    by P(m_w - M) in the combine), does not, with ranges of 256 or 1024 keys:
+    the polynomial's error depends on where it is evaluated, and near-zero
+    outputs move by more than an ulp (seeds 0-2: 99.76-99.88 % within one ulp;
+    an exact exp for the rescale factor does no better). So the decode keeps
+    its two passes."""
+    w = W.config("decode_32k", seed=0)
+    ref = oracle.attention(w)
+    n = w.past + 1
+    exact = np.zeros_like(ref)
+    one = {256: np.zeros_like(ref), 1024: np.zeros_like(ref)}
+    for h in range(w.heads):
+        kf = W.bf16_to_f32(w.k[h // w.gqa][:n]).astype(np.float64)
+        vf = W.bf16_to_f32(w.v[h // w.gqa][:n]).astype(np.float64)
+        s = ((kf @ W.bf16_to_f32(w.q[0, h]).astype(np.float64)).astype(f32) * f32(w.scale)).astype(f32)
+        e = oracle.exp_poly((s - s.max()).astype(f32))
+        exact[0, h] = bf((_split(e) @ vf).astype(f32) / f32(e.astype(np.float64).sum()))
+        for S, out in one.items():
+            ms = np.array([s[i:i + S].max() for i in range(0, n, S)], f32)
+            fw = oracle.exp_poly((ms - ms.max()).astype(f32)).astype(np.float64)
+            O = np.zeros(w.head_dim)
+            lsum = 0.0
+            for i, j0 in enumerate(range(0, n, S)):
+                e = oracle.exp_poly((s[j0:j0 + S] - ms[i]).astype(f32))
+                O += fw[i] * (_split(e) @ vf[j0:j0 + S])
+                lsum += fw[i] * e.astype(np.float64).sum()
+            out[0, h] = bf(O.astype(f32) / f32(lsum))
+    assert compare(exact, ref, w)["ulp1_share"] >= 0.999
+    for S, out in one.items():
+        r = compare(out, ref, w)
+        assert r["ulp1_share"] < 0.999 and r["max_abs_over_vmax"] <= 2.0 ** -6, (S, r)

@@ -65,6 +65,13 @@ FUSED = [
     ("fused_d128_g17_padded", 17, 1, 128, 1, 900, ("decode", "fused"), None),
     ("fused_d256_g17_padded_2kv_long", 34, 2, 256, 1, 40000, ("decode", "fused"), None),
     ("fused_few_r5_g7_d256_padded", 7, 1, 256, 5, 300, ("few_rows", "fused"), None),
+    # shapes the Chained form serves on the causal kernels: under the Fused
+    # form every row outside a full chunk of 8 takes padded decode groups
+    ("fused_d96_g17_padded", 17, 1, 96, 1, 900, ("decode", "fused"), None),
+    ("fused_d96_g17_prefill_tail", 17, 1, 96, 11, 50, ("causal", "chained"), ("decode_rows", "fused")),
+    ("fused_d160_g34_padded_2kv", 68, 2, 160, 1, 5000, ("decode", "fused"), None),
+    ("fused_d64_g300_padded", 300, 1, 64, 1, 600, ("decode", "fused"), None),
+    ("fused_d128_g100_padded_long", 100, 1, 128, 1, 32000, ("decode", "fused"), None),
     # above head_dim 256 the form falls back to Chained, like the reference
     ("fused_d288_falls_back", 4, 2, 288, 1, 300, ("decode", "chained"), None),
 ]

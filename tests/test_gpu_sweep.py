@@ -76,7 +76,7 @@ LONG_CASES = _draw_long()
 # (main kernels, main numerics, tail kernels, launches, split over keys) that
 # the draw reaches
 REACHED = {
-    ("causal", "chained", "causal", 5, False),
+    ("causal", "chained", "decode_rows", 13, False),
     ("causal", "chained", "decode", 3, False),
     ("causal", "chained", "decode", 4, False),
     ("causal", "chained", "few_rows", 4, False),
@@ -121,10 +121,11 @@ def test_sweep_reaches_every_route_class(cases, reached):
 @pytest.mark.gpu
 @pytest.mark.parametrize("cases,seed0", [(CASES, 31), (LONG_CASES, 131)], ids=["short", "long"])
 def test_sweep_parity(torch_cuda, cases, seed0):
-    """Each call: no NaN, the per-row bound max |out - ref| <= 2^-6 max |V|,
-    and at most max(2, 1 %) of its outputs past one ulp (a call of 128
-    outputs cannot show a 99.9 % share, a wrong kernel misses by far more);
-    over the calls together at least 99.9 % of outputs within one ulp."""
+    """Each call: no NaN, the per-row bound max |out - ref| <= 2^-6 max |V|;
+    a call of at least 4096 outputs at least 99.9 % of them within one ulp,
+    a smaller one at most max(2, 1 %) past one ulp (a call of 128 outputs
+    cannot show a 99.9 % share, a wrong kernel misses by far more); over the
+    calls together at least 99.9 % of outputs within one ulp."""
     within = total = 0
     for i, (name, h, kvh, d, rows, past, form) in enumerate(cases):
         w = W.make(name, heads=h, kv_heads=kvh, head_dim=d, rows=rows, past=past, seed=seed0 + i)
@@ -137,7 +138,10 @@ def test_sweep_parity(torch_cuda, cases, seed0):
         assert r["max_abs_over_vmax"] <= ABS_FACTOR, (name, r)
         n = out.size
         off = int(round((1.0 - r["ulp1_share"]) * n))
-        assert off <= max(2, n // 100), (name, r)
+        if n >= 4096:
+            assert r["ulp1_share"] >= ULP_SHARE, (name, r)
+        else:
+            assert off <= max(2, n // 100), (name, r)
         within += n - off
         total += n
     assert within / total >= ULP_SHARE, (within, total)

@@ -69,3 +69,40 @@ def test_static_refuses_a_plan_beyond_the_scratch(torch_cuda):
     call = binding.Call(0x10000, 0x20000, 0x30000, 0x40000, 1, 100, 0.0625, 0.0, 0, 0)
     rc = hsdpa.library().hsdpa_attention_static(plan.handle, ctypes.byref(call), None)
     assert binding.STATUS[rc] == "HSDPA_ERR_STATIC_SCRATCH"
+
+
+def test_static_entry_under_graph_capture(torch_cuda):
+    """hsdpa_attention_static captured in a HIP graph (its address resolved at
+    plan creation, so the captured call looks nothing up): each replay equals
+    hsdpa_attention bit for bit, also after an eager call on other inputs has
+    left its own contents in the shared scratch between the replays."""
+    h, g, d, cap = 16, 8, 256, 8192
+    plan = hsdpa.Plan(h, g, d, cap, max_rows=1)
+    w = W.make("graph_static", heads=h, kv_heads=h // g, head_dim=d, rows=1, past=5000, capacity=cap, seed=41)
+    other = W.make("graph_static_other", heads=h, kv_heads=h // g, head_dim=d, rows=1, past=700, capacity=cap,
+                   seed=42)
+    want = _run(plan, w, static=False)
+    q, k, v = _dev(w.q), _dev(w.k), _dev(w.v)
+    out = torch.full((w.rows, w.heads, w.head_dim), -1, dtype=torch.int16, device="cuda")
+    call = binding.Call(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), w.rows, w.past, w.scale, 0.0,
+                        0, 0)
+    lib = hsdpa.library()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        rc = lib.hsdpa_attention_static(plan.handle, ctypes.byref(call), ctypes.c_void_p(side.cuda_stream))
+        assert rc == 0, binding.STATUS.get(rc)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        rc = lib.hsdpa_attention_static(plan.handle, ctypes.byref(call),
+                                        ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    assert rc == 0, binding.STATUS.get(rc)
+    for i in range(3):
+        out.fill_(-1)
+        print(f"graph replay {i}", flush=True)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(out.cpu().numpy().view(np.uint16), want), f"replay {i}"
+        _run(plan, other, static=True)          # eager, other contents in the scratch
