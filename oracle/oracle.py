@@ -67,6 +67,8 @@ def lib():
         L.oracle_sdpa_head.argtypes = [u16p, u16p, u16p, ctypes.c_void_p, u16p, ctypes.c_uint64,
                                        ctypes.c_float, ctypes.c_int]
         L.oracle_sdpa_head.restype = None
+        L.oracle_sdpa_head_qk0.argtypes = L.oracle_sdpa_head.argtypes
+        L.oracle_sdpa_head_qk0.restype = None
         L.oracle_sdpa_prefill_block.argtypes = [u16p, u16p, u16p, ctypes.c_void_p, u16p, ctypes.c_uint64,
                                                 ctypes.c_float, ctypes.c_int, ctypes.c_int, ctypes.c_size_t,
                                                 ctypes.c_size_t]
@@ -110,7 +112,7 @@ def avx512_available() -> bool:
     return bool(lib().oracle_avx512_available())
 
 
-FORMS = {"chained": 0, "fused": 1, "avx2": 2}
+FORMS = {"chained": 0, "fused": 1, "avx2": 2, "chained_qk0": 3}
 
 
 def attention(w, impl: str = "auto", threads: int = 0, form: str = "chained") -> np.ndarray:
@@ -118,8 +120,10 @@ def attention(w, impl: str = "auto", threads: int = 0, form: str = "chained") ->
     [rows][heads][head_dim]. impl: 'scalar', 'avx512' or 'auto' (AVX-512
     when the host has it, which is bit-identical to the scalar one).
     form: 'chained' (the engine's default), 'fused' (the knob's online
-    softmax) or 'avx2' (a host without AVX-512 BF16); the last two run the
-    scalar emulation on `threads` threads (0: the host's cores, at most 16)."""
+    softmax), 'avx2' (a host without AVX-512 BF16) or 'chained_qk0' (the
+    default form with the knob sdpa_qk_group = 0: four QK chains); the other
+    forms than 'chained' run the scalar emulation on `threads` threads (0:
+    the host's cores, at most 16)."""
     L = lib()
     if form != "chained":
         out = np.zeros((w.rows, w.heads, w.head_dim), dtype=np.uint16)
@@ -150,15 +154,17 @@ def attention(w, impl: str = "auto", threads: int = 0, form: str = "chained") ->
     return out
 
 
-def head(q: np.ndarray, k: np.ndarray, v: np.ndarray, n: int, scale: float) -> np.ndarray:
-    """One decode head (scalar emulation): q [d], k/v [>=n][d] -> out [d] bf16 bits."""
+def head(q: np.ndarray, k: np.ndarray, v: np.ndarray, n: int, scale: float, qk_group0: bool = False) -> np.ndarray:
+    """One decode head (scalar emulation): q [d], k/v [>=n][d] -> out [d] bf16 bits.
+    qk_group0: the knob sdpa_qk_group = 0 (the QK in four chains)."""
     d = q.shape[-1]
     q = np.ascontiguousarray(q, dtype=np.uint16)
     k = np.ascontiguousarray(k, dtype=np.uint16)
     v = np.ascontiguousarray(v, dtype=np.uint16)
     sc = np.zeros(((n + 15) // 16) * 16, dtype=np.float32)
     out = np.zeros(d, dtype=np.uint16)
-    lib().oracle_sdpa_head(_ptr(q), _ptr(k), _ptr(v), _ptr(sc), _ptr(out), n, scale, d)
+    fn = lib().oracle_sdpa_head_qk0 if qk_group0 else lib().oracle_sdpa_head
+    fn(_ptr(q), _ptr(k), _ptr(v), _ptr(sc), _ptr(out), n, scale, d)
     return out
 
 

@@ -252,9 +252,14 @@ static int run_rows(const oracle_attention_spec *s, const oracle_attention_call 
     const uint16_t *kk = c->keys + kvh * c->kv_stride, *vv = c->values + kvh * c->kv_stride;
     if (form != 2 && r1 - r0 == 8) {
         const uint64_t ar = pass_row0 + r0;
-        oracle_sdpa_prefill_block(c->q + ar * s->q_row + h * s->q_head, kk, vv, scratch,
-                                  c->output + ar * s->out_row + h * d, pass_past + r0, c->scale, (int)d, 8,
-                                  s->q_row, s->out_row);
+        if (form == 3)
+            oracle_sdpa_prefill_block_qk0(c->q + ar * s->q_row + h * s->q_head, kk, vv, scratch,
+                                          c->output + ar * s->out_row + h * d, pass_past + r0, c->scale, (int)d, 8,
+                                          s->q_row, s->out_row);
+        else
+            oracle_sdpa_prefill_block(c->q + ar * s->q_row + h * s->q_head, kk, vv, scratch,
+                                      c->output + ar * s->out_row + h * d, pass_past + r0, c->scale, (int)d, 8,
+                                      s->q_row, s->out_row);
         return 0;
     }
     for (uint64_t r = r0; r < r1; r++) {
@@ -265,6 +270,8 @@ static int run_rows(const oracle_attention_spec *s, const oracle_attention_call 
             if (oracle_fused_head(qp, kk, vv, op, n, c->scale, (int)d, NULL) != 0) return -1;
         } else if (form == 2) {
             if (oracle_avx2_head(qp, kk, vv, scratch, op, n, c->scale, (int)d) != 0) return -1;
+        } else if (form == 3) {
+            oracle_sdpa_head_qk0(qp, kk, vv, scratch, op, n, c->scale, (int)d);
         } else {
             oracle_sdpa_head(qp, kk, vv, scratch, op, n, c->scale, (int)d);
         }
@@ -297,13 +304,14 @@ static void *form_worker(void *arg)
     return NULL;
 }
 
-/* The attention node with the given decode form (0 Chained, 1 Fused, 2 AVX2)
+/* The attention node with the given decode form (0 Chained, 1 Fused, 2 AVX2,
+ * 3 Chained with sdpa_qk_group = 0)
  * on `threads` threads (0 or 1: the calling thread), tasks = (q head, row
  * group) in contiguous ranges. Rows are processed in passes of 256, so a row
  * group never straddles a pass. Returns 0, or -1 on an invalid geometry. */
 int oracle_attention_form(const oracle_attention_spec *s, const oracle_attention_call *c, int form, int threads)
 {
-    if (oracle_check_geometry(s, c) != 0 || form < 0 || form > 2) return -1;
+    if (oracle_check_geometry(s, c) != 0 || form < 0 || form > 3) return -1;
     if (c->rows == 0) return 0;
     const uint64_t chunk = form == 2 ? 1 : 8;
     const uint64_t tasks = s->heads * ((c->rows + chunk - 1) / chunk);

@@ -70,6 +70,18 @@ void oracle_sdpa_prefill_block(const uint16_t *q, const uint16_t *k,
                                uint64_t past, float scale, int head_dim,
                                int rows, size_t q_row, size_t out_row);
 
+/* The same head and block with the knob sdpa_qk_group = 0
+ * (src/jit/sdpa.rs:178-202): the row kernel's four accumulation chains
+ * (decode.rs:59-128 with chains = 4, prefill.rs:104-157 with chains = 4),
+ * whose score equals oracle_fused_qk_dot's; softmax and SV unchanged. */
+void oracle_sdpa_head_qk0(const uint16_t *q, const uint16_t *k, const uint16_t *v,
+                          float *scores, uint16_t *out, uint64_t n, float scale,
+                          int head_dim);
+void oracle_sdpa_prefill_block_qk0(const uint16_t *q, const uint16_t *k,
+                                   const uint16_t *v, float *scores, uint16_t *out,
+                                   uint64_t past, float scale, int head_dim,
+                                   int rows, size_t q_row, size_t out_row);
+
 /* The score of one (query, key) pair as the grouped QK computes it, before
  * the scale (single chain + the hsum tree, prefill.rs:302-331). */
 float oracle_qk_dot(const uint16_t *q, const uint16_t *k, int head_dim);
@@ -140,7 +152,8 @@ uint16_t oracle_avx2_cvt_bf16(float x);
 /* The attention node under a decode form: 0 Chained (as
  * oracle_attention_scalar), 1 Fused (full 8-row chunks still take the block
  * kernel; other rows the Fused head, or the Chained one above head_dim 256),
- * 2 AVX2 (every row the AVX2 head). `threads` workers over (q head, row
+ * 2 AVX2 (every row the AVX2 head), 3 Chained with sdpa_qk_group = 0 (block
+ * and head with the four-chain QK). `threads` workers over (q head, row
  * group) tasks. Returns 0 or -1. */
 int oracle_attention_form(const oracle_attention_spec *spec, const oracle_attention_call *call, int form,
                           int threads);

@@ -160,14 +160,16 @@ static void softmax_blocks(float *sc, uint64_t nb)
     for (uint64_t i = 0; i < 16 * nb; i++) sc[i] = sc[i] / sum;
 }
 
+typedef float (*qk_dot_fn)(const uint16_t *, const uint16_t *, int);
+
 /* assembly.rs:116-174: QK pass (then -inf padding to a multiple of 16,
- * decode.rs:113-126), softmax, SV pass (decode.rs:348-428). */
-void oracle_sdpa_head(const uint16_t *q, const uint16_t *k, const uint16_t *v,
-                      float *scores, uint16_t *out, uint64_t n, float scale,
-                      int head_dim)
+ * decode.rs:113-126), softmax, SV pass (decode.rs:348-428), with the QK
+ * summation order `qk` (the knob sdpa_qk_group, src/jit/sdpa.rs:178-202). */
+static void sdpa_head_qk(qk_dot_fn qk, const uint16_t *q, const uint16_t *k, const uint16_t *v, float *scores,
+                         uint16_t *out, uint64_t n, float scale, int head_dim)
 {
     const size_t d = (size_t)head_dim;
-    for (uint64_t j = 0; j < n; j++) scores[j] = oracle_qk_dot(q, k + j * d, head_dim) * scale;
+    for (uint64_t j = 0; j < n; j++) scores[j] = qk(q, k + j * d, head_dim) * scale;
     for (uint64_t j = n; j < roundup16(n); j++) scores[j] = -INFINITY;
     softmax_blocks(scores, roundup16(n) / 16);
     float acc[512];
@@ -180,21 +182,41 @@ void oracle_sdpa_head(const uint16_t *q, const uint16_t *k, const uint16_t *v,
     for (size_t c = 0; c < d; c++) out[c] = oracle_cvtneps2bf16(acc[c]);
 }
 
+void oracle_sdpa_head(const uint16_t *q, const uint16_t *k, const uint16_t *v,
+                      float *scores, uint16_t *out, uint64_t n, float scale,
+                      int head_dim)
+{
+    sdpa_head_qk(oracle_qk_dot, q, k, v, scores, out, n, scale, head_dim);
+}
+
+/* sdpa_qk_group = 0 (src/jit/sdpa.rs:178-202): emit_qk with four chains
+ * (stash_scale, prefill.rs:558-567; decode.rs:59-128), whose score is the
+ * Fused form's (oracle_fused_qk_dot: chunk c into chain c % min(4, n32),
+ * (c0 + c1) + (c2 + c3), hsum). */
+void oracle_sdpa_head_qk0(const uint16_t *q, const uint16_t *k, const uint16_t *v,
+                          float *scores, uint16_t *out, uint64_t n, float scale,
+                          int head_dim)
+{
+    sdpa_head_qk(oracle_fused_qk_dot, q, k, v, scores, out, n, scale, head_dim);
+}
+
 /* assemble_prefill (prefill.rs:733-912): the whole rows x N rectangle of
  * scores (N = past + rows), -inf from n_i = past+i+1 to roundup16(n_i), the
  * decode softmax on exactly that many blocks per row, +0.0 written over the
- * columns n_i..N-1, then the SV over N positions for all rows. */
-void oracle_sdpa_prefill_block(const uint16_t *q, const uint16_t *k,
-                               const uint16_t *v, float *scores, uint16_t *out,
-                               uint64_t past, float scale, int head_dim,
-                               int rows, size_t q_row, size_t out_row)
+ * columns n_i..N-1, then the SV over N positions for all rows. The scores
+ * in the summation order `qk`: one chain (the default group of 8), or four
+ * with sdpa_qk_group = 0 (emit_qk_block with chains = 4, prefill.rs:780,
+ * 104-157: the tree of emit_qk "verbatim"). */
+static void prefill_block_qk(qk_dot_fn qk, const uint16_t *q, const uint16_t *k, const uint16_t *v, float *scores,
+                             uint16_t *out, uint64_t past, float scale, int head_dim, int rows, size_t q_row,
+                             size_t out_row)
 {
     const size_t d = (size_t)head_dim;
     const uint64_t N = past + (uint64_t)rows;
     const uint64_t rs = roundup16(N);                 /* PF_ROWB / 4 */
     for (int i = 0; i < rows; i++)
         for (uint64_t j = 0; j < N; j++)
-            scores[i * rs + j] = oracle_qk_dot(q + i * q_row, k + j * d, head_dim) * scale;
+            scores[i * rs + j] = qk(q + i * q_row, k + j * d, head_dim) * scale;
     for (int i = 0; i < rows; i++) {
         uint64_t ni = past + (uint64_t)i + 1;
         for (uint64_t j = ni; j < roundup16(ni); j++) scores[i * rs + j] = -INFINITY;
@@ -212,6 +234,22 @@ void oracle_sdpa_prefill_block(const uint16_t *q, const uint16_t *k,
         }
         for (size_t c = 0; c < d; c++) out[i * out_row + c] = oracle_cvtneps2bf16(acc[c]);
     }
+}
+
+void oracle_sdpa_prefill_block(const uint16_t *q, const uint16_t *k,
+                               const uint16_t *v, float *scores, uint16_t *out,
+                               uint64_t past, float scale, int head_dim,
+                               int rows, size_t q_row, size_t out_row)
+{
+    prefill_block_qk(oracle_qk_dot, q, k, v, scores, out, past, scale, head_dim, rows, q_row, out_row);
+}
+
+void oracle_sdpa_prefill_block_qk0(const uint16_t *q, const uint16_t *k,
+                                   const uint16_t *v, float *scores, uint16_t *out,
+                                   uint64_t past, float scale, int head_dim,
+                                   int rows, size_t q_row, size_t out_row)
+{
+    prefill_block_qk(oracle_fused_qk_dot, q, k, v, scores, out, past, scale, head_dim, rows, q_row, out_row);
 }
 
 /* tile_selector's geometry checks (attention.rs:61-98) plus the shape

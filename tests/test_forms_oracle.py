@@ -493,3 +493,61 @@ def test_one_pass_decode_fails_the_chained_bar_at_32k():
     for S, out in one.items():
         r = compare(out, ref, w)
         assert r["ulp1_share"] < 0.999 and r["max_abs_over_vmax"] <= 2.0 ** -6, (S, r)
+
+
+# ---- the knob sdpa_qk_group = 0: the Chained form with four QK chains ----------
+
+def _chain_witness(d=256):
+    """q, K rows and V rows of a two-key head whose first score is 0 in one
+    chain and 2 in four: lane 0 of chunk 0 adds 2^24, chunks 1 and 2 add 1
+    each, chunk 4 subtracts 2^24. One chain: 2^24 + 1 rounds to 2^24 (a tie,
+    to even) twice, then 0. Four chains (chunk c into chain c % 4): chain 0
+    is 2^24 - 2^24 = 0, chains 1 and 2 are 1, (0 + 1) + (1 + 0) = 2."""
+    q = np.zeros(d, np.uint16)
+    k = np.zeros((2, d), np.uint16)
+    v = np.zeros((2, d), np.uint16)
+    two12, neg_two12 = 0x4580, 0xC580                       # bf16 of 2^12 and -2^12
+    q[1], k[0, 1] = two12, two12                            # chunk 0, lane 0, odd element: 2^24
+    q[32 + 1], k[0, 32 + 1] = ONE, ONE                      # chunk 1: 1
+    q[64 + 1], k[0, 64 + 1] = ONE, ONE                      # chunk 2: 1
+    q[128 + 1], k[0, 128 + 1] = neg_two12, two12            # chunk 4: -2^24
+    v[0, :] = ONE                                           # key 0's values 1, key 1's 0
+    return q, k, v
+
+
+def test_qk_group0_four_chain_witness():
+    """The restatement of the knob sdpa_qk_group = 0 (src/jit/sdpa.rs:178-202):
+    emit_qk with four chains (decode.rs:59-128), the tree (c0 + c1) + (c2 +
+    c3). On the witness the default form's scores are (0, 0), so every
+    output is exactly 1/2; the four-chain scores are (2, 0), so the outputs
+    are bf16(1 / (1 + P(-2))) (the padded lanes' P(-inf) ~ 1e-38 vanish in
+    the sum)."""
+    q, k, v = _chain_witness()
+    assert L.oracle_qk_dot(ptr(q), ptr(np.ascontiguousarray(k[0])), 256) == 0.0
+    assert L.oracle_fused_qk_dot(ptr(q), ptr(np.ascontiguousarray(k[0])), 256) == 2.0
+    assert (oracle.head(q, k, v, 2, 1.0) == 0x3F00).all()                  # 0.5
+    want = bf(f32(1.0) / (f32(1.0) + f32(oracle.exp_poly(np.array([-2.0], f32))[0])))
+    assert (oracle.head(q, k, v, 2, 1.0, qk_group0=True) == want).all()
+    assert want != 0x3F00
+
+
+def test_qk_group0_node_block_equals_repeated_decode():
+    """Under sdpa_qk_group = 0 the prefill block sums its scores like the
+    four-chain head (emit_qk_block with chains = 4, prefill.rs:104-157, 780),
+    so the reference's invariant holds for it too: each row of an 8-row chunk
+    equals the head at n = past + r + 1, bit for bit. The two orders give
+    different score bits for part of the scores (the reference measured
+    96.8 % identical on its data, src/jit/sdpa.rs:190-193; 84 % on these
+    N(0,1) inputs)."""
+    w = W.make("qk0_block", heads=4, kv_heads=2, head_dim=256, rows=19, past=41, seed=5)
+    got = oracle.attention(w, form="chained_qk0", threads=2)
+    for r in range(w.rows):
+        for h in range(w.heads):
+            want = oracle.head(w.q[r, h], w.k[h // w.gqa], w.v[h // w.gqa], w.past + r + 1, w.scale,
+                               qk_group0=True)
+            assert np.array_equal(got[r, h], want), (r, h)
+    same = [L.oracle_qk_dot(ptr(np.ascontiguousarray(w.q[r, h])), ptr(np.ascontiguousarray(w.k[h // w.gqa, j])), 256)
+            == L.oracle_fused_qk_dot(ptr(np.ascontiguousarray(w.q[r, h])),
+                                     ptr(np.ascontiguousarray(w.k[h // w.gqa, j])), 256)
+            for r in range(w.rows) for h in range(w.heads) for j in range(w.past + w.rows)]
+    assert 0.5 < np.mean(same) < 0.99, np.mean(same)

@@ -6,6 +6,8 @@
     restatement of emit_fused (src/jit/target/x86/emit_sdpa/x86/decode.rs:
     501-669) under the node's selector: full 8-row chunks on the Chained
     numerics, the other rows Fused.
+  * sdpa_qk_group = 0: the unchanged (Chained) HIP output against the bits of
+    the reference's four-chain QK (src/jit/sdpa.rs:178-202);
   * AVX2: the unchanged (Chained) HIP output against the bits the reference
     emits on a host without AVX-512 BF16
     (src/jit/target/x86/emit_sdpa_avx2.rs:231-470), where every row runs the
@@ -127,6 +129,20 @@ def test_chained_output_against_avx2_bits(torch_cuda, name):
     print(f"config {name} against the AVX2 arm", flush=True)
     out = run_hsdpa(w)
     ref = oracle.attention(w, form="avx2")
+    res = assert_parity(out, ref, w, name)
+    print(name, res, flush=True)
+
+
+@pytest.mark.parametrize("name", ["decode_1k", "decode_32k", "prefill_512"])
+def test_chained_output_against_qk_group0_bits(torch_cuda, name):
+    """The default HIP path is within the parity bar of the bits the reference
+    emits under the knob sdpa_qk_group = 0 too (src/jit/sdpa.rs:178-202: the
+    QK in four chains instead of one, decode and prefill block alike; the same
+    exponentials at the row maximum)."""
+    w = W.config(name, seed=3)
+    print(f"config {name} against sdpa_qk_group = 0", flush=True)
+    out = run_hsdpa(w)
+    ref = oracle.attention(w, form="chained_qk0")
     res = assert_parity(out, ref, w, name)
     print(name, res, flush=True)
 
