@@ -748,6 +748,66 @@ hsdpa_status hsdpa_attention_static(const hsdpa_plan *plan, const hsdpa_call *ca
     return run_attention(plan, &c, nullptr, 0, static_cast<hipStream_t>(stream), true, nullptr);
 }
 
+// A decode step whose rows and past the kernels read from device memory
+// (AttentionCall's pointers, src/jit/execution/abi.rs:166-168): the decode
+// passes with their configuration derived on the device (frame_args).
+hsdpa_status hsdpa_attention_frame(const hsdpa_plan *plan, const hsdpa_frame_call *call, void *stream)
+{
+    if (!plan || !call) return HSDPA_ERR_NULL;
+    if (call->sink != 0.0f) return HSDPA_ERR_SINK_UNSUPPORTED;
+    const hsdpa_spec &s = plan->spec;
+    const int d = static_cast<int>(s.head_dim);
+    const int sub = s.gqa <= static_cast<uint64_t>(4 * hsdpa::kDecodeMaxGroup)
+                        ? hsdpa::decode_groups(static_cast<int>(s.gqa))
+                        : 0;
+    if (plan->max_rows != 1 || !hsdpa::decode_rows_ok(d) || sub == 0) return HSDPA_ERR_FRAME;
+    if (!call->q || !call->keys || !call->values || !call->output || !call->rows || !call->past ||
+        !call->workspace)
+        return HSDPA_ERR_NULL;
+    if (!aligned16(call->q) || !aligned16(call->keys) || !aligned16(call->values) || !aligned16(call->output) ||
+        !aligned16(call->workspace) || (reinterpret_cast<uintptr_t>(call->rows) & 7u) ||
+        (reinterpret_cast<uintptr_t>(call->past) & 7u) || (reinterpret_cast<uintptr_t>(call->status) & 3u))
+        return HSDPA_ERR_ALIGNMENT;
+    if (call->workspace_bytes < plan->ws_bytes) return HSDPA_ERR_WORKSPACE;
+    int cus = 0;
+    const hsdpa_status dev = check_device(&cus);
+    if (dev != HSDPA_OK) return dev;
+    char *ws = static_cast<char *>(call->workspace);
+    hsdpa::DecodeArgs a{};
+    a.q = call->q;
+    a.k = call->keys;
+    a.v = call->values;
+    a.out = call->output;
+    a.scores = reinterpret_cast<float *>(ws + plan->off_scores);
+    a.wgmax = reinterpret_cast<float *>(ws + plan->off_wgmax);
+    a.part_o = reinterpret_cast<float *>(ws + plan->off_part_o);
+    a.part_l = reinterpret_cast<float *>(ws + plan->off_part_l);
+    a.bmax = reinterpret_cast<float *>(ws + plan->off_bmax);
+    a.part_x = reinterpret_cast<float *>(ws + plan->off_part_x);
+    a.nblk = plan->dec_npad / 16;
+    a.npad = plan->dec_npad;
+    a.kv_stride = s.kv_stride;
+    a.q_head = s.q_head;
+    a.sub = sub;
+    a.g = hsdpa::decode_group_cols(static_cast<int>(s.gqa), sub);
+    a.rows = 1;
+    a.G = static_cast<int>(s.gqa);
+    a.cols = static_cast<int>(s.gqa);
+    a.q_row = s.q_row;
+    a.out_row = s.out_row;
+    a.scale = call->scale;
+    a.f_rows = call->rows;
+    a.f_past = call->past;
+    a.f_status = call->status;
+    a.f_cap = s.kv_capacity;
+    a.f_groups = static_cast<int>(plan->kv_heads) * sub;
+    a.f_cus = plan->cus;
+    a.f_loop = hsdpa::decode_pv_loop_ok(d, a.g, 1) ? 1 : 0;
+    const hipError_t e = hsdpa::launch_decode_frame(a, d, static_cast<int>(plan->kv_heads),
+                                                    plan->form == HSDPA_FORM_FUSED, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? HSDPA_OK : HSDPA_ERR_HIP;
+}
+
 hsdpa_status hsdpa_attention_route(const hsdpa_plan *plan, uint64_t rows, uint64_t past, hsdpa_route *out)
 {
     if (!plan || !out) return HSDPA_ERR_NULL;
@@ -842,6 +902,9 @@ const char *hsdpa_status_string(hsdpa_status status)
     case HSDPA_ERR_LAYOUT: return "the R16 copies of the KV cache are an AArch64 layout";
     case HSDPA_ERR_FORM: return "unknown decode form, or a Fused plan with more than 65536 query heads per KV head";
     case HSDPA_ERR_STATIC_SCRATCH: return "the plan's workspace exceeds the static scratch (HSDPA_STATIC_SCRATCH_BYTES)";
+    case HSDPA_ERR_FRAME:
+        return "the plan has no frame route (max_rows 1, head_dim 64/128/256, at most 4 equal groups of at most 16 "
+               "query heads per KV head)";
     }
     return "unknown status";
 }

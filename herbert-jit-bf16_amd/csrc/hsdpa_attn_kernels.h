@@ -37,6 +37,7 @@
 // lanes i/4 + 4k, k = 0..3. Pointing lane j at V[base + j/4][d0 + 4(j%4)]
 // hands lane i the four keys base..base+3 of dimension d0 + i.
 
+#include "hsdpa.h"
 #include "hsdpa_kernels.h"
 
 #include <type_traits>
@@ -385,12 +386,62 @@ template <int MR> struct DecodeIds {
     }
 };
 
+// A frame call (FRAME kernels, hsdpa_attention_frame): the row count and
+// past are read from device memory, as the reference's tasks read them
+// through AttentionCall's pointers (src/jit/execution/abi.rs:166-168), and
+// the decode configuration of n = past + 1 keys is derived here, by the rule
+// decode_cfg applies on the host for this grid family (one group per
+// workgroup, no short-cache or all-group forms): pass 1 takes as many tiles
+// per wave as one round of two workgroups per compute unit needs; pass 2 a
+// run of whole tiles per workgroup (at least 128 keys) that shares the
+// compute units among the groups, or 256 keys per workgroup where it cannot
+// loop. Every kernel of the call computes the same values. Returns the call's
+// status: HSDPA_OK with the arguments set (rows 1), or a status with nothing
+// to compute (rows 0: HSDPA_OK with n = 0; more rows than one, or past at the
+// capacity: a refusal).
+__device__ __forceinline__ uint32_t frame_args(DecodeArgs &a, bool &run)
+{
+    const uint64_t rows = *a.f_rows, past = *a.f_past;
+    run = false;
+    if (rows == 0) return HSDPA_OK;
+    if (rows > 1) return HSDPA_ERR_BATCH;
+    if (past >= a.f_cap) return HSDPA_ERR_CAPACITY;
+    run = true;
+    const uint64_t n = past + 1, groups = static_cast<uint64_t>(a.f_groups);
+    const uint64_t cus = static_cast<uint64_t>(a.f_cus);
+    const uint64_t nqk1 = (n + kDecodeKeysQK - 1) / kDecodeKeysQK;
+    uint64_t rq = (groups * nqk1 + 2 * cus - 1) / (2 * cus);
+    rq = rq > 1 ? rq : 1;
+    a.past = past;
+    a.n = n;
+    a.keys_qk = static_cast<int>(kDecodeKeysQK * rq);
+    a.nwg_qk = static_cast<int>((n + a.keys_qk - 1) / a.keys_qk);
+    if (a.f_loop) {
+        const uint64_t per = cus / groups > 0 ? cus / groups : 1;
+        const uint64_t tiles = (n + kKeyTile - 1) / kKeyTile;
+        const uint64_t run_keys = kKeyTile * ((tiles + per - 1) / per);
+        a.keys_pv = static_cast<int>(run_keys > 4 * kKeyTile ? run_keys : 4 * kKeyTile);
+    } else {
+        a.keys_pv = kDecodeKeysPV;
+    }
+    a.nwg_pv = static_cast<int>((n + a.keys_pv - 1) / a.keys_pv);
+    return HSDPA_OK;
+}
+
 // FUSED: also store the maximum of every 16-key block of each column (bmax):
 // the Fused form evaluates a block's exponentials at the running maximum of
-// the blocks up to it. TWO (with LOOP): exactly two tiles per wave.
-template <int D, bool LOOP, int MR = 0, bool FUSED = false, bool TWO = false, bool MG = false>
+// the blocks up to it. TWO (with LOOP): exactly two tiles per wave. FRAME:
+// rows and past read at run time (frame_args); workgroups past the visible
+// keys exit at once.
+template <int D, bool LOOP, int MR = 0, bool FUSED = false, bool TWO = false, bool MG = false, bool FRAME = false>
 __global__ __launch_bounds__(256) void decode_qk(DecodeArgs a)
 {
+    static_assert(!FRAME || (LOOP && MR == 0 && !TWO && !MG), "frame calls: one group per workgroup, looped tiles");
+    if constexpr (FRAME) {
+        bool run;
+        frame_args(a, run);
+        if (!run || static_cast<int>(blockIdx.x) >= a.nwg_qk) return;
+    }
     constexpr int KS = D / 32;
     constexpr int C = D / 8, KM = swz_group<D>() - 1;          // chunks per row, swizzle mask
     // MG: every group of the KV head in this workgroup (at most kDecodeMaxSub),
@@ -622,9 +673,15 @@ __global__ __launch_bounds__(256) void decode_qk(DecodeArgs a)
 // rescales what came before it by its corrections' product X (O and l, in
 // LOOP), and part_x receives the workgroup's product for the combine.
 // ---------------------------------------------------------------------------
-template <int D, int W, int NCB, bool LOOP = false, int MR = 0, bool FUSED = false>
+template <int D, int W, int NCB, bool LOOP = false, int MR = 0, bool FUSED = false, bool FRAME = false>
 __global__ __launch_bounds__(64 * W, D > 256 ? 1 : 8 / W) void decode_pv(DecodeArgs a)
 {
+    static_assert(!FRAME || MR == 0, "frame calls: one group per workgroup");
+    if constexpr (FRAME) {
+        bool run;
+        frame_args(a, run);
+        if (!run || static_cast<int>(blockIdx.x) >= a.nwg_pv) return;
+    }
     constexpr int THREADS = 64 * W;
     constexpr int KEYS = W * kKeyTile;                          // 256 or 128
     constexpr int PS = KEYS + 8;                                // P column stride, bf16
@@ -1272,9 +1329,16 @@ __global__ __launch_bounds__(512, 1) void decode_direct(DecodeArgs a)
 // ---------------------------------------------------------------------------
 constexpr int kCombineSubs = 8;
 
-template <int D, bool MR = false, bool FUSED = false>
+template <int D, bool MR = false, bool FUSED = false, bool FRAME = false>
 __global__ __launch_bounds__(512) void decode_combine(DecodeArgs a)
 {
+    static_assert(!FRAME || !MR, "frame calls: one row");
+    if constexpr (FRAME) {
+        bool run;
+        const uint32_t st = frame_args(a, run);
+        if (a.f_status && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) *a.f_status = st;
+        if (!run) return;
+    }
     __shared__ float ored[kCombineSubs][64];
     __shared__ float lred[kCombineSubs];
     __shared__ float xs[FUSED ? kFusedMaxSeg : 1];

@@ -69,6 +69,16 @@ struct DecodeArgs {
     float *bmax;            // [groups][g][nblk] maxima of the 16-key blocks
     float *part_x;          // [groups][nwg_pv][g] products of a workgroup's corrections
     uint64_t nblk;          // bmax row length: npad / 16
+    // A frame call (hsdpa_attention_frame, the FRAME kernels): rows and past
+    // are read from device memory at run time, and n, past, keys_qk, keys_pv,
+    // nwg_qk and nwg_pv are derived from them on the device (frame_args);
+    // unused otherwise.
+    const uint64_t *f_rows, *f_past;
+    uint32_t *f_status;     // null, or receives the call's hsdpa_status (the combine writes it)
+    uint64_t f_cap;         // the plan's KV capacity
+    int f_groups;           // kv_heads * sub
+    int f_cus;              // compute units the grids were sized for
+    int f_loop;             // 1: pass 2 walks a run of keys per workgroup (decode_pv_loop_ok)
 };
 
 // Causal prefill: `rows` query rows after `past` cached positions.
@@ -244,6 +254,9 @@ hipError_t launch_norm_rope(const NormRopeArgs &a, hipStream_t s);
 hipError_t launch_gate(const GateArgs &a, hipStream_t s);
 hipError_t launch_kv_append(const KvAppendArgs &a, bool vec, hipStream_t s);
 hipError_t launch_decode(const DecodeArgs &a, int head_dim, int kv_heads, hipStream_t s);
+// A frame call's decode passes (hsdpa_frame.hip): one row, equal groups, the
+// tuned head dimensions; the grids sized for any past below the capacity.
+hipError_t launch_decode_frame(const DecodeArgs &a, int head_dim, int kv_heads, bool fused, hipStream_t s);
 hipError_t launch_prefill(const PrefillArgs &a, int head_dim, int heads, const PrefillSplit &ps, hipStream_t s);
 // the key splits launch_prefill would choose (1: the one-workgroup kernel)
 int prefill_split_count(const PrefillArgs &a, int head_dim, int heads, const PrefillSplit &ps);

@@ -20,7 +20,7 @@ STATUS = {
     4: "HSDPA_ERR_STRIDE", 5: "HSDPA_ERR_SINK_UNSUPPORTED", 6: "HSDPA_ERR_CAPACITY",
     7: "HSDPA_ERR_WORKSPACE", 8: "HSDPA_ERR_ALIGNMENT", 9: "HSDPA_ERR_NULL", 10: "HSDPA_ERR_HIP",
     11: "HSDPA_ERR_NO_DEVICE", 12: "HSDPA_ERR_BATCH", 13: "HSDPA_ERR_LAYOUT", 14: "HSDPA_ERR_FORM",
-    15: "HSDPA_ERR_STATIC_SCRATCH",
+    15: "HSDPA_ERR_STATIC_SCRATCH", 16: "HSDPA_ERR_FRAME",
 }
 STATIC_SCRATCH_BYTES = 32 << 20
 FORMS = {"chained": 0, "fused": 1}
@@ -29,7 +29,8 @@ KERNELS = {0: "none", 1: "decode", 2: "few_rows", 3: "causal", 4: "causal_split"
 EXPORTS = ["hsdpa_plan_create", "hsdpa_plan_destroy", "hsdpa_workspace_bytes", "hsdpa_attention",
            "hsdpa_status_string", "hsdpa_version", "hsdpa_kv_check", "hsdpa_kv_append",
            "hsdpa_head_norm_rope", "hsdpa_output_gate", "hsdpa_kv_restore", "hsdpa_kv_take",
-           "hsdpa_attention_layer", "hsdpa_attention_route", "hsdpa_attention_static"]
+           "hsdpa_attention_layer", "hsdpa_attention_route", "hsdpa_attention_static",
+           "hsdpa_attention_frame"]
 
 
 class HsdpaError(RuntimeError):
@@ -52,6 +53,14 @@ class Call(ctypes.Structure):
                 ("output", ctypes.c_void_p), ("rows", ctypes.c_uint64), ("past", ctypes.c_uint64),
                 ("scale", ctypes.c_float), ("sink", ctypes.c_float), ("workspace", ctypes.c_void_p),
                 ("workspace_bytes", ctypes.c_uint64)]
+
+
+class FrameCall(ctypes.Structure):
+    """hsdpa_frame_call: rows and past as device pointers (AttentionCall, abi.rs:156-180)."""
+    _fields_ = [("q", ctypes.c_void_p), ("keys", ctypes.c_void_p), ("values", ctypes.c_void_p),
+                ("output", ctypes.c_void_p), ("rows", ctypes.c_void_p), ("past", ctypes.c_void_p),
+                ("scale", ctypes.c_float), ("sink", ctypes.c_float), ("workspace", ctypes.c_void_p),
+                ("workspace_bytes", ctypes.c_uint64), ("status", ctypes.c_void_p)]
 
 
 class Route(ctypes.Structure):
@@ -149,6 +158,8 @@ def library():
         L.hsdpa_attention_route.restype = ctypes.c_int
         L.hsdpa_attention_static.argtypes = [ctypes.c_void_p, ctypes.POINTER(Call), ctypes.c_void_p]
         L.hsdpa_attention_static.restype = ctypes.c_int
+        L.hsdpa_attention_frame.argtypes = [ctypes.c_void_p, ctypes.POINTER(FrameCall), ctypes.c_void_p]
+        L.hsdpa_attention_frame.restype = ctypes.c_int
         _lib = L
     return _lib
 

@@ -83,8 +83,11 @@ typedef enum hsdpa_status {
     HSDPA_ERR_FORM = 14,            /* an unknown decode form (the knob's parse, knobs.rs:66-68),
                                        or a Fused plan with more than 65 536 query heads per
                                        KV head (more padded decode groups than a grid holds) */
-    HSDPA_ERR_STATIC_SCRATCH = 15   /* hsdpa_attention_static: the plan's workspace exceeds
+    HSDPA_ERR_STATIC_SCRATCH = 15,  /* hsdpa_attention_static: the plan's workspace exceeds
                                        HSDPA_STATIC_SCRATCH_BYTES */
+    HSDPA_ERR_FRAME = 16            /* hsdpa_attention_frame: the plan has no frame route (it needs
+                                       max_rows = 1, head_dim 64, 128 or 256, and query heads per KV
+                                       head in at most 4 equal groups of at most 16) */
 } hsdpa_status;
 
 /* The decode head form (SdpaForm, src/jit/ir.rs:100-115; the knob
@@ -206,6 +209,43 @@ hsdpa_status hsdpa_attention(const hsdpa_plan *plan, const hsdpa_call *call, voi
  * threads enqueueing at once) race on it; stream-ordered calls do not. */
 #define HSDPA_STATIC_SCRATCH_BYTES (32u << 20)
 hsdpa_status hsdpa_attention_static(const hsdpa_plan *plan, const hsdpa_call *call, void *stream);
+
+/* ---- A decode step whose rows and past are read at run time ----------------
+ * The reference's AttentionCall holds rows and past as pointers into the
+ * frame, read by each task when it runs (src/jit/execution/abi.rs:156-180,
+ * read at attention.rs:122-130), so that one generated program serves every
+ * call. hsdpa_frame_call does the same on the device: *rows and *past are read
+ * by the kernels, so one enqueued sequence (or one captured HIP graph) serves
+ * successive decode steps as past grows, with nothing re-enqueued on the host.
+ * The grids are sized for any past below kv_capacity; the workgroups past the
+ * visible keys exit at once.
+ *
+ * Plans: decode-only (max_rows = 1), head_dim 64, 128 or 256, and at most 64
+ * query heads per KV head in at most 4 equal groups of at most 16 (otherwise
+ * HSDPA_ERR_FRAME); either form. Values read at run time: *rows = 0 computes
+ * nothing; *rows = 1 is one decode row with n = *past + 1 keys; *rows > 1 or
+ * *past >= kv_capacity compute nothing and report HSDPA_ERR_BATCH or
+ * HSDPA_ERR_CAPACITY through *status. The outputs are those of hsdpa_attention
+ * on the same values, up to the key partition across workgroups, which here
+ * follows n rather than the host's choice. */
+typedef struct hsdpa_frame_call {
+    const uint16_t *q;        /* as hsdpa_call */
+    const uint16_t *keys;
+    const uint16_t *values;
+    uint16_t *output;
+    const uint64_t *rows;     /* device memory, 8-byte aligned: read when the kernels run */
+    const uint64_t *past;     /* device memory, 8-byte aligned: read when the kernels run */
+    float scale;
+    float sink;               /* must be 0 */
+    void *workspace;          /* device scratch of at least hsdpa_workspace_bytes() */
+    uint64_t workspace_bytes;
+    uint32_t *status;         /* device memory or NULL: receives the step's hsdpa_status when it runs */
+} hsdpa_frame_call;
+
+/* Enqueue the three decode passes of a frame call on `stream`. Host checks
+ * (the plan's frame route, pointers, alignment, workspace) before any launch;
+ * the checks of *rows and *past happen on the device. */
+hsdpa_status hsdpa_attention_frame(const hsdpa_plan *plan, const hsdpa_frame_call *call, void *stream);
 
 /* ---- KV append: the node before the attention ------------------------------
  * The keys and values of the current block, token-major (row r, KV head h at

@@ -45,7 +45,7 @@ def test_library_has_gfx950_code():
 
 def test_status_strings_and_version():
     lib = hsdpa.library()
-    for code in range(16):
+    for code in range(17):
         assert lib.hsdpa_status_string(code) != b"unknown status", code
     assert lib.hsdpa_version() >= 200
 
@@ -203,6 +203,36 @@ def _name(rc):
     return binding.STATUS[rc]
 
 
+def _frame(plan, rows=0x60000, past=0x60008, status=0, **kw):
+    f = dict(q=0x10000, keys=0x20000, values=0x30000, output=0x40000, rows=rows, past=past, scale=0.0625,
+             sink=0.0, workspace=0x50000, workspace_bytes=plan.workspace_bytes, status=status)
+    f.update(kw)
+    c = binding.FrameCall(**f)
+    return _name(hsdpa.library().hsdpa_attention_frame(plan.handle, ctypes.byref(c), None))
+
+
+def test_frame_call_refusals_before_any_device_work():
+    """hsdpa_attention_frame takes decode-only plans at head_dim 64, 128 and
+    256 with equal decode groups; everything else is refused on the host
+    before any launch, as are missing pointers, misalignment and a short
+    workspace (rows and past are only read on the device)."""
+    assert _frame(hsdpa.Plan(16, 8, 256, 4096)) == "HSDPA_ERR_FRAME"                   # any rows
+    assert _frame(hsdpa.Plan(16, 8, 96, 4096, max_rows=1)) == "HSDPA_ERR_FRAME"        # untuned head_dim
+    assert _frame(hsdpa.Plan(17, 17, 128, 4096, max_rows=1)) == "HSDPA_ERR_FRAME"      # padded groups
+    assert _frame(hsdpa.Plan(100, 100, 128, 4096, max_rows=1)) == "HSDPA_ERR_FRAME"    # more than 4 groups
+    p = hsdpa.Plan(16, 8, 256, 4096, max_rows=1)
+    assert _frame(p, rows=0) == "HSDPA_ERR_NULL"
+    assert _frame(p, past=0) == "HSDPA_ERR_NULL"
+    assert _frame(p, rows=0x60004) == "HSDPA_ERR_ALIGNMENT"
+    assert _frame(p, status=0x60002) == "HSDPA_ERR_ALIGNMENT"
+    assert _frame(p, q=0x10008) == "HSDPA_ERR_ALIGNMENT"
+    assert _frame(p, workspace_bytes=p.workspace_bytes - 1) == "HSDPA_ERR_WORKSPACE"
+    assert _frame(p, sink=1.0) == "HSDPA_ERR_SINK_UNSUPPORTED"
+    # every check passed: with no GPU the device check refuses
+    assert _frame(p) == "HSDPA_ERR_NO_DEVICE"
+    assert _frame(hsdpa.Plan(64, 32, 128, 4096, max_rows=1, form="fused")) == "HSDPA_ERR_NO_DEVICE"
+
+
 def test_call_refusals_before_any_device_work():
     p = hsdpa.Plan(16, 8, 256, 100)
     assert _name(_call(p, rows=0)) == "HSDPA_OK"                     # the empty call is a no-op
@@ -261,6 +291,7 @@ RECORDS = {
     "hsdpa_kv_call": binding.KvCall, "hsdpa_norm_rope_spec": binding.NormRopeSpec,
     "hsdpa_norm_rope_call": binding.NormRopeCall, "hsdpa_gate_spec": binding.GateSpec,
     "hsdpa_gate_call": binding.GateCall, "hsdpa_layer_call": binding.LayerCall, "hsdpa_route": binding.Route,
+    "hsdpa_frame_call": binding.FrameCall,
 }
 
 
