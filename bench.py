@@ -295,6 +295,129 @@ def bench_config(torch, hsdpa, W, name, kind, steps, warmup, form="chained"):
                          "kernel": PREFILL_KERNELS[name]}}
 
 
+def bench_prefill_passes(torch, hsdpa, W, name, steps, warmup, rows_per_pass=256):
+    """The chunk as the reference engine sends it to the attention node:
+    passes of at most 256 rows (prefill_pass, src/jit/schedule.rs:290-298,
+    bounded by max_batch, src/jit/model/mounted.rs:185-187), each a call
+    after the rows before it (4096 rows after 8192 keys: 16 calls after 8192,
+    8448, ..., 12032 keys), one plan with max_rows = 256. `steps` chunks are
+    captured into one HIP graph. Returns the record (TFLOP/s over the chunk)."""
+    w = W.config(name, seed=0)
+    q, ks, vs, out = device_buffers(torch, w, copies=1)
+    plan = hsdpa.Plan(w.heads, w.gqa, w.head_dim, w.capacity, max_rows=rows_per_pass)
+    ws = torch.empty(plan.workspace_bytes, dtype=torch.uint8, device="cuda")
+    passes = [(r0, min(rows_per_pass, w.rows - r0)) for r0 in range(0, w.rows, rows_per_pass)]
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    qrow_b, orow_b = 2 * w.q_row, 2 * w.out_row
+
+    def chunk():
+        for r0, rows in passes:
+            plan.attention_raw(q.data_ptr() + r0 * qrow_b, ks[0].data_ptr(), vs[0].data_ptr(),
+                               out.data_ptr() + r0 * orow_b, rows, w.past + r0, w.scale, ws.data_ptr(), ws.numel(),
+                               stream.cuda_stream)
+
+    with torch.cuda.stream(stream):
+        for _ in range(warmup):
+            chunk()
+    torch.cuda.synchronize()
+    eager = out.clone()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        for _ in range(steps):
+            chunk()
+    torch.cuda.synchronize()
+    out.zero_()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        start.record(stream)
+        graph.replay()
+        end.record(stream)
+    torch.cuda.synchronize()
+    if not torch.equal(eager, out):
+        print(f"{name} in passes: graph replay differs from the eager calls", file=sys.stderr)
+        sys.exit(3)
+    ms = start.elapsed_time(end) / steps
+    kernels = sorted({plan.route(rows, w.past + r0)["main"] for r0, rows in passes})
+    launches = sum(plan.route(rows, w.past + r0)["launches"] for r0, rows in passes)
+    flops = w.prefill_flops()
+    val = flops / (ms * 1e-3) / 1e12
+    log(f"{name} in {len(passes)} passes of {rows_per_pass} rows: {ms*1e3:.2f} us/chunk, {val:.1f} TFLOP/s "
+        f"({val/MFMA_BF16_PEAK_TFS:.1%} of MFMA peak), kernels {kernels}, {launches} launches")
+    del q, ks, vs, out, ws
+    torch.cuda.empty_cache()
+    return {"value": round(val, 2), "unit": "TFLOP/s", "ms_per_chunk": round(ms, 5), "steps": steps,
+            "passes": len(passes), "rows_per_pass": rows_per_pass, "kernels": kernels, "launches": launches,
+            "frac": round(val / MFMA_BF16_PEAK_TFS, 4),
+            "workload": f"the {w.rows}-row chunk as {len(passes)} sequential hsdpa_attention calls of "
+                        f"{rows_per_pass} rows after {w.past}, {w.past + rows_per_pass}, ... keys (the reference "
+                        f"engine's prefill passes), one HIP graph of {steps} chunks"}
+
+
+def bench_frame(torch, hsdpa, W, name, steps, warmup):
+    """Decode through hsdpa_attention_frame (rows and past read from device
+    memory by the kernels): a HIP graph of `steps` frame calls over distinct
+    caches (at least 1 GiB), as the other decode timings rotate theirs."""
+    w = W.config(name, seed=0)
+    per_cache = 2 * w.kv_heads * w.capacity * w.head_dim * 2
+    copies = max(4, -(-(1 << 30) // per_cache))
+    q, ks, vs, out = device_buffers(torch, w, copies=copies)
+    plan = hsdpa.Plan(w.heads, w.gqa, w.head_dim, w.capacity, max_rows=1)
+    ws = torch.empty(plan.workspace_bytes, dtype=torch.uint8, device="cuda")
+    vals = torch.tensor([1, w.past], dtype=torch.int64, device="cuda")
+    status = torch.zeros(1, dtype=torch.int32, device="cuda")
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+
+    def call(i):
+        plan.attention_frame_raw(q.data_ptr(), ks[i % copies].data_ptr(), vs[i % copies].data_ptr(), out.data_ptr(),
+                                 vals.data_ptr(), vals.data_ptr() + 8, w.scale, ws.data_ptr(), ws.numel(),
+                                 status.data_ptr(), stream.cuda_stream)
+
+    with torch.cuda.stream(stream):
+        for i in range(warmup):
+            call(i)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        for i in range(steps):
+            call(i)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        start.record(stream)
+        graph.replay()
+        end.record(stream)
+    torch.cuda.synchronize()
+    if int(status.item()) != 0:
+        print(f"{name} frame: status {int(status.item())}", file=sys.stderr)
+        sys.exit(3)
+    ms = start.elapsed_time(end) / steps
+    val = w.decode_bytes() / (ms * 1e-3) / 1e9
+    log(f"{name} frame call: {ms*1e3:.2f} us/step, {val:.1f} GB/s")
+    del q, ks, vs, out, ws
+    torch.cuda.empty_cache()
+    return {"us": round(ms * 1e3, 2), "GB/s": round(val, 1), "frac": round(val / HBM_PEAK_GBS, 4)}
+
+
+def cpu_config_baseline(w, kind, threads, runs=5):
+    """The AVX-512 BF16 restatement on this host for one configuration, the
+    whole call (a decode uses min(threads, Hq) workers: the reference's decode
+    node has Hq tasks). Median of `runs` after one warm-up."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle
+
+    used = min(threads, w.heads) if kind == "decode" else threads
+    med = median_time(lambda: oracle.attention(w, "avx512", threads=used), 1, runs)
+    if kind == "decode":
+        val, unit = w.decode_bytes() / med / 1e9, "GB/s"
+    else:
+        val, unit = w.prefill_flops() / med / 1e12, "TFLOP/s"
+    return {"value": round(val, 4), "unit": unit, "cores": used, "kind": "port",
+            "sample": f"the whole call, {runs} runs after 1 warm-up, median {med*1e3:.2f} ms"}
+
+
 def cpu_baseline(w_decode):
     """Time the AVX-512 BF16 restatement of the reference on this host: the
     reference's decode node has Hq tasks, so it uses min(cores, Hq) threads;
@@ -404,7 +527,15 @@ def main():
     }
     if "prefill_4096_after_8192" in configs:
         result["prefill"] = configs["prefill_4096_after_8192"]
+        # the same chunk as the reference engine sends it: passes of 256 rows
+        configs["prefill_4096_after_8192"]["engine_passes"] = bench_prefill_passes(
+            torch, hsdpa, W, "prefill_4096_after_8192", psteps, min(args.warmup, 3))
     result["configs"] = configs
+    # the headline decode through the frame entry (rows and past read on the device)
+    if not args.only or "decode_32k" in args.only:
+        result["frame"] = {"decode_32k": bench_frame(torch, hsdpa, W, "decode_32k", args.steps, args.warmup),
+                           "entry": "hsdpa_attention_frame: the kernels read rows and past from device memory "
+                                    "and derive their key partition from them; graph of the timed steps"}
     # the decode configurations under the reference's Fused form (plan form =
     # HSDPA_FORM_FUSED), beside the Chained default above
     if not args.no_fused:
@@ -491,11 +622,23 @@ def main():
         if cb is None:
             result["cpu_baseline"] = {"value": None, "unit": "GB/s", "cores": 0, "kind": "port", "sample": why}
         else:
-            result["cpu_baseline"] = cb
-            if wp_cpu is not None:
-                import oracle
+            import oracle
 
-                result["prefill"]["cpu_baseline"] = cpu_prefill_sample(wp_cpu, oracle.lib().oracle_physical_cores())
+            result["cpu_baseline"] = cb
+            cores = oracle.lib().oracle_physical_cores()
+            if wp_cpu is not None:
+                result["prefill"]["cpu_baseline"] = cpu_prefill_sample(wp_cpu, cores)
+            # every configuration's own CPU figure beside its GPU one (the
+            # 4096-row chunk: the bounded sample above; the headline: above)
+            for name, rec in configs.items():
+                if name == "decode_32k":
+                    rec["cpu_baseline"] = {k: cb[k] for k in ("value", "unit", "cores", "kind", "sample")}
+                elif name == "prefill_4096_after_8192":
+                    rec["cpu_baseline"] = result["prefill"]["cpu_baseline"]
+                else:
+                    kind = "prefill" if name.startswith("prefill") else "decode"
+                    rec["cpu_baseline"] = cpu_config_baseline(W.config(name, seed=0), kind, cores)
+                log(f"{name} cpu: {rec['cpu_baseline']['value']} {rec['cpu_baseline']['unit']}")
     print(json.dumps(result), flush=True)
 
 

@@ -391,8 +391,9 @@ template <int MR> struct DecodeIds {
 // through AttentionCall's pointers (src/jit/execution/abi.rs:166-168), and
 // the decode configuration of n = past + 1 keys is derived here, by the rule
 // decode_cfg applies on the host for this grid family (one group per
-// workgroup, no short-cache or all-group forms): pass 1 takes as many tiles
-// per wave as one round of two workgroups per compute unit needs; pass 2 a
+// workgroup, no short-cache or all-group forms): pass 1 takes decode_cfg's
+// tiles per wave (at least as many as one round of two workgroups per
+// compute unit needs); pass 2 a
 // run of whole tiles per workgroup (at least 128 keys) that shares the
 // compute units among the groups, or 256 keys per workgroup where it cannot
 // loop. Every kernel of the call computes the same values. Returns the call's
@@ -410,8 +411,24 @@ __device__ __forceinline__ uint32_t frame_args(DecodeArgs &a, bool &run)
     const uint64_t n = past + 1, groups = static_cast<uint64_t>(a.f_groups);
     const uint64_t cus = static_cast<uint64_t>(a.f_cus);
     const uint64_t nqk1 = (n + kDecodeKeysQK - 1) / kDecodeKeysQK;
-    uint64_t rq = (groups * nqk1 + 2 * cus - 1) / (2 * cus);
-    rq = rq > 1 ? rq : 1;
+    // decode_cfg's rule: two tiles per wave at least once one per wave
+    // needs more than one workgroup per compute unit, as many as one round
+    // of two per unit needs, then the count up to twice that which leaves
+    // the fewest tiles on the busiest unit
+    const uint64_t rounds = (groups * nqk1 + 2 * cus - 1) / (2 * cus);
+    uint64_t rq = groups * nqk1 > cus && rounds < 2 ? 2 : rounds > 1 ? rounds : 1;
+    if (rq > 1) {
+        uint64_t best = rq, cost = ~uint64_t{0};
+        for (uint64_t r = rq; r <= 2 * rq; r++) {
+            const uint64_t wgs = groups * ((nqk1 + r - 1) / r);
+            const uint64_t cc = (wgs + cus - 1) / cus * r;
+            if (cc < cost) {
+                cost = cc;
+                best = r;
+            }
+        }
+        rq = best;
+    }
     a.past = past;
     a.n = n;
     a.keys_qk = static_cast<int>(kDecodeKeysQK * rq);

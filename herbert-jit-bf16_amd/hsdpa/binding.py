@@ -208,6 +208,16 @@ class Plan:
         if rc != 0:
             raise HsdpaError(rc, "hsdpa_attention")
 
+    def attention_frame_raw(self, q: int, keys: int, values: int, output: int, rows_ptr: int, past_ptr: int,
+                            scale: float, workspace: int, workspace_bytes: int, status_ptr: int = 0,
+                            stream: int = 0) -> None:
+        """hsdpa_attention_frame: rows and past are device pointers the kernels read."""
+        call = FrameCall(q, keys, values, output, rows_ptr, past_ptr, scale, 0.0, workspace, workspace_bytes,
+                         status_ptr)
+        rc = library().hsdpa_attention_frame(self._h, ctypes.byref(call), ctypes.c_void_p(stream))
+        if rc != 0:
+            raise HsdpaError(rc, "hsdpa_attention_frame")
+
     def close(self) -> None:
         if self._h:
             library().hsdpa_plan_destroy(self._h)

@@ -103,6 +103,7 @@ CASES = [
     ("prefill_qwen_512_after_1000", 16, 2, 256, 512, 1000, 1600, True, 64),
     ("prefill_short_gated_96_after_160", 16, 2, 256, 96, 160, 300, True, 64),
     ("decode_ungated_d128_g4", 8, 2, 128, 1, 300, 400, False, 128),
+    ("decode_direct_gated_qwen_1k", 16, 2, 256, 1, 1023, 1100, True, 64),       # pass 2 gates the outputs
     ("prefill_ragged_d64_g2", 8, 4, 64, 70, 33, 200, True, 32),
     ("decode_g16_no_rope", 16, 1, 256, 1, 5000, 5100, True, 0),
     ("decode_g32_two_groups", 32, 1, 128, 1, 700, 800, True, 64),

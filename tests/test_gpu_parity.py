@@ -27,6 +27,11 @@ SMALL = [
     ("decode_direct_d256_n700_g3_kv5", 15, 5, 256, 1, 699, "decode"),
     ("decode_direct_d256_g16_n200", 32, 2, 256, 1, 199, "decode"),               # two P column blocks
     ("decode_direct_d128_g12_n300", 12, 1, 128, 1, 299, "decode"),
+    # more of them: partial tiles, odd groups
+    ("decode_direct_d256_n17_g7", 7, 1, 256, 1, 16, "decode"),
+    ("decode_direct_d128_n257_g5_kv3", 15, 3, 128, 1, 256, "decode"),
+    ("decode_direct_d64_n512_g2", 4, 2, 64, 1, 511, "decode"),
+    ("decode_direct_d256_n1000_g6", 12, 2, 256, 1, 999, "decode"),
     ("prefill_d256_r2_g80", 160, 2, 256, 2, 0, "causal"),             # 160 columns: past the decode kernels
     ("prefill_d256_r19_p37", 8, 2, 256, 19, 37, "causal"),
     ("prefill_d128_r70_p5", 8, 8, 128, 70, 5, "causal"),
@@ -243,3 +248,33 @@ def test_gqa_groups(torch_cuda, case):
     ref = oracle.attention(w)
     r = assert_parity(out, ref, w, name)
     print(name, r, flush=True)
+
+
+def test_prefill_4096_as_engine_passes(torch_cuda):
+    """The 4096-row chunk after 8192 keys as the reference engine sends it to
+    the attention node: 16 calls of 256 rows after 8192, 8448, ... keys
+    (prefill_pass, src/jit/schedule.rs:290-298), on a plan with max_rows 256.
+    The oracle's rows do not depend on how the chunk is cut (it runs passes of
+    256 rows itself), so the whole output meets the bar against it."""
+    import torch
+
+    if not oracle.avx512_available():
+        pytest.skip("host lacks AVX-512 BF16: the scalar oracle is too slow at this size")
+    w = W.config("prefill_4096_after_8192", seed=5)
+    plan = hsdpa.Plan(w.heads, w.gqa, w.head_dim, w.capacity, max_rows=256)
+    dev = torch.device("cuda")
+    q = torch.from_numpy(np.ascontiguousarray(w.q).view(np.int16)).to(dev)
+    k = torch.from_numpy(np.ascontiguousarray(w.k).view(np.int16)).to(dev)
+    v = torch.from_numpy(np.ascontiguousarray(w.v).view(np.int16)).to(dev)
+    out = torch.full((w.rows, w.heads, w.head_dim), -1, dtype=torch.int16, device=dev)
+    ws = torch.empty(plan.workspace_bytes, dtype=torch.uint8, device=dev)
+    stream = torch.cuda.current_stream().cuda_stream
+    for r0 in range(0, w.rows, 256):
+        print(f"pass rows {r0}..{r0 + 255} after {w.past + r0}: {plan.route(256, w.past + r0)['main']}", flush=True)
+        plan.attention_raw(q.data_ptr() + 2 * r0 * w.q_row, k.data_ptr(), v.data_ptr(),
+                           out.data_ptr() + 2 * r0 * w.out_row, 256, w.past + r0, w.scale, ws.data_ptr(),
+                           plan.workspace_bytes, stream)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy().view(np.uint16)
+    r = assert_parity(got, oracle.attention(w, "avx512"), w, "prefill_4096_passes")
+    print("prefill_4096_passes", r, flush=True)
