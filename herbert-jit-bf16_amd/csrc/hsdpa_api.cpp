@@ -802,7 +802,13 @@ hsdpa_status hsdpa_attention_frame(const hsdpa_plan *plan, const hsdpa_frame_cal
     a.f_cap = s.kv_capacity;
     a.f_groups = static_cast<int>(plan->kv_heads) * sub;
     a.f_cus = plan->cus;
-    a.f_loop = hsdpa::decode_pv_loop_ok(d, a.g, 1) ? 1 : 0;
+    // pass 2 walks runs of keys where it can and where 256-key workgroups
+    // would not fit the compute units in one round at the capacity
+    const uint64_t nch_cap = (s.kv_capacity + hsdpa::kDecodeKeysPV - 1) / hsdpa::kDecodeKeysPV;
+    a.f_loop = hsdpa::decode_pv_loop_ok(d, a.g, 1) &&
+                       static_cast<uint64_t>(a.f_groups) * nch_cap > static_cast<uint64_t>(plan->cus)
+                   ? 1
+                   : 0;
     const hipError_t e = hsdpa::launch_decode_frame(a, d, static_cast<int>(plan->kv_heads),
                                                     plan->form == HSDPA_FORM_FUSED, static_cast<hipStream_t>(stream));
     return e == hipSuccess ? HSDPA_OK : HSDPA_ERR_HIP;

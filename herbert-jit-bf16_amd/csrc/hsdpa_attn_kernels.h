@@ -395,8 +395,9 @@ template <int MR> struct DecodeIds {
 // tiles per wave (at least as many as one round of two workgroups per
 // compute unit needs); pass 2 a
 // run of whole tiles per workgroup (at least 128 keys) that shares the
-// compute units among the groups, or 256 keys per workgroup where it cannot
-// loop. Every kernel of the call computes the same values. Returns the call's
+// compute units among the groups, or (f_loop 0: every past below the
+// capacity fits one round of them, or the run cannot loop) 256 keys per
+// workgroup. Every kernel of the call computes the same values. Returns the call's
 // status: HSDPA_OK with the arguments set (rows 1), or a status with nothing
 // to compute (rows 0: HSDPA_OK with n = 0; more rows than one, or past at the
 // capacity: a refusal).

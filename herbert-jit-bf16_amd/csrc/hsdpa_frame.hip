@@ -36,12 +36,13 @@ static hipError_t frame_d(const DecodeArgs &a, int kv_heads, hipStream_t s)
         e = a.g <= 8 ? launch(decode_pv<D, 8, 1, true, 0, FUSED, true>, gpv, dim3(512), s, a)
                      : launch(decode_pv<D, 8, 2, true, 0, FUSED, true>, gpv, dim3(512), s, a);
     } else {
-        // 256 keys per workgroup (D = 256 with more than 8 heads per group)
+        // 256 keys per workgroup: where every past below the capacity fits one
+        // round of them (the host's choice up to that length, faster there
+        // than a one-chunk run), or where the run cannot loop (D = 256 with
+        // more than 8 heads per group)
         const dim3 gpv(static_cast<unsigned>((cap + kDecodeKeysPV - 1) / kDecodeKeysPV), kv_heads, a.sub);
-        if constexpr (D == 256)
-            e = launch(decode_pv<D, 8, 2, false, 0, FUSED, true>, gpv, dim3(512), s, a);
-        else
-            return hipErrorInvalidValue;                    // decode_pv_loop_ok holds below D = 256
+        e = a.g <= 8 ? launch(decode_pv<D, 8, 1, false, 0, FUSED, true>, gpv, dim3(512), s, a)
+                     : launch(decode_pv<D, 8, 2, false, 0, FUSED, true>, gpv, dim3(512), s, a);
     }
     if (e != hipSuccess) return e;
     return launch(decode_combine<D, false, FUSED, true>, dim3(kv_heads * a.sub * a.g, (D + 63) / 64),
