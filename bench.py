@@ -52,16 +52,16 @@ MFMA_BF16_PEAK_TFS = 2500.0  # MI355X dense bf16 MFMA, TFLOP/s
 # Summary and commands: profiles/pmc_traffic_bench_configs.md
 TRAFFIC_BYTES = {
     "chained": {
-        "decode_1k": (2 * (564.1 + 2249.6) + (34.0 + 4.0)) * 1024,
-        "decode_32k": (2 * (16467.5 + 17514.3 + 1090.5) + (2112.0 + 2056.0 + 8.0)) * 1024,
+        "decode_1k": (2 * (564.4 + 2243.1) + (34.0 + 4.0)) * 1024,
+        "decode_32k": (2 * (16464.7 + 17504.8 + 1090.5) + (2112.0 + 2056.0 + 8.0)) * 1024,
         "prefill_512": (2 * 8605.7 + 4096.0) * 1024,
-        "prefill_4096_after_8192": (2 * (72934.6 + 148666.9 + 31024.8) + (376.0 + 87312.9 + 15360.0)) * 1024,
-        "decode_128k_outliers": (2 * (65627.9 + 69783.0 + 1090.5) + (8320.2 + 2056.0 + 8.0)) * 1024,
+        "prefill_4096_after_8192": (2 * (72934.9 + 149439.2 + 31019.6) + (376.0 + 87294.3 + 15360.0)) * 1024,
+        "decode_128k_outliers": (2 * (65628.1 + 69784.6 + 1090.5) + (8320.2 + 2056.0 + 8.0)) * 1024,
     },
     "fused": {
-        "decode_1k": (2 * (565.6 + 2276.0) + (36.0 + 4.0)) * 1024,
-        "decode_32k": (2 * (16476.1 + 17540.6 + 1130.6) + (2240.0 + 2064.0 + 8.0)) * 1024,
-        "decode_128k_outliers": (2 * (65633.9 + 69804.7 + 1130.6) + (8832.3 + 6672.0 + 8.0)) * 1024,
+        "decode_1k": (2 * (569.7 + 2277.6) + (36.0 + 4.0)) * 1024,
+        "decode_32k": (2 * (16472.7 + 17543.2 + 1126.0) + (2240.0 + 2064.0 + 8.0)) * 1024,
+        "decode_128k_outliers": (2 * (65638.5 + 69812.1 + 1126.0) + (8832.2 + 6672.0 + 8.0)) * 1024,
     },
 }
 
