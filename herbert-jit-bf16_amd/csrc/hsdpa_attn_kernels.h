@@ -920,8 +920,11 @@ __global__ __launch_bounds__(64 * W, D > 256 ? 1 : 8 / W) void decode_pv(DecodeA
         //    LOOP the next chunk's V registers are live here, so the operands
         //    come in two halves of the tiles, in quarters at D = 256 (the
         //    halves spilled 29 registers under the Fused form: 128K keys on
-        //    16/2 heads 77.5 -> 71.2 us Fused, 48K 30.0 -> 29.2 us Chained).
-        constexpr int PH = LOOP && D == 256 && TPP % 4 == 0 ? 4 : LOOP && TPP % 2 == 0 ? 2 : 1, TPH = TPP / PH;
+        //    16/2 heads 77.5 -> 71.2 us Fused, 48K 30.0 -> 29.2 us Chained),
+        //    in eighths under the Fused form at D = 256 (quarters spilled 9
+        //    registers there, and each reload waited for the next chunk's V
+        //    loads: 128K keys 69.8 -> 68.5 us).
+        constexpr int PH = FUSED && LOOP && D == 256 && TPP % 8 == 0 ? 8 : LOOP && D == 256 && TPP % 4 == 0 ? 4 : LOOP && TPP % 2 == 0 ? 2 : 1, TPH = TPP / PH;
 #pragma unroll
         for (int ph = 0; ph < PH; ph++) {
             u32x4 bp[TPH][NCB], av[TPH][DBW];
@@ -1374,8 +1377,24 @@ __global__ __launch_bounds__(512) void decode_combine(DecodeArgs a)
         float carry = 1.0f;                 // product over the workgroups after the segment
         for (int s1 = a.nwg_pv; s1 > 0; s1 -= kFusedMaxSeg) {
             const int s0 = s1 > kFusedMaxSeg ? s1 - kFusedMaxSeg : 0, cnt = s1 - s0;
+            // the segment's products first, then its first batch of partials,
+            // so that the partials arrive while the products are scanned (one
+            // round trip instead of two)
+            const float xv = tid < cnt ? a.part_x[base + static_cast<uint64_t>(s0 + tid) * a.g] : 1.0f;
+            float xo[BATCH], xl[BATCH];
+            auto load_batch = [&](int w0) {
+#pragma unroll
+                for (int b = 0; b < BATCH; b++) {
+                    const int w = w0 + kCombineSubs * b;
+                    const uint64_t part = base + static_cast<uint64_t>(w < s1 ? w : s0) * a.g;
+                    xo[b] = a.part_o[part * D + dim];
+                    xl[b] = a.part_l[part];
+                }
+            };
+            int w0 = s0 + sub;
+            load_batch(w0);
             __syncthreads();                // the previous segment's xs is read
-            if (tid < cnt) xs[tid] = a.part_x[base + static_cast<uint64_t>(s0 + tid) * a.g];
+            if (tid < cnt) xs[tid] = xv;
             __syncthreads();
             // xs[i] <- the product of xs[i .. cnt-1]
             for (int off = 1; off < cnt; off *= 2) {
@@ -1384,15 +1403,8 @@ __global__ __launch_bounds__(512) void decode_combine(DecodeArgs a)
                 if (tid < cnt) xs[tid] = xs[tid] * y;
                 __syncthreads();
             }
-            for (int w0 = s0 + sub; w0 < s1; w0 += kCombineSubs * BATCH) {
-                float xo[BATCH], xl[BATCH];
-#pragma unroll
-                for (int b = 0; b < BATCH; b++) {
-                    const int w = w0 + kCombineSubs * b;
-                    const uint64_t part = base + static_cast<uint64_t>(w < s1 ? w : s0) * a.g;
-                    xo[b] = a.part_o[part * D + dim];
-                    xl[b] = a.part_l[part];
-                }
+            for (; w0 < s1; w0 += kCombineSubs * BATCH) {
+                if (w0 != s0 + sub) load_batch(w0);
 #pragma unroll
                 for (int b = 0; b < BATCH; b++) {
                     const int i = w0 + kCombineSubs * b - s0;

@@ -7,10 +7,10 @@
 // The GPU keeps the two passes of the Chained kernels (scores first, then the
 // exponentials and P.V), because the exponentials must be evaluated where the
 // reference evaluates them: at each block's running maximum, which depends on
-// every key before the block. Pass 1 also stores the block maxima; pass 2
-// computes each block's running maximum and correction; the combine applies
-// the corrections of the later workgroups (decode_qk, decode_pv and
-// decode_combine with FUSED in hsdpa_attn_kernels.h). Head dimensions 32 to
+// every key before the block. Pass 1 also stores the block maxima where pass
+// 2 reads them; pass 2 computes each block's running maximum and correction;
+// the combine applies the corrections of the later workgroups (decode_qk,
+// decode_pv and decode_combine with FUSED in hsdpa_attn_kernels.h). Head dimensions 32 to
 // 256: the form declines above (src/jit/ir.rs:146-148).
 //
 // In a translation unit of its own, like hsdpa_attn_more.hip, so that the
@@ -19,6 +19,22 @@
 #include "hsdpa_attn_kernels.h"
 
 namespace hsdpa {
+
+// Pass 1 differs from the Chained one only in storing the maximum of every
+// 16-key block (bmax). Pass 2 reads those only for the blocks between the last
+// pass-1 workgroup wholly before its keys and its first key, and decode_direct
+// reads them all; where every pass-2 workgroup starts at a pass-1 workgroup's
+// first key (keys_pv a multiple of keys_qk) the Chained pass 1 writes all that
+// pass 2 reads.
+static bool fused_needs_bmax(const DecodeArgs &a) { return a.direct || a.keys_pv % a.keys_qk != 0; }
+
+template <int D, int MR, bool BMAX>
+static hipError_t fused_pass1(const DecodeArgs &a, dim3 gqk, hipStream_t s)
+{
+    return a.keys_qk == 8 * kKeyTile ? launch(decode_qk<D, true, MR, BMAX, true>, gqk, dim3(256), s, a)
+           : a.keys_qk > 4 * kKeyTile  ? launch(decode_qk<D, true, MR, BMAX>, gqk, dim3(256), s, a)
+                                       : launch(decode_qk<D, false, MR, BMAX>, gqk, dim3(256), s, a);
+}
 
 // The tuned head dimensions (64, 128, 256): the configurations of the Chained
 // launcher, one row (MR = 0), a few rows (MR = 1) or several groups on one
@@ -30,9 +46,7 @@ static hipError_t fused_dm(const DecodeArgs &a, int kv_heads, hipStream_t s)
     const auto pad8 = [](int n) { return static_cast<unsigned>((n + 7) / 8 * 8); };
     const dim3 gqk = xcd ? dim3(pad8(a.nwg_qk) * a.sub, kv_heads, 1) : dim3(a.nwg_qk, kv_heads, a.sub);
     const dim3 gpv = xcd ? dim3(pad8(a.nwg_pv) * a.sub, kv_heads, 1) : dim3(a.nwg_pv, kv_heads, a.sub);
-    hipError_t e = a.keys_qk == 8 * kKeyTile ? launch(decode_qk<D, true, MR, true, true>, gqk, dim3(256), s, a)
-                   : a.keys_qk > 4 * kKeyTile  ? launch(decode_qk<D, true, MR, true>, gqk, dim3(256), s, a)
-                                               : launch(decode_qk<D, false, MR, true>, gqk, dim3(256), s, a);
+    hipError_t e = fused_needs_bmax(a) ? fused_pass1<D, MR, true>(a, gqk, s) : fused_pass1<D, MR, false>(a, gqk, s);
     if (e != hipSuccess) return e;
     if (a.direct) {
         // a short cache: pass 2 over every key writes the outputs (decode_direct_ok)
@@ -77,9 +91,7 @@ template <int D, int MR>
 static hipError_t fused_more_m(const DecodeArgs &a, int kv_heads, hipStream_t s)
 {
     const dim3 gqk(a.nwg_qk, kv_heads, a.sub), gpv(a.nwg_pv, kv_heads, a.sub);
-    hipError_t e = a.keys_qk == 8 * kKeyTile ? launch(decode_qk<D, true, MR, true, true>, gqk, dim3(256), s, a)
-                   : a.keys_qk > 4 * kKeyTile  ? launch(decode_qk<D, true, MR, true>, gqk, dim3(256), s, a)
-                                               : launch(decode_qk<D, false, MR, true>, gqk, dim3(256), s, a);
+    hipError_t e = fused_needs_bmax(a) ? fused_pass1<D, MR, true>(a, gqk, s) : fused_pass1<D, MR, false>(a, gqk, s);
     if (e != hipSuccess) return e;
     constexpr bool WIDE = D / 16 >= 8 || 8 % (D / 16) == 0;        // decode_wide_ok
     if (a.keys_pv == 4 * kKeyTile) {
