@@ -409,20 +409,24 @@ __device__ __forceinline__ uint32_t frame_args(DecodeArgs &a, bool &run)
     if (rows > 1) return HSDPA_ERR_BATCH;
     if (past >= a.f_cap) return HSDPA_ERR_CAPACITY;
     run = true;
-    const uint64_t n = past + 1, groups = static_cast<uint64_t>(a.f_groups);
-    const uint64_t cus = static_cast<uint64_t>(a.f_cus);
-    const uint64_t nqk1 = (n + kDecodeKeysQK - 1) / kDecodeKeysQK;
+    // in 32 bits: every kernel of the call runs this before its first load, and
+    // 64-bit divisions made it hundreds of instructions. The frame entry
+    // refuses capacities and group counts whose products would not fit
+    // (groups * ceil(capacity / 128) < 2^31).
+    const uint32_t n = static_cast<uint32_t>(past) + 1u, groups = static_cast<uint32_t>(a.f_groups);
+    const uint32_t cus = static_cast<uint32_t>(a.f_cus);
+    const uint32_t nqk1 = (n + kDecodeKeysQK - 1) / kDecodeKeysQK;
     // decode_cfg's rule: two tiles per wave at least once one per wave
     // needs more than one workgroup per compute unit, as many as one round
     // of two per unit needs, then the count up to twice that which leaves
     // the fewest tiles on the busiest unit
-    const uint64_t rounds = (groups * nqk1 + 2 * cus - 1) / (2 * cus);
-    uint64_t rq = groups * nqk1 > cus && rounds < 2 ? 2 : rounds > 1 ? rounds : 1;
+    const uint32_t rounds = (groups * nqk1 + 2 * cus - 1) / (2 * cus);
+    uint32_t rq = groups * nqk1 > cus && rounds < 2 ? 2 : rounds > 1 ? rounds : 1;
     if (rq > 1) {
-        uint64_t best = rq, cost = ~uint64_t{0};
-        for (uint64_t r = rq; r <= 2 * rq; r++) {
-            const uint64_t wgs = groups * ((nqk1 + r - 1) / r);
-            const uint64_t cc = (wgs + cus - 1) / cus * r;
+        uint32_t best = rq, cost = ~0u;
+        for (uint32_t r = rq; r <= 2 * rq; r++) {
+            const uint32_t wgs = groups * ((nqk1 + r - 1) / r);
+            const uint32_t cc = (wgs + cus - 1) / cus * r;
             if (cc < cost) {
                 cost = cc;
                 best = r;
@@ -433,16 +437,16 @@ __device__ __forceinline__ uint32_t frame_args(DecodeArgs &a, bool &run)
     a.past = past;
     a.n = n;
     a.keys_qk = static_cast<int>(kDecodeKeysQK * rq);
-    a.nwg_qk = static_cast<int>((n + a.keys_qk - 1) / a.keys_qk);
+    a.nwg_qk = static_cast<int>((n + static_cast<uint32_t>(a.keys_qk) - 1) / static_cast<uint32_t>(a.keys_qk));
     if (a.f_loop) {
-        const uint64_t per = cus / groups > 0 ? cus / groups : 1;
-        const uint64_t tiles = (n + kKeyTile - 1) / kKeyTile;
-        const uint64_t run_keys = kKeyTile * ((tiles + per - 1) / per);
+        const uint32_t per = cus / groups > 0 ? cus / groups : 1;
+        const uint32_t tiles = (n + kKeyTile - 1) / kKeyTile;
+        const uint32_t run_keys = kKeyTile * ((tiles + per - 1) / per);
         a.keys_pv = static_cast<int>(run_keys > 4 * kKeyTile ? run_keys : 4 * kKeyTile);
     } else {
         a.keys_pv = kDecodeKeysPV;
     }
-    a.nwg_pv = static_cast<int>((n + a.keys_pv - 1) / a.keys_pv);
+    a.nwg_pv = static_cast<int>((n + static_cast<uint32_t>(a.keys_pv) - 1) / static_cast<uint32_t>(a.keys_pv));
     return HSDPA_OK;
 }
 
@@ -576,7 +580,10 @@ __global__ __launch_bounds__(256) void decode_qk(DecodeArgs a)
                     *reinterpret_cast<float4 *>(sp + 16 * b) = v4;
                 }
             }
-            if constexpr (FUSED) {
+            // a frame call's pass 2 reads block maxima only where its
+            // workgroups start inside a pass-1 workgroup's keys (the host path
+            // launches the Chained pass 1 where none does)
+            if (FUSED && (!FRAME || a.keys_pv % a.keys_qk != 0)) {
                 // block b of the tile: keys t0 + 16 b + 4 G + r over the four lane
                 // groups G of column i (the same scaled values as stored above)
 #pragma unroll
@@ -606,13 +613,14 @@ __global__ __launch_bounds__(256) void decode_qk(DecodeArgs a)
         // itself the scheduler interleaves them and keeps only a few outstanding.
         __builtin_amdgcn_sched_barrier(0);
         tile(j0 + kKeyTile * wave, kr);
-    } else if constexpr (TWO) {
+    } else if (TWO || (FRAME && a.keys_qk == 8 * kKeyTile)) {
         // exactly two rounds of one tile per wave (keys_qk = 256): both tiles
         // requested before the first is scored. In the loop below the second
         // is requested at the top of the loop and waits behind the first
         // (32K keys on 2 KV heads: 21.3 -> 20.6 us); for more rounds the loop
         // runs faster with one tile in flight (two: 0.8 us slower at 64K and
-        // 128K)
+        // 128K). A frame call takes this form whenever its step's keys_qk is
+        // 256.
         u32x4 kr0[Tile<D, 64>::kPer], kr1[Tile<D, 64>::kPer];
         tile_gload<D, 64, NT>(kbase, j0 + kKeyTile * wave, j1, l, kr0);
         tile_gload<D, 64, NT>(kbase, j0 + 4 * kKeyTile + kKeyTile * wave, j1, l, kr1);
