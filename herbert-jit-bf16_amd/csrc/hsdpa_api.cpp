@@ -762,9 +762,11 @@ hsdpa_status hsdpa_attention_frame(const hsdpa_plan *plan, const hsdpa_frame_cal
                         : 0;
     if (plan->max_rows != 1 || !hsdpa::decode_rows_ok(d) || sub == 0) return HSDPA_ERR_FRAME;
     // the kernels derive the step's configuration in 32-bit arithmetic
-    // (frame_args): groups * ceil(capacity / 128) below 2^31
-    if (plan->kv_heads * static_cast<uint64_t>(sub) *
-            ((s.kv_capacity + hsdpa::kDecodeKeysQK - 1) / hsdpa::kDecodeKeysQK) >= (static_cast<uint64_t>(1) << 31))
+    // (frame_args): the capacity and groups * ceil(capacity / 128) below 2^31
+    constexpr uint64_t k31 = static_cast<uint64_t>(1) << 31;
+    if (s.kv_capacity >= k31 ||
+        plan->kv_heads * static_cast<uint64_t>(sub) *
+                ((s.kv_capacity + hsdpa::kDecodeKeysQK - 1) / hsdpa::kDecodeKeysQK) >= k31)
         return HSDPA_ERR_FRAME;
     if (!call->q || !call->keys || !call->values || !call->output || !call->rows || !call->past ||
         !call->workspace)

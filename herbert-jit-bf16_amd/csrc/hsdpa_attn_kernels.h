@@ -411,8 +411,8 @@ __device__ __forceinline__ uint32_t frame_args(DecodeArgs &a, bool &run)
     run = true;
     // in 32 bits: every kernel of the call runs this before its first load, and
     // 64-bit divisions made it hundreds of instructions. The frame entry
-    // refuses capacities and group counts whose products would not fit
-    // (groups * ceil(capacity / 128) < 2^31).
+    // refuses capacities of 2^31 keys or more, and group counts with
+    // groups * ceil(capacity / 128) of 2^31 or more.
     const uint32_t n = static_cast<uint32_t>(past) + 1u, groups = static_cast<uint32_t>(a.f_groups);
     const uint32_t cus = static_cast<uint32_t>(a.f_cus);
     const uint32_t nqk1 = (n + kDecodeKeysQK - 1) / kDecodeKeysQK;

@@ -87,8 +87,9 @@ typedef enum hsdpa_status {
                                        HSDPA_STATIC_SCRATCH_BYTES */
     HSDPA_ERR_FRAME = 16            /* hsdpa_attention_frame: the plan has no frame route (it needs
                                        max_rows = 1, head_dim 64, 128 or 256, query heads per KV
-                                       head in at most 4 equal groups of at most 16, and decode
-                                       groups x ceil(kv_capacity / 128) below 2^31) */
+                                       head in at most 4 equal groups of at most 16, kv_capacity
+                                       below 2^31, and decode groups x ceil(kv_capacity / 128)
+                                       below 2^31) */
 } hsdpa_status;
 
 /* The decode head form (SdpaForm, src/jit/ir.rs:100-115; the knob
@@ -222,10 +223,10 @@ hsdpa_status hsdpa_attention_static(const hsdpa_plan *plan, const hsdpa_call *ca
  * visible keys exit at once.
  *
  * Plans: decode-only (max_rows = 1), head_dim 64, 128 or 256, at most 64
- * query heads per KV head in at most 4 equal groups of at most 16, and
- * kv_heads x groups x ceil(kv_capacity / 128) below 2^31 (the kernels derive
- * each step's configuration in 32-bit arithmetic; otherwise HSDPA_ERR_FRAME);
- * either form. Values read at run time: *rows = 0 computes
+ * query heads per KV head in at most 4 equal groups of at most 16,
+ * kv_capacity below 2^31 and kv_heads x groups x ceil(kv_capacity / 128)
+ * below 2^31 (the kernels derive each step's configuration in 32-bit
+ * arithmetic; otherwise HSDPA_ERR_FRAME); either form. Values read at run time: *rows = 0 computes
  * nothing; *rows = 1 is one decode row with n = *past + 1 keys; *rows > 1 or
  * *past >= kv_capacity compute nothing and report HSDPA_ERR_BATCH or
  * HSDPA_ERR_CAPACITY through *status. The outputs are those of hsdpa_attention

@@ -220,10 +220,12 @@ def test_frame_call_refusals_before_any_device_work():
     assert _frame(hsdpa.Plan(16, 8, 96, 4096, max_rows=1)) == "HSDPA_ERR_FRAME"        # untuned head_dim
     assert _frame(hsdpa.Plan(17, 17, 128, 4096, max_rows=1)) == "HSDPA_ERR_FRAME"      # padded groups
     assert _frame(hsdpa.Plan(100, 100, 128, 4096, max_rows=1)) == "HSDPA_ERR_FRAME"    # more than 4 groups
-    # the step's configuration is derived in 32 bits on the device: groups x
-    # ceil(capacity / 128) must stay below 2^31
+    # the step's configuration is derived in 32 bits on the device: the
+    # capacity and groups x ceil(capacity / 128) must stay below 2^31
     assert _frame(hsdpa.Plan(1024, 1, 64, 1 << 28, max_rows=1)) == "HSDPA_ERR_FRAME"
     assert _frame(hsdpa.Plan(1023, 1, 64, 1 << 28, max_rows=1)) != "HSDPA_ERR_FRAME"
+    assert _frame(hsdpa.Plan(16, 8, 64, 1 << 31, max_rows=1)) == "HSDPA_ERR_FRAME"
+    assert _frame(hsdpa.Plan(16, 8, 64, (1 << 31) - 1, max_rows=1)) != "HSDPA_ERR_FRAME"
     p = hsdpa.Plan(16, 8, 256, 4096, max_rows=1)
     assert _frame(p, rows=0) == "HSDPA_ERR_NULL"
     assert _frame(p, past=0) == "HSDPA_ERR_NULL"
