@@ -143,6 +143,42 @@ __device__ __forceinline__ float dpp(float x, float old)
     return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(old), __float_as_int(x), CTRL, ROWS, 0xF, false));
 }
 
+// Lane k of each 16-lane row, in every lane of the row (row_newbcast; k a
+// constant once unrolled).
+__device__ __forceinline__ float row_lane(float x, int k)
+{
+    switch (k) {
+    case 0: return dpp<0x150, 0xF>(x, x);
+    case 1: return dpp<0x151, 0xF>(x, x);
+    case 2: return dpp<0x152, 0xF>(x, x);
+    case 3: return dpp<0x153, 0xF>(x, x);
+    case 4: return dpp<0x154, 0xF>(x, x);
+    case 5: return dpp<0x155, 0xF>(x, x);
+    case 6: return dpp<0x156, 0xF>(x, x);
+    case 7: return dpp<0x157, 0xF>(x, x);
+    case 8: return dpp<0x158, 0xF>(x, x);
+    case 9: return dpp<0x159, 0xF>(x, x);
+    case 10: return dpp<0x15A, 0xF>(x, x);
+    case 11: return dpp<0x15B, 0xF>(x, x);
+    case 12: return dpp<0x15C, 0xF>(x, x);
+    case 13: return dpp<0x15D, 0xF>(x, x);
+    case 14: return dpp<0x15E, 0xF>(x, x);
+    default: return dpp<0x15F, 0xF>(x, x);
+    }
+}
+
+// Lane b - n of the same 16-lane row in lane b (row_shr:n, n = 1, 2, 4 or 8);
+// lanes b < n keep `old`.
+__device__ __forceinline__ float row_shr_n(float x, int n, float old)
+{
+    switch (n) {
+    case 1: return dpp<0x111, 0xF>(x, old);
+    case 2: return dpp<0x112, 0xF>(x, old);
+    case 4: return dpp<0x114, 0xF>(x, old);
+    default: return dpp<0x118, 0xF>(x, old);
+    }
+}
+
 __device__ __forceinline__ float row_sum16(float x)
 {
     x += dpp<0xB1, 0xF>(x, 0.0f);    // quad_perm [1,0,3,2]
@@ -844,21 +880,26 @@ __global__ __launch_bounds__(64 * W, D > 256 ? 1 : 8 / W) void decode_pv(DecodeA
                 const int h = tid / NB, b = tid - h * NB;
                 const float m0 = smax[h];
                 float mb = fbm[tid] > m0 ? fbm[tid] : m0;
+                // with 16 blocks a column is one 16-lane DPP row: the shifts
+                // and broadcasts are row_shr and row_newbcast moves instead of
+                // LDS permutes, each of which the next step waited out (the
+                // 15 broadcasts of the product)
+                constexpr bool ROW = NB == 16;
 #pragma unroll
                 for (int off = 1; off < NB; off *= 2) {
-                    const float o = __shfl_up(mb, off, NB);
+                    const float o = ROW ? row_shr_n(mb, off, kNegInf) : __shfl_up(mb, off, NB);
                     if (b >= off && o > mb) mb = o;
                 }
-                const float mprev = __shfl_up(mb, 1, NB);
+                const float mprev = ROW ? row_shr_n(mb, 1, m0) : __shfl_up(mb, 1, NB);
                 const float mp = b > 0 ? mprev : m0;
                 const float cor = exp_poly(mp - mb);
                 float c = 1.0f;
 #pragma unroll
                 for (int k = 1; k < NB; k++) {
-                    const float ck = __shfl(cor, k, NB);
+                    const float ck = ROW ? row_lane(cor, k) : __shfl(cor, k, NB);
                     c = k > b ? c * ck : c;
                 }
-                const float mlast = __shfl(mb, NB - 1, NB);
+                const float mlast = ROW ? row_lane(mb, NB - 1) : __shfl(mb, NB - 1, NB);
                 fmb[tid] = mb;
                 fcf[tid] = c;
                 if (b == 0) {
@@ -1219,14 +1260,17 @@ __global__ __launch_bounds__(512, 1) void decode_direct(DecodeArgs a)
     }
     __builtin_amdgcn_sched_barrier(0);                          // all loads issued first
     if constexpr (FUSED) {
-        // running maxima: an inclusive prefix maximum over the wave's lanes
+        // running maxima: an inclusive prefix maximum over the wave's lanes,
+        // by DPP moves (within each 16-lane row by row_shr 1, 2, 4, 8, then
+        // row_bcast:15 into rows 1 and 3, row_bcast:31 into rows 2 and 3),
+        // and the previous lane's by wave_shr:1; LDS permutes, each waited
+        // out by the next step, took longer
         float mb = mxv;
 #pragma unroll
-        for (int off = 1; off < 64; off *= 2) {
-            const float o = __shfl_up(mb, off);
-            if (l >= off) mb = fmaxnn(mb, o);
-        }
-        const float mprev = __shfl_up(mb, 1);
+        for (int off = 1; off < 16; off *= 2) mb = fmaxnn(mb, row_shr_n(mb, off, kNegInf));
+        mb = fmaxnn(mb, dpp<0x142, 0xA>(mb, kNegInf));
+        mb = fmaxnn(mb, dpp<0x143, 0xC>(mb, kNegInf));
+        const float mprev = dpp<0x138, 0xF>(mb, kNegInf);
         const float cor = l > 0 ? exp_poly(mprev - mb) : 1.0f;
         // C_l = the corrections of blocks l + 1 .. NB - 1 multiplied left to
         // right, each broadcast from its lane in turn
