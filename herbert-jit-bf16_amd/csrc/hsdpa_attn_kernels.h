@@ -167,6 +167,10 @@ __device__ __forceinline__ float row_lane(float x, int k)
     }
 }
 
+// Lane l ^ 8 in lane l (row_ror:8 within the 16-lane row): a DPP move where
+// __shfl_xor takes an LDS permute.
+__device__ __forceinline__ float row_xor8(float x) { return dpp<0x128, 0xF>(x, x); }
+
 // Lane b - n of the same 16-lane row in lane b (row_shr:n, n = 1, 2, 4 or 8);
 // lanes b < n keep `old`.
 __device__ __forceinline__ float row_shr_n(float x, int n, float old)
@@ -1029,7 +1033,7 @@ __global__ __launch_bounds__(64 * W, D > 256 ? 1 : 8 / W) void decode_pv(DecodeA
         f32x4 s;
 #pragma unroll
         for (int r = 0; r < 4; r++) {
-            if constexpr (NCB == 1) s[r] = o[0][db][r] + __shfl_xor(o[0][db][r], 8);
+            if constexpr (NCB == 1) s[r] = o[0][db][r] + row_xor8(o[0][db][r]);
             else s[r] = o[0][db][r] + o[NCB - 1][db][r];
         }
         if (part == 0 && j < 8 * NCB && j < a.g && (ALL || dgi * DBW + db < DB)) {
@@ -1374,7 +1378,7 @@ __global__ __launch_bounds__(512, 1) void decode_direct(DecodeArgs a)
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 // hi column + lo column
-                const float os = NCB == 1 ? sum[0][r] + __shfl_xor(sum[0][r], 8) : sum[0][r] + sum[NCB - 1][r];
+                const float os = NCB == 1 ? sum[0][r] + row_xor8(sum[0][r]) : sum[0][r] + sum[NCB - 1][r];
                 ob[r] = static_cast<uint16_t>(cvt_out(FUSED ? os * (1.0f / L) : os / L));
             }
             if (j < CM && h < g) {
