@@ -69,10 +69,14 @@ def lib():
         L.oracle_sdpa_head.restype = None
         L.oracle_sdpa_head_qk0.argtypes = L.oracle_sdpa_head.argtypes
         L.oracle_sdpa_head_qk0.restype = None
+        L.oracle_sdpa_head_sink.argtypes = L.oracle_sdpa_head.argtypes + [ctypes.c_float]
+        L.oracle_sdpa_head_sink.restype = None
         L.oracle_sdpa_prefill_block.argtypes = [u16p, u16p, u16p, ctypes.c_void_p, u16p, ctypes.c_uint64,
                                                 ctypes.c_float, ctypes.c_int, ctypes.c_int, ctypes.c_size_t,
                                                 ctypes.c_size_t]
         L.oracle_sdpa_prefill_block.restype = None
+        L.oracle_sdpa_prefill_block_sink.argtypes = L.oracle_sdpa_prefill_block.argtypes + [ctypes.c_float]
+        L.oracle_sdpa_prefill_block_sink.restype = None
         L.oracle_attention_scalar.argtypes = [ctypes.POINTER(Spec), ctypes.POINTER(Call)]
         L.oracle_attention_scalar.restype = ctypes.c_int
         L.oracle_attention_avx512.argtypes = [ctypes.POINTER(Spec), ctypes.POINTER(Call), ctypes.c_int]
@@ -93,6 +97,8 @@ def lib():
         L.oracle_avx2_head.argtypes = [u16p, u16p, u16p, ctypes.c_void_p, u16p, ctypes.c_uint64, ctypes.c_float,
                                        ctypes.c_int]
         L.oracle_avx2_head.restype = ctypes.c_int
+        L.oracle_avx2_head_sink.argtypes = L.oracle_avx2_head.argtypes + [ctypes.c_float]
+        L.oracle_avx2_head_sink.restype = ctypes.c_int
         L.oracle_avx2_cvt_bf16.argtypes = [ctypes.c_float]
         L.oracle_avx2_cvt_bf16.restype = ctypes.c_uint16
         L.oracle_exp_poly_n.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint64]
@@ -112,10 +118,10 @@ def avx512_available() -> bool:
     return bool(lib().oracle_avx512_available())
 
 
-FORMS = {"chained": 0, "fused": 1, "avx2": 2, "chained_qk0": 3}
+FORMS = {"chained": 0, "fused": 1, "avx2": 2, "chained_qk0": 3, "chained_sink": 4, "avx2_sink": 5}
 
 
-def attention(w, impl: str = "auto", threads: int = 0, form: str = "chained") -> np.ndarray:
+def attention(w, impl: str = "auto", threads: int = 0, form: str = "chained", sink: float | None = None) -> np.ndarray:
     """Run the reference attention node on workload `w`; returns out bf16 bits
     [rows][heads][head_dim]. impl: 'scalar', 'avx512' or 'auto' (AVX-512
     when the host has it, which is bit-identical to the scalar one).
@@ -123,15 +129,22 @@ def attention(w, impl: str = "auto", threads: int = 0, form: str = "chained") ->
     softmax), 'avx2' (a host without AVX-512 BF16) or 'chained_qk0' (the
     default form with the knob sdpa_qk_group = 0: four QK chains); the other
     forms than 'chained' run the scalar emulation on `threads` threads (0:
-    the host's cores, at most 16)."""
+    the host's cores, at most 16). sink: the softmax sink value with the
+    sink on (SdpaShape::sink); the Fused form declines it and the engine runs
+    the Chained one, the AVX2 arm has its own (forms 'chained_sink' and
+    'avx2_sink' of the scalar emulation)."""
     L = lib()
+    sink_value = 0.0
+    if sink is not None:
+        form = "avx2_sink" if form == "avx2" else "chained_sink"
+        sink_value = float(sink)
     if form != "chained":
         out = np.zeros((w.rows, w.heads, w.head_dim), dtype=np.uint16)
         q = np.ascontiguousarray(w.q)
         k = np.ascontiguousarray(w.k)
         v = np.ascontiguousarray(w.v)
         spec = Spec(w.heads, w.gqa, w.head_dim, w.q_row, w.head_dim, w.out_row)
-        call = Call(_ptr(q), _ptr(k), _ptr(v), _ptr(out), w.rows, w.past, w.kv_stride, w.scale, 0.0)
+        call = Call(_ptr(q), _ptr(k), _ptr(v), _ptr(out), w.rows, w.past, w.kv_stride, w.scale, sink_value)
         rc = L.oracle_attention_form(ctypes.byref(spec), ctypes.byref(call), FORMS[form],
                                      threads or min(16, os.cpu_count() or 1))
         if rc != 0:
@@ -154,15 +167,21 @@ def attention(w, impl: str = "auto", threads: int = 0, form: str = "chained") ->
     return out
 
 
-def head(q: np.ndarray, k: np.ndarray, v: np.ndarray, n: int, scale: float, qk_group0: bool = False) -> np.ndarray:
+def head(q: np.ndarray, k: np.ndarray, v: np.ndarray, n: int, scale: float, qk_group0: bool = False,
+         sink: float | None = None) -> np.ndarray:
     """One decode head (scalar emulation): q [d], k/v [>=n][d] -> out [d] bf16 bits.
-    qk_group0: the knob sdpa_qk_group = 0 (the QK in four chains)."""
+    qk_group0: the knob sdpa_qk_group = 0 (the QK in four chains); sink: the
+    softmax sink value with the sink on."""
     d = q.shape[-1]
     q = np.ascontiguousarray(q, dtype=np.uint16)
     k = np.ascontiguousarray(k, dtype=np.uint16)
     v = np.ascontiguousarray(v, dtype=np.uint16)
     sc = np.zeros(((n + 15) // 16) * 16, dtype=np.float32)
     out = np.zeros(d, dtype=np.uint16)
+    if sink is not None:
+        assert not qk_group0
+        lib().oracle_sdpa_head_sink(_ptr(q), _ptr(k), _ptr(v), _ptr(sc), _ptr(out), n, scale, d, float(sink))
+        return out
     fn = lib().oracle_sdpa_head_qk0 if qk_group0 else lib().oracle_sdpa_head
     fn(_ptr(q), _ptr(k), _ptr(v), _ptr(sc), _ptr(out), n, scale, d)
     return out
@@ -190,21 +209,27 @@ def fused_head(q: np.ndarray, k: np.ndarray, v: np.ndarray, n: int, scale: float
     return (out, a) if acc else out
 
 
-def avx2_head(q: np.ndarray, k: np.ndarray, v: np.ndarray, n: int, scale: float) -> np.ndarray:
-    """One AVX2-arm decode head: out [d] bf16 bits."""
+def avx2_head(q: np.ndarray, k: np.ndarray, v: np.ndarray, n: int, scale: float,
+              sink: float | None = None) -> np.ndarray:
+    """One AVX2-arm decode head: out [d] bf16 bits (sink: the softmax sink value
+    with the sink on)."""
     d = q.shape[-1]
     q = np.ascontiguousarray(q, dtype=np.uint16)
     k = np.ascontiguousarray(k, dtype=np.uint16)
     v = np.ascontiguousarray(v, dtype=np.uint16)
     sc = np.zeros(((n + 7) // 8) * 8 + 8, dtype=np.float32)
     out = np.zeros(d, dtype=np.uint16)
-    if lib().oracle_avx2_head(_ptr(q), _ptr(k), _ptr(v), _ptr(sc), _ptr(out), n, scale, d) != 0:
+    rc = (lib().oracle_avx2_head(_ptr(q), _ptr(k), _ptr(v), _ptr(sc), _ptr(out), n, scale, d) if sink is None else
+          lib().oracle_avx2_head_sink(_ptr(q), _ptr(k), _ptr(v), _ptr(sc), _ptr(out), n, scale, d, float(sink)))
+    if rc != 0:
         raise ValueError("the AVX2 arm declines this head_dim")
     return out
 
 
-def prefill_block(q: np.ndarray, k: np.ndarray, v: np.ndarray, past: int, scale: float) -> np.ndarray:
-    """The 8-row prefill block (scalar emulation): q [rows][d] -> out [rows][d]."""
+def prefill_block(q: np.ndarray, k: np.ndarray, v: np.ndarray, past: int, scale: float,
+                  sink: float | None = None) -> np.ndarray:
+    """The 8-row prefill block (scalar emulation): q [rows][d] -> out [rows][d]
+    (sink: the softmax sink value with the sink on)."""
     rows, d = q.shape
     q = np.ascontiguousarray(q, dtype=np.uint16)
     k = np.ascontiguousarray(k, dtype=np.uint16)
@@ -212,7 +237,11 @@ def prefill_block(q: np.ndarray, k: np.ndarray, v: np.ndarray, past: int, scale:
     N = past + rows
     sc = np.zeros(rows * ((N + 15) // 16) * 16, dtype=np.float32)
     out = np.zeros((rows, d), dtype=np.uint16)
-    lib().oracle_sdpa_prefill_block(_ptr(q), _ptr(k), _ptr(v), _ptr(sc), _ptr(out), past, scale, d, rows, d, d)
+    if sink is None:
+        lib().oracle_sdpa_prefill_block(_ptr(q), _ptr(k), _ptr(v), _ptr(sc), _ptr(out), past, scale, d, rows, d, d)
+    else:
+        lib().oracle_sdpa_prefill_block_sink(_ptr(q), _ptr(k), _ptr(v), _ptr(sc), _ptr(out), past, scale, d, rows, d,
+                                             d, float(sink))
     return out
 
 

@@ -187,13 +187,15 @@ float oracle_avx2_qk_dot(const uint16_t *q, const uint16_t *k, int head_dim)
     return avx2_hsum8(lanes);
 }
 
-/* The AVX2 head (emit_sdpa_avx2.rs:231-470), no sink: scores with -inf
- * padding to a multiple of 8; softmax over ceil(n/8) blocks of 8 (lane-wise
- * max, hmax8; exponentials with lane sums in block order, hsum8; vdivps by the
- * sum); SV with FMA in position order; the integer RNE conversion.
+/* The AVX2 head (emit_sdpa_avx2.rs:231-470): scores with -inf padding to a
+ * multiple of 8; softmax over ceil(n/8) blocks of 8 (lane-wise max, hmax8;
+ * exponentials with lane sums in block order, hsum8; vdivps by the sum); SV
+ * with FMA in position order; the integer RNE conversion. With the sink
+ * (emit_sdpa_avx2.rs:362-400): vmaxss(hmax, sink), the exponential of
+ * sink - max added after the hsum, 1/sum by vdivss and vmulps.
  * scores: at least roundup8(n) f32. */
-int oracle_avx2_head(const uint16_t *q, const uint16_t *k, const uint16_t *v, float *scores, uint16_t *out,
-                     uint64_t n, float scale, int head_dim)
+static int avx2_head(const uint16_t *q, const uint16_t *k, const uint16_t *v, float *scores, uint16_t *out,
+                     uint64_t n, float scale, int head_dim, int sink_on, float sink)
 {
     if (head_dim <= 0 || head_dim % 16 != 0 || head_dim > 512) return -1;      /* check_avx2 */
     const size_t d = (size_t)head_dim;
@@ -207,7 +209,8 @@ int oracle_avx2_head(const uint16_t *q, const uint16_t *k, const uint16_t *v, fl
         for (int L = 0; L < 8; L++) maxv[L] = -INFINITY;
         for (uint64_t b = 0; b < nb; b++)
             for (int L = 0; L < 8; L++) maxv[L] = vmax(maxv[L], scores[8 * b + L]);
-        const float m = avx2_hmax8(maxv);
+        const float hm = avx2_hmax8(maxv);
+        const float m = sink_on ? vmax(hm, sink) : hm;
         float sumv[8] = {0};
         for (uint64_t b = 0; b < nb; b++)
             for (int L = 0; L < 8; L++) {
@@ -215,8 +218,14 @@ int oracle_avx2_head(const uint16_t *q, const uint16_t *k, const uint16_t *v, fl
                 sumv[L] = sumv[L] + w;
                 scores[8 * b + L] = w;
             }
-        const float sum = avx2_hsum8(sumv);
-        for (uint64_t i = 0; i < 8 * nb; i++) scores[i] = scores[i] / sum;
+        float sum = avx2_hsum8(sumv);
+        if (sink_on) {
+            sum = sum + oracle_exp_poly(sink - m);
+            const float inv = 1.0f / sum;
+            for (uint64_t i = 0; i < 8 * nb; i++) scores[i] = scores[i] * inv;
+        } else {
+            for (uint64_t i = 0; i < 8 * nb; i++) scores[i] = scores[i] / sum;
+        }
         for (uint64_t j = 0; j < n; j++) {
             const float p = scores[j];
             const uint16_t *vr = v + j * d;
@@ -225,6 +234,18 @@ int oracle_avx2_head(const uint16_t *q, const uint16_t *k, const uint16_t *v, fl
     }
     for (size_t c = 0; c < d; c++) out[c] = oracle_avx2_cvt_bf16(acc[c]);
     return 0;
+}
+
+int oracle_avx2_head(const uint16_t *q, const uint16_t *k, const uint16_t *v, float *scores, uint16_t *out,
+                     uint64_t n, float scale, int head_dim)
+{
+    return avx2_head(q, k, v, scores, out, n, scale, head_dim, 0, 0.0f);
+}
+
+int oracle_avx2_head_sink(const uint16_t *q, const uint16_t *k, const uint16_t *v, float *scores, uint16_t *out,
+                          uint64_t n, float scale, int head_dim, float sink)
+{
+    return avx2_head(q, k, v, scores, out, n, scale, head_dim, 1, sink);
 }
 
 /* ---- the attention node under a form ------------------------------------------ */
@@ -250,9 +271,13 @@ static int run_rows(const oracle_attention_spec *s, const oracle_attention_call 
 {
     const uint64_t d = s->head_dim, kvh = h / s->gqa;
     const uint16_t *kk = c->keys + kvh * c->kv_stride, *vv = c->values + kvh * c->kv_stride;
-    if (form != 2 && r1 - r0 == 8) {
+    if (form != 2 && form != 5 && r1 - r0 == 8) {
         const uint64_t ar = pass_row0 + r0;
-        if (form == 3)
+        if (form == 4)
+            oracle_sdpa_prefill_block_sink(c->q + ar * s->q_row + h * s->q_head, kk, vv, scratch,
+                                           c->output + ar * s->out_row + h * d, pass_past + r0, c->scale, (int)d, 8,
+                                           s->q_row, s->out_row, c->sink);
+        else if (form == 3)
             oracle_sdpa_prefill_block_qk0(c->q + ar * s->q_row + h * s->q_head, kk, vv, scratch,
                                           c->output + ar * s->out_row + h * d, pass_past + r0, c->scale, (int)d, 8,
                                           s->q_row, s->out_row);
@@ -270,6 +295,10 @@ static int run_rows(const oracle_attention_spec *s, const oracle_attention_call 
             if (oracle_fused_head(qp, kk, vv, op, n, c->scale, (int)d, NULL) != 0) return -1;
         } else if (form == 2) {
             if (oracle_avx2_head(qp, kk, vv, scratch, op, n, c->scale, (int)d) != 0) return -1;
+        } else if (form == 5) {
+            if (oracle_avx2_head_sink(qp, kk, vv, scratch, op, n, c->scale, (int)d, c->sink) != 0) return -1;
+        } else if (form == 4) {
+            oracle_sdpa_head_sink(qp, kk, vv, scratch, op, n, c->scale, (int)d, c->sink);
         } else if (form == 3) {
             oracle_sdpa_head_qk0(qp, kk, vv, scratch, op, n, c->scale, (int)d);
         } else {
@@ -284,7 +313,7 @@ static void *form_worker(void *arg)
     form_job *j = (form_job *)arg;
     const oracle_attention_spec *s = j->s;
     const oracle_attention_call *c = j->c;
-    const uint64_t chunk = j->form == 2 ? 1 : 8;
+    const uint64_t chunk = j->form == 2 || j->form == 5 ? 1 : 8;
     const uint64_t groups = (c->rows + chunk - 1) / chunk;
     float *scratch = (float *)malloc(sizeof(float) * 8 * (((c->past + c->rows + 16) + 15) & ~(uint64_t)15));
     if (!scratch) {
@@ -305,15 +334,20 @@ static void *form_worker(void *arg)
 }
 
 /* The attention node with the given decode form (0 Chained, 1 Fused, 2 AVX2,
- * 3 Chained with sdpa_qk_group = 0)
+ * 3 Chained with sdpa_qk_group = 0, 4 Chained with the softmax sink c->sink,
+ * 5 AVX2 with the sink; the Fused form declines a sink, src/jit/emit_sdpa.rs:
+ * 468-470, and the engine then runs the Chained one)
  * on `threads` threads (0 or 1: the calling thread), tasks = (q head, row
  * group) in contiguous ranges. Rows are processed in passes of 256, so a row
  * group never straddles a pass. Returns 0, or -1 on an invalid geometry. */
 int oracle_attention_form(const oracle_attention_spec *s, const oracle_attention_call *c, int form, int threads)
 {
-    if (oracle_check_geometry(s, c) != 0 || form < 0 || form > 3) return -1;
+    if (form < 0 || form > 5) return -1;
+    oracle_attention_call cg = *c;
+    if (form >= 4) cg.sink = 0.0f;                 /* the sink forms take any value */
+    if (oracle_check_geometry(s, &cg) != 0) return -1;
     if (c->rows == 0) return 0;
-    const uint64_t chunk = form == 2 ? 1 : 8;
+    const uint64_t chunk = form == 2 || form == 5 ? 1 : 8;
     const uint64_t tasks = s->heads * ((c->rows + chunk - 1) / chunk);
     int nt = threads < 1 ? 1 : threads;
     if ((uint64_t)nt > tasks) nt = (int)tasks;

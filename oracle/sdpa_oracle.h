@@ -82,6 +82,16 @@ void oracle_sdpa_prefill_block_qk0(const uint16_t *q, const uint16_t *k,
                                    uint64_t past, float scale, int head_dim,
                                    int rows, size_t q_row, size_t out_row);
 
+/* The head and the block with the softmax sink on (SdpaShape::sink,
+ * src/jit/ir.rs:55-60): emit_softmax with sink_on (decode.rs:239-290). */
+void oracle_sdpa_head_sink(const uint16_t *q, const uint16_t *k, const uint16_t *v,
+                           float *scores, uint16_t *out, uint64_t n, float scale,
+                           int head_dim, float sink);
+void oracle_sdpa_prefill_block_sink(const uint16_t *q, const uint16_t *k,
+                                    const uint16_t *v, float *scores, uint16_t *out,
+                                    uint64_t past, float scale, int head_dim,
+                                    int rows, size_t q_row, size_t out_row, float sink);
+
 /* The score of one (query, key) pair as the grouped QK computes it, before
  * the scale (single chain + the hsum tree, prefill.rs:302-331). */
 float oracle_qk_dot(const uint16_t *q, const uint16_t *k, int head_dim);
@@ -109,7 +119,8 @@ typedef struct oracle_attention_call {
     uint64_t past;
     uint64_t kv_stride;      /* elements per KV head */
     float scale;
-    float sink;              /* must be 0: the engine never emits a sink */
+    float sink;              /* the sink value: 0 except under the sink forms of
+                                oracle_attention_form (4 and 5) */
 } oracle_attention_call;
 
 /* The whole attention node, scalar emulation, single thread: task ->
@@ -145,6 +156,9 @@ float oracle_avx2_qk_dot(const uint16_t *q, const uint16_t *k, int head_dim);
  * multiple of 16 (check_avx2). */
 int oracle_avx2_head(const uint16_t *q, const uint16_t *k, const uint16_t *v, float *scores, uint16_t *out,
                      uint64_t n, float scale, int head_dim);
+/* The same with the softmax sink on (emit_sdpa_avx2.rs:362-400). */
+int oracle_avx2_head_sink(const uint16_t *q, const uint16_t *k, const uint16_t *v, float *scores, uint16_t *out,
+                          uint64_t n, float scale, int head_dim, float sink);
 /* oracle_exp_poly element by element over n floats. */
 void oracle_exp_poly_n(const float *x, float *y, uint64_t n);
 /* The AVX2 arm's integer round to nearest even (emit_sdpa_avx2.rs:208-217). */
@@ -153,8 +167,10 @@ uint16_t oracle_avx2_cvt_bf16(float x);
  * oracle_attention_scalar), 1 Fused (full 8-row chunks still take the block
  * kernel; other rows the Fused head, or the Chained one above head_dim 256),
  * 2 AVX2 (every row the AVX2 head), 3 Chained with sdpa_qk_group = 0 (block
- * and head with the four-chain QK). `threads` workers over (q head, row
- * group) tasks. Returns 0 or -1. */
+ * and head with the four-chain QK), 4 Chained with the softmax sink call->sink
+ * (block and head), 5 AVX2 with the sink. The Fused form declines a sink
+ * (src/jit/emit_sdpa.rs:468-470) and the engine runs the Chained one: form 4.
+ * `threads` workers over (q head, row group) tasks. Returns 0 or -1. */
 int oracle_attention_form(const oracle_attention_spec *spec, const oracle_attention_call *call, int form,
                           int threads);
 

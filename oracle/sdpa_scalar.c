@@ -139,16 +139,20 @@ float oracle_qk_dot(const uint16_t *q, const uint16_t *k, int head_dim)
 
 static inline uint64_t roundup16(uint64_t n) { return (n + 15u) & ~(uint64_t)15u; }
 
-/* emit_softmax (decode.rs:212-293) on `nb` blocks of 16 scores, no sink:
- * lane-wise max then hmax; lane-wise exp and sequential lane sums, then hsum;
- * true division by the sum. */
-static void softmax_blocks(float *sc, uint64_t nb)
+/* emit_softmax (decode.rs:212-293) on `nb` blocks of 16 scores: lane-wise
+ * max then hmax; lane-wise exp and sequential lane sums, then hsum; true
+ * division by the sum. With the sink (sink_on, decode.rs:239-290): the
+ * maximum is vmaxss(hmax, sink), the sum after the hsum gains the
+ * exponential of sink - max (vsubss, the exp sequence, vaddss), and the
+ * scores are multiplied by 1/sum (vdivss once, then vmulps). */
+static void softmax_blocks(float *sc, uint64_t nb, int sink_on, float sink)
 {
     float maxv[16];
     for (int L = 0; L < 16; L++) maxv[L] = -INFINITY;
     for (uint64_t b = 0; b < nb; b++)
         for (int L = 0; L < 16; L++) maxv[L] = vmax(maxv[L], sc[16 * b + L]);
-    const float m = hmax16(maxv);
+    const float hm = hmax16(maxv);
+    const float m = sink_on ? vmax(hm, sink) : hm;
     float sumv[16] = {0};
     for (uint64_t b = 0; b < nb; b++)
         for (int L = 0; L < 16; L++) {
@@ -156,8 +160,14 @@ static void softmax_blocks(float *sc, uint64_t nb)
             sumv[L] = sumv[L] + w;
             sc[16 * b + L] = w;
         }
-    const float sum = hsum16(sumv);
-    for (uint64_t i = 0; i < 16 * nb; i++) sc[i] = sc[i] / sum;
+    float sum = hsum16(sumv);
+    if (sink_on) {
+        sum = sum + oracle_exp_poly(sink - m);
+        const float inv = 1.0f / sum;
+        for (uint64_t i = 0; i < 16 * nb; i++) sc[i] = sc[i] * inv;
+    } else {
+        for (uint64_t i = 0; i < 16 * nb; i++) sc[i] = sc[i] / sum;
+    }
 }
 
 typedef float (*qk_dot_fn)(const uint16_t *, const uint16_t *, int);
@@ -166,12 +176,12 @@ typedef float (*qk_dot_fn)(const uint16_t *, const uint16_t *, int);
  * decode.rs:113-126), softmax, SV pass (decode.rs:348-428), with the QK
  * summation order `qk` (the knob sdpa_qk_group, src/jit/sdpa.rs:178-202). */
 static void sdpa_head_qk(qk_dot_fn qk, const uint16_t *q, const uint16_t *k, const uint16_t *v, float *scores,
-                         uint16_t *out, uint64_t n, float scale, int head_dim)
+                         uint16_t *out, uint64_t n, float scale, int head_dim, int sink_on, float sink)
 {
     const size_t d = (size_t)head_dim;
     for (uint64_t j = 0; j < n; j++) scores[j] = qk(q, k + j * d, head_dim) * scale;
     for (uint64_t j = n; j < roundup16(n); j++) scores[j] = -INFINITY;
-    softmax_blocks(scores, roundup16(n) / 16);
+    softmax_blocks(scores, roundup16(n) / 16, sink_on, sink);
     float acc[512];
     for (size_t c = 0; c < d; c++) acc[c] = 0.0f;
     for (uint64_t j = 0; j < n; j++) {
@@ -186,7 +196,16 @@ void oracle_sdpa_head(const uint16_t *q, const uint16_t *k, const uint16_t *v,
                       float *scores, uint16_t *out, uint64_t n, float scale,
                       int head_dim)
 {
-    sdpa_head_qk(oracle_qk_dot, q, k, v, scores, out, n, scale, head_dim);
+    sdpa_head_qk(oracle_qk_dot, q, k, v, scores, out, n, scale, head_dim, 0, 0.0f);
+}
+
+/* The head with the softmax sink (SdpaShape::sink, src/jit/ir.rs:55-60;
+ * emit_softmax with sink_on, decode.rs:239-290). */
+void oracle_sdpa_head_sink(const uint16_t *q, const uint16_t *k, const uint16_t *v,
+                           float *scores, uint16_t *out, uint64_t n, float scale,
+                           int head_dim, float sink)
+{
+    sdpa_head_qk(oracle_qk_dot, q, k, v, scores, out, n, scale, head_dim, 1, sink);
 }
 
 /* sdpa_qk_group = 0 (src/jit/sdpa.rs:178-202): emit_qk with four chains
@@ -197,7 +216,7 @@ void oracle_sdpa_head_qk0(const uint16_t *q, const uint16_t *k, const uint16_t *
                           float *scores, uint16_t *out, uint64_t n, float scale,
                           int head_dim)
 {
-    sdpa_head_qk(oracle_fused_qk_dot, q, k, v, scores, out, n, scale, head_dim);
+    sdpa_head_qk(oracle_fused_qk_dot, q, k, v, scores, out, n, scale, head_dim, 0, 0.0f);
 }
 
 /* assemble_prefill (prefill.rs:733-912): the whole rows x N rectangle of
@@ -209,7 +228,7 @@ void oracle_sdpa_head_qk0(const uint16_t *q, const uint16_t *k, const uint16_t *
  * 104-157: the tree of emit_qk "verbatim"). */
 static void prefill_block_qk(qk_dot_fn qk, const uint16_t *q, const uint16_t *k, const uint16_t *v, float *scores,
                              uint16_t *out, uint64_t past, float scale, int head_dim, int rows, size_t q_row,
-                             size_t out_row)
+                             size_t out_row, int sink_on, float sink)
 {
     const size_t d = (size_t)head_dim;
     const uint64_t N = past + (uint64_t)rows;
@@ -221,7 +240,8 @@ static void prefill_block_qk(qk_dot_fn qk, const uint16_t *q, const uint16_t *k,
         uint64_t ni = past + (uint64_t)i + 1;
         for (uint64_t j = ni; j < roundup16(ni); j++) scores[i * rs + j] = -INFINITY;
     }
-    for (int i = 0; i < rows; i++) softmax_blocks(scores + i * rs, roundup16(past + (uint64_t)i + 1) / 16);
+    for (int i = 0; i < rows; i++)
+        softmax_blocks(scores + i * rs, roundup16(past + (uint64_t)i + 1) / 16, sink_on, sink);
     for (int i = 0; i < rows; i++)
         for (int t = 0; t < rows - 1 - i; t++) scores[i * rs + past + (uint64_t)(i + 1 + t)] = 0.0f;
     for (int i = 0; i < rows; i++) {
@@ -241,7 +261,17 @@ void oracle_sdpa_prefill_block(const uint16_t *q, const uint16_t *k,
                                uint64_t past, float scale, int head_dim,
                                int rows, size_t q_row, size_t out_row)
 {
-    prefill_block_qk(oracle_qk_dot, q, k, v, scores, out, past, scale, head_dim, rows, q_row, out_row);
+    prefill_block_qk(oracle_qk_dot, q, k, v, scores, out, past, scale, head_dim, rows, q_row, out_row, 0, 0.0f);
+}
+
+/* The block with the softmax sink: emit_softmax is re-emitted per row
+ * (decode.rs:207-210), so each row's softmax is the head's. */
+void oracle_sdpa_prefill_block_sink(const uint16_t *q, const uint16_t *k,
+                                    const uint16_t *v, float *scores, uint16_t *out,
+                                    uint64_t past, float scale, int head_dim,
+                                    int rows, size_t q_row, size_t out_row, float sink)
+{
+    prefill_block_qk(oracle_qk_dot, q, k, v, scores, out, past, scale, head_dim, rows, q_row, out_row, 1, sink);
 }
 
 void oracle_sdpa_prefill_block_qk0(const uint16_t *q, const uint16_t *k,
@@ -249,7 +279,8 @@ void oracle_sdpa_prefill_block_qk0(const uint16_t *q, const uint16_t *k,
                                    uint64_t past, float scale, int head_dim,
                                    int rows, size_t q_row, size_t out_row)
 {
-    prefill_block_qk(oracle_fused_qk_dot, q, k, v, scores, out, past, scale, head_dim, rows, q_row, out_row);
+    prefill_block_qk(oracle_fused_qk_dot, q, k, v, scores, out, past, scale, head_dim, rows, q_row, out_row, 0,
+                     0.0f);
 }
 
 /* tile_selector's geometry checks (attention.rs:61-98) plus the shape
