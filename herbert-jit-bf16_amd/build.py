@@ -22,9 +22,10 @@ OUT = os.path.join(HERE, "hsdpa", "libhsdpa.so")
 # kernels and the element kernels, the attention kernels of the other head
 # dimensions, the decode passes under the Fused form, the short-chunk
 # prefill, the static scratch of the entry point that allocates nothing, the
-# decode passes of frame calls (rows and past read at run time), the C ABI
+# decode passes of frame calls (rows and past read at run time), the causal
+# prefill with the softmax sink, the C ABI
 SOURCES = ["hsdpa_kernels.hip", "hsdpa_attn_more.hip", "hsdpa_fused.hip", "hsdpa_prefill_short.hip",
-           "hsdpa_static.hip", "hsdpa_frame.hip", "hsdpa_api.cpp"]
+           "hsdpa_static.hip", "hsdpa_frame.hip", "hsdpa_sink.hip", "hsdpa_api.cpp"]
 HIPCC = os.environ.get("HIPCC", shutil.which("hipcc") or "/opt/rocm/bin/hipcc")
 
 # -ffp-contract=off: the exponential and the score scaling must round exactly

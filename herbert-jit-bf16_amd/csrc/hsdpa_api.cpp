@@ -48,7 +48,7 @@ hsdpa_status check_spec(const hsdpa_spec &s)
     if (s.head_dim % 32 != 0 || s.head_dim > 512) return HSDPA_ERR_HEAD_DIM;
     if (!hsdpa::head_dim_supported(static_cast<int>(s.head_dim))) return HSDPA_ERR_HEAD_DIM;
     if (s.heads % s.gqa != 0) return HSDPA_ERR_GQA;
-    if (s.sink != 0) return HSDPA_ERR_SINK_UNSUPPORTED;
+    if (s.sink > 1) return HSDPA_ERR_SINK_UNSUPPORTED;         // SdpaShape::sink is a flag
     const uint64_t lim = static_cast<uint64_t>(INT32_MAX) / 2;
     if (s.heads > lim || s.gqa > lim || s.q_row > lim || s.q_head > lim || s.out_row > lim)
         return HSDPA_ERR_STRIDE;
@@ -456,7 +456,9 @@ hsdpa_status hsdpa_plan_create(const hsdpa_spec *spec, hsdpa_plan **out)
     const uint64_t d = spec->head_dim, g = spec->gqa, kvh = spec->heads / spec->gqa;
     const uint64_t cap = spec->kv_capacity;
     p->kv_heads = kvh;
-    p->form = spec->form == HSDPA_FORM_FUSED && d <= 256 ? HSDPA_FORM_FUSED : HSDPA_FORM_CHAINED;
+    // the Fused form declines the sink (src/jit/emit_sdpa.rs:468-470) and the
+    // engine then emits the Chained one
+    p->form = spec->form == HSDPA_FORM_FUSED && d <= 256 && !spec->sink ? HSDPA_FORM_FUSED : HSDPA_FORM_CHAINED;
     if (p->form == HSDPA_FORM_FUSED && g > kFusedMaxGqa) {
         delete p;
         return HSDPA_ERR_FORM;
@@ -597,6 +599,8 @@ static hsdpa_status run_part(const hsdpa_plan *plan, const hsdpa_call *call, con
         a.pv_all = c.pv_all;
         a.direct = c.direct;
         a.scale = call->scale;
+        a.sink = call->sink;
+        a.sink_on = s.sink != 0;
         a.gate = gp;
         const hipError_t e = part.fused ? hsdpa::launch_decode_fused(a, d, static_cast<int>(plan->kv_heads), st)
                                         : hsdpa::launch_decode(a, d, static_cast<int>(plan->kv_heads), st);
@@ -616,6 +620,8 @@ static hsdpa_status run_part(const hsdpa_plan *plan, const hsdpa_call *call, con
     a.kv_stride = s.kv_stride;
     a.gqa = static_cast<int>(s.gqa);
     a.scale = call->scale;
+    a.sink = call->sink;
+    a.sink_on = s.sink != 0;
     a.gate = gp;
     a.gate_row = gate_row;
     hsdpa::PrefillSplit ps{};
@@ -633,7 +639,9 @@ static hsdpa_status run_part(const hsdpa_plan *plan, const hsdpa_call *call, con
     probe.units = hsdpa::kSplitUnits;
     const int sp_any = hsdpa::prefill_split_count(a, d, static_cast<int>(s.heads), probe);
     const uint64_t ntiles = (n + hsdpa::kKeyTile - 1) / hsdpa::kKeyTile;
-    if (sp_any > 1 && hsdpa::prefill_short_ok(d) && ntiles <= static_cast<uint64_t>(hsdpa::kShortMaxTiles)) {
+    // (not with the sink: those kernels are not instantiated with it)
+    if (sp_any > 1 && !a.sink_on && hsdpa::prefill_short_ok(d) &&
+        ntiles <= static_cast<uint64_t>(hsdpa::kShortMaxTiles)) {
         if (kernels) *kernels = HSDPA_KERNELS_CAUSAL_SHORT;
         if (splits) *splits = 1;
         if (launches) *launches += 1;
@@ -718,7 +726,6 @@ static hsdpa_status check_attention_call(const hsdpa_plan *plan, const hsdpa_cal
 hsdpa_status hsdpa_attention(const hsdpa_plan *plan, const hsdpa_call *call, void *stream)
 {
     if (!plan || !call) return HSDPA_ERR_NULL;
-    if (call->sink != 0.0f) return HSDPA_ERR_SINK_UNSUPPORTED;
     if (call->rows == 0) return HSDPA_OK;  // the selector's empty call (attention.rs:129-130)
     const hsdpa_status st = check_attention_call(plan, call);
     if (st != HSDPA_OK) return st;
@@ -732,7 +739,6 @@ hsdpa_status hsdpa_attention(const hsdpa_plan *plan, const hsdpa_call *call, voi
 hsdpa_status hsdpa_attention_static(const hsdpa_plan *plan, const hsdpa_call *call, void *stream)
 {
     if (!plan || !call) return HSDPA_ERR_NULL;
-    if (call->sink != 0.0f) return HSDPA_ERR_SINK_UNSUPPORTED;
     if (call->rows == 0) return HSDPA_OK;
     if (plan->ws_bytes > HSDPA_STATIC_SCRATCH_BYTES) return HSDPA_ERR_STATIC_SCRATCH;
     int cus = 0;
@@ -754,7 +760,6 @@ hsdpa_status hsdpa_attention_static(const hsdpa_plan *plan, const hsdpa_call *ca
 hsdpa_status hsdpa_attention_frame(const hsdpa_plan *plan, const hsdpa_frame_call *call, void *stream)
 {
     if (!plan || !call) return HSDPA_ERR_NULL;
-    if (call->sink != 0.0f) return HSDPA_ERR_SINK_UNSUPPORTED;
     const hsdpa_spec &s = plan->spec;
     const int d = static_cast<int>(s.head_dim);
     const int sub = s.gqa <= static_cast<uint64_t>(4 * hsdpa::kDecodeMaxGroup)
@@ -803,6 +808,8 @@ hsdpa_status hsdpa_attention_frame(const hsdpa_plan *plan, const hsdpa_frame_cal
     a.q_row = s.q_row;
     a.out_row = s.out_row;
     a.scale = call->scale;
+    a.sink = call->sink;
+    a.sink_on = s.sink != 0;
     a.f_rows = call->rows;
     a.f_past = call->past;
     a.f_status = call->status;
@@ -838,8 +845,11 @@ hsdpa_status hsdpa_attention_route(const hsdpa_plan *plan, uint64_t rows, uint64
 hsdpa_status hsdpa_attention_layer(const hsdpa_plan *plan, const hsdpa_layer_call *call, void *stream)
 {
     if (!plan || !call) return HSDPA_ERR_NULL;
-    if (call->rows == 0) return HSDPA_OK;
     const hsdpa_spec &s = plan->spec;
+    // the layer's attention node has no sink (its shape: src/jit/schedule/scheduler.rs:111,
+    // its call: src/jit/schedule/lowering.rs:609), and the layer call carries none
+    if (s.sink) return HSDPA_ERR_SINK_UNSUPPORTED;
+    if (call->rows == 0) return HSDPA_OK;
     // the two head-norm-rope nodes (q, then k), checked as hsdpa_head_norm_rope does
     const hsdpa_norm_rope_spec qs = {s.heads, s.head_dim, s.q_head, s.q_row, call->rotary_dims,
                                      call->table_row, call->positions, call->plus_one, 0};

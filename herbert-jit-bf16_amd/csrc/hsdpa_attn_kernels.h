@@ -842,6 +842,8 @@ __global__ __launch_bounds__(64 * W, D > 256 ? 1 : 8 / W) void decode_pv(DecodeA
     // 2. exact maximum per query head (FUSED: the running maximum entering the
     //    workgroup): a DPP reduction over the head's lanes
     m = group_max_hi(m, T);
+    // the sink joins the maximum (the Fused form declines it)
+    if (!FUSED && a.sink_on) m = m > a.sink ? m : a.sink;
     if (u == T - 1 && jh < a.g) smax[jh] = m;
     __syncthreads();
 
@@ -1046,6 +1048,8 @@ __global__ __launch_bounds__(64 * W, D > 256 ? 1 : 8 / W) void decode_pv(DecodeA
         const int p0 = (tid % (THREADS / KEYS)) * (KEYS / 64);
         float L = 0.0f;
         for (int w = 0; w < KEYS / 64; w++) L += lpart[p0 + w][tid];
+        // the sink's exponential, once per column: in workgroup 0's sum
+        if (!FUSED && a.sink_on && wg == 0) L += exp_poly(a.sink - smax[tid]);
         a.part_l[pbase + tid] = L;
         if constexpr (FUSED) a.part_x[pbase + tid] = fxw[tid];
     }
@@ -1124,10 +1128,14 @@ __global__ __launch_bounds__(512, 1) void decode_pv_all(DecodeArgs a)
             for (int b = 0; b < BATCH; b++) m = (w0 + b * T < a.nwg_qk && mx[b] > m) ? mx[b] : m;
         }
         m = group_max_hi(m, T);
+        if (a.sink_on) m = m > a.sink ? m : a.sink;             // the sink joins the maximum
         // the previous group's P operand reads and partial sums are done
         // before this barrier, so its slots may be rewritten after it
         if (u == T - 1 && jh < a.g) smax[jh] = m;
         __syncthreads();
+        // column tid's maximum, for the sink's term (smax is rewritten by the
+        // next group once every wave has passed this group's second barrier)
+        const float mcol = tid < a.g ? smax[tid] : 0.0f;
 #pragma unroll
         for (int i = 0; i < kDecodeMaxGroup / 2; i++) {
             const int h = tid / KEYS + 2 * i;
@@ -1179,6 +1187,7 @@ __global__ __launch_bounds__(512, 1) void decode_pv_all(DecodeArgs a)
             const int p0 = (tid % (THREADS / KEYS)) * (KEYS / 64);
             float L = 0.0f;
             for (int w = 0; w < KEYS / 64; w++) L += lpart[p0 + w][tid];
+            if (a.sink_on && wg == 0) L += exp_poly(a.sink - mcol);  // once per column
             a.part_l[pbase + tid] = L;
         }
     };
@@ -1289,7 +1298,8 @@ __global__ __launch_bounds__(512, 1) void decode_direct(DecodeArgs a)
             fcf[wave * NB + l] = c;
         }
     } else {
-        const float m = group_max_hi(mxv, 32);
+        float m = group_max_hi(mxv, 32);
+        if (a.sink_on) m = m > a.sink ? m : a.sink;             // the sink joins the maximum
         if (ml == 31 && mcol < g) smax[mcol] = m;
     }
     __syncthreads();
@@ -1361,6 +1371,7 @@ __global__ __launch_bounds__(512, 1) void decode_direct(DecodeArgs a)
         // columns of parity p were summed by waves 4 p .. 4 p + 3
 #pragma unroll
         for (int w = 0; w < 4; w++) L += lpart[4 * (hc & 1) + w][hc];
+        if (!FUSED && a.sink_on) L += exp_poly(a.sink - smax[hc]);
         // the column's (row, head) and where its output goes
         const int row = MR ? hc / a.G : 0, head = kvh * a.G + hc - row * a.G;
         const uint64_t obase = static_cast<uint64_t>(row) * a.out_row + static_cast<uint64_t>(head) * D + d0 + 4 * G;
@@ -1379,7 +1390,7 @@ __global__ __launch_bounds__(512, 1) void decode_direct(DecodeArgs a)
             for (int r = 0; r < 4; r++) {
                 // hi column + lo column
                 const float os = NCB == 1 ? sum[0][r] + row_xor8(sum[0][r]) : sum[0][r] + sum[NCB - 1][r];
-                ob[r] = static_cast<uint16_t>(cvt_out(FUSED ? os * (1.0f / L) : os / L));
+                ob[r] = static_cast<uint16_t>(cvt_out(FUSED || a.sink_on ? os * (1.0f / L) : os / L));
             }
             if (j < CM && h < g) {
 #pragma unroll
@@ -1500,7 +1511,8 @@ __global__ __launch_bounds__(512) void decode_combine(DecodeArgs a)
             os += ored[i][t];
             ls += lred[i];
         }
-        uint16_t ob = static_cast<uint16_t>(cvt_out(FUSED ? os * (1.0f / ls) : os / ls));
+        // the Fused form and the sink normalise by the reciprocal (decode.rs:653-659, 280-290)
+        uint16_t ob = static_cast<uint16_t>(cvt_out(FUSED || a.sink_on ? os * (1.0f / ls) : os / ls));
         uint64_t oat = static_cast<uint64_t>(h) * D + dim, gat = oat;
         if constexpr (MR) {
             // group kvh = y sub + z; its column jh is column z g + jh of KV head y
@@ -1575,7 +1587,55 @@ __device__ __forceinline__ void split_pack_hw(const float *e, u32x4 &hi, u32x4 &
     }
 }
 
-template <int D, int HPW, bool POW2, int NW = 8>
+// The sink joins a causal row's maximum m (under POW2 the maximum of the
+// unscaled dot products, as the kernels keep it): the scaled maximum becomes
+// the larger of M and the sink (vmaxss, decode.rs:239-290), returned in ms;
+// the result is the maximum the exponentials take, ms / scale under POW2
+// (exact for a power of two; a quotient past the f32 range is infinite, and
+// every exponential then clamps as the reference's does).
+template <bool POW2>
+__device__ __forceinline__ float sink_max(float m, const PrefillArgs &a, float &ms)
+{
+    const float s = POW2 ? m * a.scale : m;
+    ms = s > a.sink ? s : a.sink;
+    return POW2 ? ms / a.scale : ms;
+}
+
+// A row's normalisation: the division by its sum, or (the sink) the
+// product with the sum's reciprocal.
+struct div_norm {
+    float l;
+    __device__ __forceinline__ float operator()(float x) const { return x / l; }
+};
+struct rcp_norm {
+    float inv;
+    __device__ __forceinline__ float operator()(float x) const { return x * inv; }
+};
+
+// The outputs of one row held in the 32x32 accumulators o (lane: row
+// col, dimensions 32 dt + 8 c + 4 grp ..), normalised, gated, stored.
+template <int D, typename N>
+__device__ __forceinline__ void store_rows(const f32x16 *o, uint16_t *op, const uint16_t *gp, int grp, N nrm)
+{
+#pragma unroll
+    for (int dt = 0; dt < D / 32; dt++)
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            uint32_t b0 = cvt_out(nrm(o[dt][4 * c])), b1 = cvt_out(nrm(o[dt][4 * c + 1]));
+            uint32_t b2 = cvt_out(nrm(o[dt][4 * c + 2])), b3 = cvt_out(nrm(o[dt][4 * c + 3]));
+            const int at = 32 * dt + 8 * c + 4 * grp;
+            if (gp) {
+                const uint2 g = *reinterpret_cast<const uint2 *>(gp + at);
+                b0 = gate_bf16(static_cast<uint16_t>(b0), static_cast<uint16_t>(g.x));
+                b1 = gate_bf16(static_cast<uint16_t>(b1), static_cast<uint16_t>(g.x >> 16));
+                b2 = gate_bf16(static_cast<uint16_t>(b2), static_cast<uint16_t>(g.y));
+                b3 = gate_bf16(static_cast<uint16_t>(b3), static_cast<uint16_t>(g.y >> 16));
+            }
+            *reinterpret_cast<uint2 *>(op + at) = uint2{b0 | (b1 << 16), b2 | (b3 << 16)};
+        }
+}
+
+template <int D, int HPW, bool POW2, int NW = 8, bool SINK = false>
 __global__ __launch_bounds__(64 * NW, 1) void prefill_attn(PrefillArgs a)
 {
     constexpr int RB = NW / HPW, THREADS = 64 * NW;
@@ -1651,6 +1711,8 @@ __global__ __launch_bounds__(64 * NW, 1) void prefill_attn(PrefillArgs a)
         __syncthreads();
     }
     m = __builtin_fmaxf(m, __shfl_xor(m, 32));
+    float ms = 0.0f;                                            // the scaled maximum, with the sink
+    if constexpr (SINK) m = sink_max<POW2>(m, a, ms);
     ExpArgs ex;
     ex.m = m;
     ex.scale = a.scale;
@@ -1667,7 +1729,9 @@ __global__ __launch_bounds__(64 * NW, 1) void prefill_attn(PrefillArgs a)
     f32x16 o[D / 32];
 #pragma unroll
     for (int dt = 0; dt < D / 32; dt++) o[dt] = f32x16{};
-    float lsum = 0.0f;
+    // the sink's exponential starts the row's sum (in one of its two lanes),
+    // so that nothing of it stays live across the tiles
+    float lsum = SINK && grp == 0 ? exp_poly(a.sink - ms) : 0.0f;
     for (int t = 0; t < ntiles; t++) {
         const uint64_t t0 = static_cast<uint64_t>(t) * kKeyTile;
         const int b = t & 1;
@@ -1718,23 +1782,9 @@ __global__ __launch_bounds__(64 * NW, 1) void prefill_attn(PrefillArgs a)
     if (rowv) {
         uint16_t *op = a.out + row * a.out_row + static_cast<uint64_t>(head) * D;
         const uint16_t *gp = a.gate ? a.gate + row * a.gate_row + static_cast<uint64_t>(head) * D : nullptr;
-#pragma unroll
-        for (int dt = 0; dt < D / 32; dt++)
-#pragma unroll
-            for (int c = 0; c < 4; c++) {
-                uint32_t b0 = cvt_out(o[dt][4 * c] / lsum), b1 = cvt_out(o[dt][4 * c + 1] / lsum);
-                uint32_t b2 = cvt_out(o[dt][4 * c + 2] / lsum), b3 = cvt_out(o[dt][4 * c + 3] / lsum);
-                const int at = 32 * dt + 8 * c + 4 * grp;
-                if (gp) {
-                    const uint2 g = *reinterpret_cast<const uint2 *>(gp + at);
-                    b0 = gate_bf16(static_cast<uint16_t>(b0), static_cast<uint16_t>(g.x));
-                    b1 = gate_bf16(static_cast<uint16_t>(b1), static_cast<uint16_t>(g.x >> 16));
-                    b2 = gate_bf16(static_cast<uint16_t>(b2), static_cast<uint16_t>(g.y));
-                    b3 = gate_bf16(static_cast<uint16_t>(b3), static_cast<uint16_t>(g.y >> 16));
-                }
-                uint2 w = {b0 | (b1 << 16), b2 | (b3 << 16)};
-                *reinterpret_cast<uint2 *>(op + at) = w;
-            }
+        // O / l, or with the sink O times 1 / l
+        if constexpr (SINK) store_rows<D>(o, op, gp, grp, rcp_norm{1.0f / lsum});
+        else store_rows<D>(o, op, gp, grp, div_norm{lsum});
     }
 }
 
@@ -2434,7 +2484,7 @@ __global__ __launch_bounds__(64 * NW, 1) void prefill_split_max(PrefillArgs a, S
     if (PAIRED && segs.n > 1) run(segs.s1);
 }
 
-template <int D, int HPW, bool POW2, int NW, bool PAIRED = false>
+template <int D, int HPW, bool POW2, int NW, bool PAIRED = false, bool SINK = false>
 __global__ __launch_bounds__(64 * NW, 1) void prefill_split_pv(PrefillArgs a, SplitArgs sp)
 {
     constexpr int RB = NW / HPW, THREADS = 64 * NW;
@@ -2470,6 +2520,8 @@ __global__ __launch_bounds__(64 * NW, 1) void prefill_split_pv(PrefillArgs a, Sp
             for (int z = 0; z < nz; z++)
                 m = __builtin_fmaxf(m, sp.smax[(static_cast<uint64_t>(z) * sp.heads + head) * a.rows + row]);
         }
+        float ms = 0.0f;                                        // the scaled maximum, with the sink
+        if constexpr (SINK) m = sink_max<POW2>(m, a, ms);
         ExpArgs ex;
         ex.m = m;
         ex.scale = a.scale;
@@ -2487,7 +2539,9 @@ __global__ __launch_bounds__(64 * NW, 1) void prefill_split_pv(PrefillArgs a, Sp
         f32x16 o[D / 32];
 #pragma unroll
         for (int dt = 0; dt < D / 32; dt++) o[dt] = f32x16{};
-        float lsum = 0.0f;
+        // the sink's exponential, once per row: it starts the sum of the whole
+        // range's or of slot 0's (in one lane of two)
+        float lsum = SINK && (DIRECT || sg.slot == 0) && grp == 0 ? exp_poly(a.sink - ms) : 0.0f;
         if (tb < te) {
             tile_gload<D, THREADS, false>(kg, static_cast<uint64_t>(tb) * kKeyTile, a.n, tid, kr);
             tile_gload<D, THREADS, false>(vg, static_cast<uint64_t>(tb) * kKeyTile, a.n, tid, vr);
@@ -2552,22 +2606,8 @@ __global__ __launch_bounds__(64 * NW, 1) void prefill_split_pv(PrefillArgs a, Sp
             // a whole row group: its output, as prefill_attn writes it
             uint16_t *op = a.out + row * a.out_row + static_cast<uint64_t>(head) * D;
             const uint16_t *gp = a.gate ? a.gate + row * a.gate_row + static_cast<uint64_t>(head) * D : nullptr;
-#pragma unroll
-            for (int dt = 0; dt < D / 32; dt++)
-#pragma unroll
-                for (int c = 0; c < 4; c++) {
-                    uint32_t b0 = cvt_out(o[dt][4 * c] / lsum), b1 = cvt_out(o[dt][4 * c + 1] / lsum);
-                    uint32_t b2 = cvt_out(o[dt][4 * c + 2] / lsum), b3 = cvt_out(o[dt][4 * c + 3] / lsum);
-                    const int at = 32 * dt + 8 * c + 4 * grp;
-                    if (gp) {
-                        const uint2 g = *reinterpret_cast<const uint2 *>(gp + at);
-                        b0 = gate_bf16(static_cast<uint16_t>(b0), static_cast<uint16_t>(g.x));
-                        b1 = gate_bf16(static_cast<uint16_t>(b1), static_cast<uint16_t>(g.x >> 16));
-                        b2 = gate_bf16(static_cast<uint16_t>(b2), static_cast<uint16_t>(g.y));
-                        b3 = gate_bf16(static_cast<uint16_t>(b3), static_cast<uint16_t>(g.y >> 16));
-                    }
-                    *reinterpret_cast<uint2 *>(op + at) = uint2{b0 | (b1 << 16), b2 | (b3 << 16)};
-                }
+            if constexpr (SINK) store_rows<D>(o, op, gp, grp, rcp_norm{1.0f / lsum});
+            else store_rows<D>(o, op, gp, grp, div_norm{lsum});
         } else {
             const uint64_t cell = (static_cast<uint64_t>(sg.slot) * sp.srows + (row - sp.r0)) * sp.heads + head;
             float *op = sp.so + cell * D;
@@ -2616,7 +2656,7 @@ static bool scale_is_pow2(float s)
 // The three split kernels on grid (row groups, head groups, splits). POW2:
 // whether a power-of-two scale takes the folded form (the general form rounds
 // identically).
-template <int D, int HPW, int NW, bool POW2_FORM = true>
+template <int D, int HPW, int NW, bool POW2_FORM = true, bool SINK = false>
 static hipError_t launch_prefill_split(const PrefillArgs &a, int heads, const PrefillSplit &ps, dim3 grid, int splits,
                                        hipStream_t s)
 {
@@ -2625,10 +2665,10 @@ static hipError_t launch_prefill_split(const PrefillArgs &a, int heads, const Pr
     hipError_t e;
     if (POW2_FORM && scale_is_pow2(a.scale)) {
         e = launch(prefill_split_max<D, HPW, POW2_FORM, NW>, gs, dim3(64 * NW), s, a, sp);
-        if (e == hipSuccess) e = launch(prefill_split_pv<D, HPW, POW2_FORM, NW>, gs, dim3(64 * NW), s, a, sp);
+        if (e == hipSuccess) e = launch(prefill_split_pv<D, HPW, POW2_FORM, NW, false, SINK>, gs, dim3(64 * NW), s, a, sp);
     } else {
         e = launch(prefill_split_max<D, HPW, false, NW>, gs, dim3(64 * NW), s, a, sp);
-        if (e == hipSuccess) e = launch(prefill_split_pv<D, HPW, false, NW>, gs, dim3(64 * NW), s, a, sp);
+        if (e == hipSuccess) e = launch(prefill_split_pv<D, HPW, false, NW, false, SINK>, gs, dim3(64 * NW), s, a, sp);
     }
     if (e != hipSuccess) return e;
     const dim3 gc(static_cast<unsigned>(a.rows), heads);
@@ -2639,7 +2679,7 @@ static hipError_t launch_prefill_split(const PrefillArgs &a, int heads, const Pr
 
 // The paired form on the causal kernel's grid (row groups, head groups); pr
 // from prefill_pairs.
-template <int D, int HPW, int NW, bool POW2_FORM = true>
+template <int D, int HPW, int NW, bool POW2_FORM = true, bool SINK = false>
 static hipError_t launch_prefill_paired(const PrefillArgs &a, int heads, const PrefillSplit &ps, dim3 grid,
                                         const PairRows &pr, hipStream_t s)
 {
@@ -2647,10 +2687,11 @@ static hipError_t launch_prefill_paired(const PrefillArgs &a, int heads, const P
     hipError_t e;
     if (POW2_FORM && scale_is_pow2(a.scale)) {
         e = launch(prefill_split_max<D, HPW, POW2_FORM, NW, true>, grid, dim3(64 * NW), s, a, sp);
-        if (e == hipSuccess) e = launch(prefill_split_pv<D, HPW, POW2_FORM, NW, true>, grid, dim3(64 * NW), s, a, sp);
+        if (e == hipSuccess)
+            e = launch(prefill_split_pv<D, HPW, POW2_FORM, NW, true, SINK>, grid, dim3(64 * NW), s, a, sp);
     } else {
         e = launch(prefill_split_max<D, HPW, false, NW, true>, grid, dim3(64 * NW), s, a, sp);
-        if (e == hipSuccess) e = launch(prefill_split_pv<D, HPW, false, NW, true>, grid, dim3(64 * NW), s, a, sp);
+        if (e == hipSuccess) e = launch(prefill_split_pv<D, HPW, false, NW, true, SINK>, grid, dim3(64 * NW), s, a, sp);
     }
     if (e != hipSuccess) return e;
     return launch(prefill_split_combine<D>, dim3(static_cast<unsigned>(pr.srows), heads), dim3(D), s, a, sp, 2);
@@ -2667,7 +2708,7 @@ __global__ __launch_bounds__(D) void prefill_split_combine(PrefillArgs a, SplitA
         o += sp.so[cell * D + dim];
         ls += sp.sl[cell];
     }
-    uint16_t ob = static_cast<uint16_t>(cvt_out(o / ls));
+    uint16_t ob = static_cast<uint16_t>(cvt_out(a.sink_on ? o * (1.0f / ls) : o / ls));   // the sink: O times 1 / l
     if (a.gate) ob = gate_bf16(ob, a.gate[row * a.gate_row + head * D + dim]);
     a.out[row * a.out_row + head * D + dim] = ob;
 }
@@ -2726,8 +2767,14 @@ __global__ __launch_bounds__(CombineShape<D>::THREADS) void prefill_split_combin
     }
     const float sv[4] = {sum.x, sum.y, sum.z, sum.w};
     uint16_t ob[4];
+    if (a.sink_on) {
+        const float inv = 1.0f / L;                             // the sink: O times 1 / l
 #pragma unroll
-    for (int r = 0; r < 4; r++) ob[r] = static_cast<uint16_t>(cvt_out(sv[r] / L));
+        for (int r = 0; r < 4; r++) ob[r] = static_cast<uint16_t>(cvt_out(sv[r] * inv));
+    } else {
+#pragma unroll
+        for (int r = 0; r < 4; r++) ob[r] = static_cast<uint16_t>(cvt_out(sv[r] / L));
+    }
     if (a.gate) {
         const uint2 gw = *reinterpret_cast<const uint2 *>(a.gate + row * a.gate_row + head * D + 4 * t);
         const uint16_t gv[4] = {static_cast<uint16_t>(gw.x), static_cast<uint16_t>(gw.x >> 16),

@@ -79,6 +79,12 @@ struct DecodeArgs {
     int f_groups;           // kv_heads * sub
     int f_cus;              // compute units the grids were sized for
     int f_loop;             // 1: pass 2 walks a run of keys per workgroup (decode_pv_loop_ok)
+    // The softmax sink (SdpaShape::sink), the Chained kernels only: with
+    // sink_on, each column's maximum is the larger of its scores' and `sink`,
+    // the sum of its exponentials gains P(sink - M) (pass-2 workgroup 0 adds
+    // it to its partial sum), and the output is the sum times its reciprocal.
+    float sink;
+    int sink_on;
 };
 
 // Causal prefill: `rows` query rows after `past` cached positions.
@@ -93,6 +99,11 @@ struct PrefillArgs {
     float scale;
     const uint16_t *gate;   // null, or the output gate: row r, head h at gate + r*gate_row + h*head_dim
     uint64_t gate_row;
+    // The softmax sink, as DecodeArgs': the row maximum is the larger of the
+    // scores' and `sink`, the row sum gains P(sink - M), and the output is the
+    // sum times its reciprocal.
+    float sink;
+    int sink_on;
 };
 
 // The split form of the causal kernel (see prefill_split_max): workspace for
@@ -285,6 +296,9 @@ hipError_t static_scratch(void **ptr);
 // the pass-2 workgroups a Fused combine can scan per head (its LDS)
 constexpr int kFusedMaxSeg = 512;
 hipError_t launch_prefill_more(const PrefillArgs &a, int head_dim, int heads, const PrefillSplit &ps, hipStream_t s);
+// the causal prefill with the softmax sink, every head dimension (hsdpa_sink.hip):
+// one query head per workgroup, as the grid of prefill_hpw for a sink call
+hipError_t launch_prefill_sink(const PrefillArgs &a, int head_dim, int heads, const PrefillSplit &ps, hipStream_t s);
 
 // Splits for a causal call whose one-workgroup grid has `wgs` workgroups: enough
 // to fill the compute units once, at least 4 tiles of the longest row group

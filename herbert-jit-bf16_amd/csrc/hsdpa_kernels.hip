@@ -367,6 +367,7 @@ hipError_t launch_decode(const DecodeArgs &a, int head_dim, int kv_heads, hipStr
 // that divides the group size), one head x 32 NW rows at the others.
 static int prefill_hpw(const PrefillArgs &a, int head_dim)
 {
+    if (a.sink_on) return 1;                                    // launch_prefill_sink's grid
     if (head_dim == 64 || head_dim == 128 || head_dim == 256)
         return a.gqa % 8 == 0 ? 8 : a.gqa % 4 == 0 ? 4 : a.gqa % 2 == 0 ? 2 : 1;
     return 1;
@@ -445,6 +446,7 @@ hipError_t launch_gate(const GateArgs &a, hipStream_t s)
 
 hipError_t launch_prefill(const PrefillArgs &a, int head_dim, int heads, const PrefillSplit &ps, hipStream_t s)
 {
+    if (a.sink_on) return launch_prefill_sink(a, head_dim, heads, ps, s);
     switch (head_dim) {
     case 64: return prefill_d<64>(a, heads, ps, s);
     case 128: return prefill_d<128>(a, heads, ps, s);

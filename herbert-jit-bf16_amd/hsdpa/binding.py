@@ -210,9 +210,9 @@ class Plan:
 
     def attention_frame_raw(self, q: int, keys: int, values: int, output: int, rows_ptr: int, past_ptr: int,
                             scale: float, workspace: int, workspace_bytes: int, status_ptr: int = 0,
-                            stream: int = 0) -> None:
+                            stream: int = 0, sink: float = 0.0) -> None:
         """hsdpa_attention_frame: rows and past are device pointers the kernels read."""
-        call = FrameCall(q, keys, values, output, rows_ptr, past_ptr, scale, 0.0, workspace, workspace_bytes,
+        call = FrameCall(q, keys, values, output, rows_ptr, past_ptr, scale, sink, workspace, workspace_bytes,
                          status_ptr)
         rc = library().hsdpa_attention_frame(self._h, ctypes.byref(call), ctypes.c_void_p(stream))
         if rc != 0:
@@ -230,9 +230,11 @@ class Plan:
             pass
 
 
-def attention_torch(plan: Plan, q, k, v, out, rows: int, past: int, scale: float, workspace, stream=None) -> None:
+def attention_torch(plan: Plan, q, k, v, out, rows: int, past: int, scale: float, workspace, stream=None,
+                    sink: float = 0.0) -> None:
     """Enqueue the node on torch device tensors (uint16/int16/bfloat16 views of
-    bf16 data). `workspace` is a uint8 device tensor of plan.workspace_bytes."""
+    bf16 data). `workspace` is a uint8 device tensor of plan.workspace_bytes;
+    `sink` is the sink's score, read when the plan has the sink flag."""
     import torch
 
     for t in (q, k, v, out, workspace):
@@ -240,7 +242,7 @@ def attention_torch(plan: Plan, q, k, v, out, rows: int, past: int, scale: float
             raise ValueError("tensors must be contiguous device tensors")
     s = torch.cuda.current_stream() if stream is None else stream
     plan.attention_raw(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), rows, past, scale,
-                       workspace.data_ptr(), workspace.numel() * workspace.element_size(), s.cuda_stream)
+                       workspace.data_ptr(), workspace.numel() * workspace.element_size(), s.cuda_stream, sink)
 
 
 def kv_spec(heads: int, head_dim: int, capacity: int, max_batch: int, stride: int | None = None,

@@ -70,7 +70,8 @@ typedef enum hsdpa_status {
     HSDPA_ERR_STRIDE = 4,           /* q_head < head_dim, heads*q_head > q_row,
                                        heads*head_dim > out_row, kv_stride < capacity*head_dim
                                        (attention.rs:65-75, abi.rs:78-84) */
-    HSDPA_ERR_SINK_UNSUPPORTED = 5, /* a softmax sink: never emitted for this model */
+    HSDPA_ERR_SINK_UNSUPPORTED = 5, /* spec.sink above 1, or a layer call on a plan with the
+                                       sink (the layer's node has none: scheduler.rs:111) */
     HSDPA_ERR_CAPACITY = 6,         /* past + rows > kv_capacity (model/mounted.rs:634-670) */
     HSDPA_ERR_WORKSPACE = 7,        /* workspace missing or smaller than hsdpa_workspace_bytes */
     HSDPA_ERR_ALIGNMENT = 8,        /* a pointer or stride not 16-byte aligned */
@@ -121,7 +122,11 @@ typedef struct hsdpa_spec {
     uint64_t kv_capacity;  /* positions reserved per KV head */
     uint64_t kv_stride;    /* elements between two KV heads of one cache (>= kv_capacity*head_dim) */
     uint32_t grouped;      /* AttentionSpec::grouped: task order only, no effect on results */
-    uint32_t sink;         /* SdpaShape::sink: must be 0 */
+    uint32_t sink;         /* SdpaShape::sink (ir.rs:55-60): 0, or 1 for the softmax sink of the call's
+                              `sink` value: the maximum becomes max(scores, sink), the sum gains
+                              exp(sink - max) (decode.rs:239-290); a Fused plan with the sink runs
+                              the Chained form, as the engine does when Fused declines it
+                              (emit_sdpa.rs:468-470) */
     uint32_t form;         /* hsdpa_form */
     uint32_t reserved;     /* 0 */
     uint64_t max_rows;     /* the most rows one call will pass (0: any, up to kv_capacity); sizes the
@@ -139,7 +144,8 @@ typedef struct hsdpa_call {
     uint64_t rows;           /* rows of this call: 1 = decode, more = causal prefill, 0 = nothing */
     uint64_t past;           /* positions cached before the first row; row r sees past+r+1 keys */
     float scale;             /* 1/sqrt(head_dim) in the engine (src/jit/schedule.rs:189-192) */
-    float sink;              /* must be 0 */
+    float sink;              /* the sink's score (AttentionCall::sink, abi.rs:174): read when spec.sink is
+                                1, ignored otherwise */
     void *workspace;         /* device scratch of at least hsdpa_workspace_bytes() */
     uint64_t workspace_bytes;
 } hsdpa_call;
@@ -240,7 +246,7 @@ typedef struct hsdpa_frame_call {
     const uint64_t *rows;     /* device memory, 8-byte aligned: read when the kernels run */
     const uint64_t *past;     /* device memory, 8-byte aligned: read when the kernels run */
     float scale;
-    float sink;               /* must be 0 */
+    float sink;               /* as hsdpa_call */
     void *workspace;          /* device scratch of at least hsdpa_workspace_bytes() */
     uint64_t workspace_bytes;
     uint32_t *status;         /* device memory or NULL: receives the step's hsdpa_status when it runs */

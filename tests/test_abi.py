@@ -56,7 +56,7 @@ def test_status_strings_and_version():
     (dict(heads=16, gqa=8, head_dim=16, kv_capacity=10), "HSDPA_ERR_HEAD_DIM"),
     (dict(heads=16, gqa=8, head_dim=544, kv_capacity=10), "HSDPA_ERR_HEAD_DIM"),
     (dict(heads=16, gqa=8, head_dim=1024, kv_capacity=10), "HSDPA_ERR_HEAD_DIM"),
-    (dict(heads=16, gqa=8, head_dim=256, kv_capacity=10, sink=True), "HSDPA_ERR_SINK_UNSUPPORTED"),
+    (dict(heads=16, gqa=8, head_dim=256, kv_capacity=10, sink=2), "HSDPA_ERR_SINK_UNSUPPORTED"),
     (dict(heads=0, gqa=1, head_dim=256, kv_capacity=1), "HSDPA_ERR_EMPTY"),
     (dict(heads=16, gqa=8, head_dim=0, kv_capacity=1), "HSDPA_ERR_EMPTY"),
     (dict(heads=16, gqa=8, head_dim=256, kv_capacity=10, q_head=128), "HSDPA_ERR_STRIDE"),
@@ -152,6 +152,9 @@ def test_route_names_the_kernels():
     assert (r["main"], r["tail"], r["tail_rows"], r["tail_form"]) == ("causal_paired", "few_rows", 3, "fused")
     # above head_dim 256 the Fused form falls back to Chained
     assert hsdpa.Plan(4, 2, 288, 100, form="fused").route(1, 10)["main_form"] == "chained"
+    # the Fused form declines the sink (emit_sdpa.rs:468-470): Chained, on every part
+    r = hsdpa.Plan(16, 8, 256, 40000, form="fused", sink=True).route(13, 100)
+    assert (r["main_form"], r["tail_form"]) == ("chained", "chained")
     # a group size with no equal split into groups of at most 16 (17) takes padded
     # groups on the decode kernels at the tuned head dimensions...
     r = hsdpa.Plan(17, 17, 128, 100, form="fused").route(1, 10)
@@ -233,9 +236,11 @@ def test_frame_call_refusals_before_any_device_work():
     assert _frame(p, status=0x60002) == "HSDPA_ERR_ALIGNMENT"
     assert _frame(p, q=0x10008) == "HSDPA_ERR_ALIGNMENT"
     assert _frame(p, workspace_bytes=p.workspace_bytes - 1) == "HSDPA_ERR_WORKSPACE"
-    assert _frame(p, sink=1.0) == "HSDPA_ERR_SINK_UNSUPPORTED"
-    # every check passed: with no GPU the device check refuses
+    # every check passed: with no GPU the device check refuses (a sink value
+    # without the plan's sink flag is ignored, as the reference's call does)
     assert _frame(p) == "HSDPA_ERR_NO_DEVICE"
+    assert _frame(p, sink=1.0) == "HSDPA_ERR_NO_DEVICE"
+    assert _frame(hsdpa.Plan(16, 8, 256, 4096, max_rows=1, sink=True), sink=1.0) == "HSDPA_ERR_NO_DEVICE"
     assert _frame(hsdpa.Plan(64, 32, 128, 4096, max_rows=1, form="fused")) == "HSDPA_ERR_NO_DEVICE"
 
 
@@ -245,7 +250,8 @@ def test_call_refusals_before_any_device_work():
     assert _name(_call(p, rows=2, past=99)) == "HSDPA_ERR_CAPACITY"
     assert _name(_call(p, rows=101)) == "HSDPA_ERR_CAPACITY"
     assert _name(_call(p, rows=1, past=2**63)) == "HSDPA_ERR_CAPACITY"
-    assert _name(_call(p, sink=0.5)) == "HSDPA_ERR_SINK_UNSUPPORTED"
+    assert _name(_call(p, sink=0.5)) == "HSDPA_ERR_NO_DEVICE"        # ignored without the flag
+    assert _name(_call(hsdpa.Plan(16, 8, 256, 100, sink=True), sink=0.5)) == "HSDPA_ERR_NO_DEVICE"
     assert _name(_call(p, q=0)) == "HSDPA_ERR_NULL"
     assert _name(_call(p, ws=0)) == "HSDPA_ERR_NULL"
     assert _name(_call(p, k=0x20002)) == "HSDPA_ERR_ALIGNMENT"

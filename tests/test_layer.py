@@ -66,3 +66,12 @@ def test_layer_accepts_no_rope_and_no_gate_on_the_host():
     assert rc(p, rotary_dims=0, cos=0, sin=0, table_row=0, positions=0) == "HSDPA_ERR_NO_DEVICE"
     assert rc(p, gate=0, gate_row=0) == "HSDPA_ERR_NO_DEVICE"
     assert hsdpa.library().hsdpa_attention_layer(None, None, None) == 9
+
+
+def test_layer_refuses_a_plan_with_the_sink():
+    """The layer's attention node has no sink (src/jit/schedule/scheduler.rs:111)
+    and the layer call carries no sink value: a plan with the flag is refused,
+    before anything else, even for an empty call."""
+    p = hsdpa.Plan(HEADS, GQA, HD, CAP, q_row=Q_ROW, sink=True)
+    assert rc(p) == "HSDPA_ERR_SINK_UNSUPPORTED"
+    assert rc(p, rows=0, q=0) == "HSDPA_ERR_SINK_UNSUPPORTED"
