@@ -914,7 +914,7 @@ const char *hsdpa_status_string(hsdpa_status status)
     case HSDPA_ERR_HEAD_DIM: return "head_dim out of domain (a multiple of 32 from 32 to 512)";
     case HSDPA_ERR_GQA: return "heads is not a multiple of gqa";
     case HSDPA_ERR_STRIDE: return "invalid q/out/kv strides for this geometry";
-    case HSDPA_ERR_SINK_UNSUPPORTED: return "softmax sink is not supported";
+    case HSDPA_ERR_SINK_UNSUPPORTED: return "sink flag above 1, or a layer call on a plan with the sink";
     case HSDPA_ERR_CAPACITY: return "past + rows exceeds the KV capacity";
     case HSDPA_ERR_WORKSPACE: return "workspace missing or too small";
     case HSDPA_ERR_ALIGNMENT: return "pointer or stride not 16-byte aligned";
