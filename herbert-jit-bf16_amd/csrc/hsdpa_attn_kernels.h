@@ -1411,7 +1411,8 @@ __global__ __launch_bounds__(512, 1) void decode_direct(DecodeArgs a)
 // FUSED: the partials of workgroup w are relative to the running maximum at
 // its end; the product S_w of the later workgroups' correction products
 // brings them to the last one's (out = sum S_w O_w / sum S_w l_w). S_w comes
-// from a doubling scan in LDS over segments of kFusedMaxSeg workgroups, the
+// from a suffix product over segments of kFusedMaxSeg workgroups (one per
+// thread: lane shuffles within each wave, then the later waves' totals), the
 // last segment first. The output is the sum times its reciprocal, as the
 // Fused form normalises (decode.rs:653-659).
 // ---------------------------------------------------------------------------
@@ -1430,6 +1431,8 @@ __global__ __launch_bounds__(512) void decode_combine(DecodeArgs a)
     __shared__ float ored[kCombineSubs][64];
     __shared__ float lred[kCombineSubs];
     __shared__ float xs[FUSED ? kFusedMaxSeg : 1];
+    __shared__ float wt[FUSED ? kCombineSubs : 1];              // the waves' suffix totals
+    static_assert(!FUSED || kFusedMaxSeg == 64 * kCombineSubs, "one scan element per thread");
     const int h = blockIdx.x, kvh = h / a.g, jh = h % a.g;
     const int t = threadIdx.x & 63, sub = threadIdx.x >> 6;
     // D not a multiple of 64: lanes past D in the last block read dimension 0
@@ -1460,16 +1463,24 @@ __global__ __launch_bounds__(512) void decode_combine(DecodeArgs a)
             };
             int w0 = s0 + sub;
             load_batch(w0);
-            __syncthreads();                // the previous segment's xs is read
-            if (tid < cnt) xs[tid] = xv;
-            __syncthreads();
-            // xs[i] <- the product of xs[i .. cnt-1]
-            for (int off = 1; off < cnt; off *= 2) {
-                const float y = tid + off < cnt ? xs[tid + off] : 1.0f;
-                __syncthreads();
-                if (tid < cnt) xs[tid] = xs[tid] * y;
-                __syncthreads();
+            // xs[i] <- the product of the segment's products i .. cnt-1 (the
+            // threads past cnt hold 1): a suffix product within each wave by
+            // lane shuffles, then times the later waves' totals; a doubling
+            // scan in LDS took two barriers per step
+            const int lane = tid & 63;
+            float p = xv;
+#pragma unroll
+            for (int off = 1; off < 64; off *= 2) {
+                const float y = __shfl_down(p, off);
+                p = lane + off < 64 ? p * y : p;
             }
+            __syncthreads();                // the previous segment's xs and wt are read
+            if (lane == 0) wt[sub] = p;
+            __syncthreads();
+            float later = 1.0f;
+            for (int u = kCombineSubs - 1; u > sub; u--) later = later * wt[u];
+            xs[tid] = p * later;
+            __syncthreads();
             for (; w0 < s1; w0 += kCombineSubs * BATCH) {
                 if (w0 != s0 + sub) load_batch(w0);
 #pragma unroll
