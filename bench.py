@@ -52,16 +52,16 @@ MFMA_BF16_PEAK_TFS = 2500.0  # MI355X dense bf16 MFMA, TFLOP/s
 # Summary and commands: profiles/pmc_traffic_bench_configs.md
 TRAFFIC_BYTES = {
     "chained": {
-        "decode_1k": (2 * (564.4 + 2243.1) + (34.0 + 4.0)) * 1024,
-        "decode_32k": (2 * (16464.7 + 17504.8 + 1090.5) + (2112.0 + 2056.0 + 8.0)) * 1024,
-        "prefill_512": (2 * 8605.7 + 4096.0) * 1024,
-        "prefill_4096_after_8192": (2 * (72934.9 + 149439.2 + 31019.6) + (376.0 + 87294.3 + 15360.0)) * 1024,
-        "decode_128k_outliers": (2 * (65628.1 + 69784.6 + 1090.5) + (8320.2 + 2056.0 + 8.0)) * 1024,
+        "decode_1k": (2 * (564.3 + 2250.6) + (34.0 + 4.0)) * 1024,
+        "decode_32k": (2 * (16467.6 + 17514.9 + 1084.0) + (2112.0 + 2056.0 + 8.0)) * 1024,
+        "prefill_512": (2 * 8605.5 + 4096.0) * 1024,
+        "prefill_4096_after_8192": (2 * (72935.0 + 148541.5 + 31022.3) + (376.0 + 87282.1 + 15360.0)) * 1024,
+        "decode_128k_outliers": (2 * (65628.0 + 69774.4 + 1084.0) + (8320.1 + 2056.0 + 8.0)) * 1024,
     },
     "fused": {
-        "decode_1k": (2 * (569.7 + 2277.6) + (36.0 + 4.0)) * 1024,
-        "decode_32k": (2 * (16472.7 + 17543.2 + 1126.0) + (2240.0 + 2064.0 + 8.0)) * 1024,
-        "decode_128k_outliers": (2 * (65638.5 + 69812.1 + 1126.0) + (8832.2 + 6672.0 + 8.0)) * 1024,
+        "decode_1k": (2 * (569.8 + 2275.0) + (36.0 + 4.0)) * 1024,
+        "decode_32k": (2 * (16467.8 + 17542.4 + 1144.0) + (2112.0 + 2064.0 + 8.0)) * 1024,
+        "decode_128k_outliers": (2 * (65625.7 + 69810.7 + 1144.0) + (8320.1 + 2064.0 + 8.0)) * 1024,
     },
 }
 
