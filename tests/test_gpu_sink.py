@@ -193,3 +193,93 @@ def test_sink_static_entry_matches(torch_cuda):
         outs.append(out.cpu().numpy().view(np.uint16))
     assert (outs[0] == outs[1]).all()
     assert_parity(outs[0], oracle.attention(w, sink=7.5), w, "sink static")
+
+
+# A seeded sweep with the sink on: group shapes, head dimensions (tuned and
+# not), rows and cached positions drawn at random (fixed seed), a Chained or a
+# Fused plan (the latter runs the Chained form with the sink), and sink values
+# from far below the scores to dominant.
+SWEEP_GROUPS = [(8, 2), (16, 2), (16, 4), (12, 1), (6, 3), (34, 2), (24, 2), (4, 4), (10, 2), (64, 4)]
+SWEEP_DIMS = [64, 128, 256, 256, 128, 32, 96, 160, 384]
+SWEEP_ROWS = [1, 1, 1, 2, 3, 5, 8, 9, 16, 33, 64, 100, 257]
+SWEEP_SINKS = [-40.0, -2.0, 0.0, 1.5, 3.0, 5.0, 8.0, 12.0]
+SWEEP_SEED = 20261203
+SWEEP_COUNT = 32
+SWEEP_MAX_WORK = 1.5e8          # rows x keys x heads x head_dim: the oracle's sink form is scalar
+
+
+def _sweep_draw():
+    rng = np.random.default_rng(SWEEP_SEED)
+    out = []
+    while len(out) < SWEEP_COUNT:
+        h, kvh = SWEEP_GROUPS[rng.integers(len(SWEEP_GROUPS))]
+        d = int(SWEEP_DIMS[rng.integers(len(SWEEP_DIMS))])
+        rows = int(SWEEP_ROWS[rng.integers(len(SWEEP_ROWS))])
+        past = int([0, rng.integers(1, 64), rng.integers(64, 1100), rng.integers(1100, 12000)][rng.integers(4)])
+        form = "fused" if rng.random() < 0.3 else "chained"
+        sink = float(SWEEP_SINKS[rng.integers(len(SWEEP_SINKS))])
+        if rows * (past + rows) * h * d > SWEEP_MAX_WORK:
+            continue
+        out.append((f"k{len(out):02d}_h{h}k{kvh}_d{d}_r{rows}_p{past}_{form}_s{sink:g}", h, kvh, d, rows, past, form,
+                    sink))
+    return out
+
+
+SWEEP = _sweep_draw()
+
+# the kernel families the draw reaches (main kernels, tail kernels, split over keys)
+SWEEP_REACHED = {
+    ("causal", "none", False),
+    ("causal_split", "none", True),
+    ("decode", "none", False),
+    ("few_rows", "none", False),
+}
+
+
+def _sweep_plan(h, kvh, d, rows, past, form):
+    return hsdpa.Plan(h, h // kvh, d, past + rows, form=form, sink=True)
+
+
+def test_sink_sweep_reaches_the_kernel_families():
+    """The draw reaches the decode, few-rows and causal kernels, split and
+    not, every part on the Chained form (checked on the host, before the
+    parity sweep)."""
+    seen = set()
+    for _, h, kvh, d, rows, past, form, _s in SWEEP:
+        r = _sweep_plan(h, kvh, d, rows, past, form).route(rows, past)
+        assert r["main_form"] == "chained" and r["tail_form"] == "chained", r
+        seen.add((r["main"], r["tail"], r["splits"] > 1))
+    assert SWEEP_REACHED <= seen, sorted(SWEEP_REACHED - seen)
+
+
+def test_sink_sweep_parity(torch_cuda):
+    """Each call against the oracle's sink form: no NaN, the per-row bound,
+    a call of at least 4096 outputs at least 99.9 % of them within one ulp, a
+    smaller one at most max(2, 1 %) past one ulp; pooled, at least 99.9 %."""
+    from parity import ABS_FACTOR, ULP_SHARE
+
+    within = total = 0
+    for i, (name, h, kvh, d, rows, past, form, sink) in enumerate(SWEEP):
+        w = W.make(name, heads=h, kv_heads=kvh, head_dim=d, rows=rows, past=past, seed=400 + i)
+        plan = _sweep_plan(h, kvh, d, rows, past, form)
+        print(f"case {name}", flush=True)
+        q = torch.from_numpy(np.ascontiguousarray(w.q).view(np.int16)).cuda()
+        k = torch.from_numpy(np.ascontiguousarray(w.k).view(np.int16)).cuda()
+        v = torch.from_numpy(np.ascontiguousarray(w.v).view(np.int16)).cuda()
+        out = torch.full((w.rows, w.heads, w.head_dim), -1, dtype=torch.int16, device="cuda")
+        ws = torch.empty(plan.workspace_bytes, dtype=torch.uint8, device="cuda")
+        hsdpa.attention_torch(plan, q, k, v, out, w.rows, w.past, w.scale, ws, sink=sink)
+        torch.cuda.synchronize()
+        got = out.cpu().numpy().view(np.uint16)
+        r = compare(got, oracle.attention(w, sink=sink), w)
+        assert not r["nan"], (name, r)
+        assert r["max_abs_over_vmax"] <= ABS_FACTOR, (name, r)
+        n = got.size
+        off = int(round((1.0 - r["ulp1_share"]) * n))
+        if n >= 4096:
+            assert r["ulp1_share"] >= ULP_SHARE, (name, r)
+        else:
+            assert off <= max(2, n // 100), (name, r)
+        within += n - off
+        total += n
+    assert within / total >= ULP_SHARE, (within, total)
