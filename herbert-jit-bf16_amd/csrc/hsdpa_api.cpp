@@ -25,7 +25,7 @@ struct hsdpa_plan {
     uint64_t dec_nwg_qk;      // pass-1 workgroups per group, at most
     uint64_t dec_cols;        // columns per KV head: query heads, or (row, head) pairs (0: no decode)
     uint64_t dec_part;        // (pass-2 workgroup, column) partials per KV head, at most
-    uint64_t off_scores, off_wgmax, off_part_o, off_part_l, off_bmax, off_part_x, dec_bytes;
+    uint64_t off_scores, off_wgmax, off_part_o, off_part_l, off_bmax, off_part_x, off_fcfg, dec_bytes;
     // split causal workspace (floats), after the decode's: partial row maxima,
     // outputs and sums of split_units (split, 32-row group, head) cells
     uint64_t split_units;
@@ -517,6 +517,9 @@ hsdpa_status hsdpa_plan_create(const hsdpa_spec *spec, hsdpa_plan **out)
         p->off_part_x = off;
         off = align_up(off + kvh * part * 4, kAlign);
     }
+    // a frame call's step configuration (decode-only plans)
+    p->off_fcfg = off;
+    if (p->max_rows == 1) off += kAlign;
     p->dec_bytes = off;
     // the split causal kernel: (split, 32-row group, head) cells, enough for
     // one round of the compute units (8 row blocks of 32 per workgroup), when
@@ -813,6 +816,7 @@ hsdpa_status hsdpa_attention_frame(const hsdpa_plan *plan, const hsdpa_frame_cal
     a.f_rows = call->rows;
     a.f_past = call->past;
     a.f_status = call->status;
+    a.f_cfg = reinterpret_cast<uint32_t *>(ws + plan->off_fcfg);
     a.f_cap = s.kv_capacity;
     a.f_groups = static_cast<int>(plan->kv_heads) * sub;
     a.f_cus = plan->cus;

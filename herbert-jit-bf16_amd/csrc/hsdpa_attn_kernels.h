@@ -437,10 +437,13 @@ template <int MR> struct DecodeIds {
 // run of whole tiles per workgroup (at least 128 keys) that shares the
 // compute units among the groups, or (f_loop 0: every past below the
 // capacity fits one round of them, or the run cannot loop) 256 keys per
-// workgroup. Every kernel of the call computes the same values. Returns the call's
-// status: HSDPA_OK with the arguments set (rows 1), or a status with nothing
-// to compute (rows 0: HSDPA_OK with n = 0; more rows than one, or past at the
-// capacity: a refusal).
+// workgroup. Pass 1 derives them (each workgroup alike) and its first
+// workgroup leaves them in the workspace (f_cfg) for pass 2 and the combine
+// (frame_cfg_load): deriving them again took the step 0.9 us at 32K, the
+// divisions of the tile rule on each kernel's critical path. Returns the
+// call's status: HSDPA_OK with the arguments set (rows 1), or a status with
+// nothing to compute (rows 0: HSDPA_OK with n = 0; more rows than one, or
+// past at the capacity: a refusal).
 __device__ __forceinline__ uint32_t frame_args(DecodeArgs &a, bool &run)
 {
     const uint64_t rows = *a.f_rows, past = *a.f_past;
@@ -490,6 +493,30 @@ __device__ __forceinline__ uint32_t frame_args(DecodeArgs &a, bool &run)
     return HSDPA_OK;
 }
 
+// The step's configuration in the workspace: status, run, past (low, high),
+// keys_qk, nwg_qk, keys_pv, nwg_pv (32 bytes, 16-byte aligned).
+__device__ __forceinline__ void frame_cfg_store(const DecodeArgs &a, uint32_t status, bool run)
+{
+    uint4 *c = reinterpret_cast<uint4 *>(a.f_cfg);
+    c[0] = make_uint4(status, run ? 1u : 0u, static_cast<uint32_t>(a.past), static_cast<uint32_t>(a.past >> 32));
+    c[1] = make_uint4(static_cast<uint32_t>(a.keys_qk), static_cast<uint32_t>(a.nwg_qk),
+                      static_cast<uint32_t>(a.keys_pv), static_cast<uint32_t>(a.nwg_pv));
+}
+
+__device__ __forceinline__ uint32_t frame_cfg_load(DecodeArgs &a, bool &run)
+{
+    const uint4 *c = reinterpret_cast<const uint4 *>(a.f_cfg);
+    const uint4 c0 = c[0], c1 = c[1];
+    run = c0.y != 0;
+    a.past = static_cast<uint64_t>(c0.z) | (static_cast<uint64_t>(c0.w) << 32);
+    a.n = run ? a.past + 1 : 0;
+    a.keys_qk = static_cast<int>(c1.x);
+    a.nwg_qk = static_cast<int>(c1.y);
+    a.keys_pv = static_cast<int>(c1.z);
+    a.nwg_pv = static_cast<int>(c1.w);
+    return c0.x;
+}
+
 // FUSED: also store the maximum of every 16-key block of each column (bmax):
 // the Fused form evaluates a block's exponentials at the running maximum of
 // the blocks up to it. TWO (with LOOP): exactly two tiles per wave. FRAME:
@@ -501,7 +528,8 @@ __global__ __launch_bounds__(256) void decode_qk(DecodeArgs a)
     static_assert(!FRAME || (LOOP && MR == 0 && !TWO && !MG), "frame calls: one group per workgroup, looped tiles");
     if constexpr (FRAME) {
         bool run;
-        frame_args(a, run);
+        const uint32_t st = frame_args(a, run);
+        if (blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0 && threadIdx.x == 0) frame_cfg_store(a, st, run);
         if (!run || static_cast<int>(blockIdx.x) >= a.nwg_qk) return;
     }
     constexpr int KS = D / 32;
@@ -745,7 +773,7 @@ __global__ __launch_bounds__(64 * W, D > 256 ? 1 : 8 / W) void decode_pv(DecodeA
     static_assert(!FRAME || MR == 0, "frame calls: one group per workgroup");
     if constexpr (FRAME) {
         bool run;
-        frame_args(a, run);
+        frame_cfg_load(a, run);
         if (!run || static_cast<int>(blockIdx.x) >= a.nwg_pv) return;
     }
     constexpr int THREADS = 64 * W;
@@ -1424,7 +1452,7 @@ __global__ __launch_bounds__(512) void decode_combine(DecodeArgs a)
     static_assert(!FRAME || !MR, "frame calls: one row");
     if constexpr (FRAME) {
         bool run;
-        const uint32_t st = frame_args(a, run);
+        const uint32_t st = frame_cfg_load(a, run);
         if (a.f_status && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) *a.f_status = st;
         if (!run) return;
     }

@@ -75,6 +75,7 @@ struct DecodeArgs {
     // unused otherwise.
     const uint64_t *f_rows, *f_past;
     uint32_t *f_status;     // null, or receives the call's hsdpa_status (the combine writes it)
+    uint32_t *f_cfg;        // workspace: the step's configuration, stored by pass 1 for pass 2 and the combine
     uint64_t f_cap;         // the plan's KV capacity
     int f_groups;           // kv_heads * sub
     int f_cus;              // compute units the grids were sized for
