@@ -377,7 +377,8 @@ DecodeCfg decode_cfg(const hsdpa_plan *p, uint64_t rows, uint64_t n, int sub, bo
         const uint64_t per = cu1 / groups > 0 ? cu1 / groups : 1;
         const uint64_t tiles = (n + hsdpa::kKeyTile - 1) / hsdpa::kKeyTile;
         const uint64_t run = hsdpa::kKeyTile * ((tiles + per - 1) / per);
-        c.keys_pv = groups * nch <= cu1 || !hsdpa::decode_pv_loop_ok(d, c.g, static_cast<int>(rows)) ||
+        c.keys_pv = groups * nch <= cu1 || !hsdpa::decode_pv_loop_ok(d, c.g, static_cast<int>(rows), fused) ||
+                            !hsdpa::decode_pv_loop_rows_ok(d, static_cast<int>(rows), sub, p->kv_heads * nch, cu1) ||
                             run > (1u << 30)
                         ? hsdpa::kDecodeKeysPV
                         : static_cast<int>(run);
@@ -416,8 +417,18 @@ uint64_t decode_nwg_pv_max(const hsdpa_plan *p, uint64_t rows, int sub)
     // the chunked pass 2 gives way to 256-key workgroups where it cannot run
     // (decode_pv_loop_ok) or a run would exceed 2^30 keys
     const uint64_t run_max = 32 * (((cap + 31) / 32 + per - 1) / per);
-    if (!hsdpa::decode_pv_loop_ok(d, g, static_cast<int>(rows)) || run_max > (uint64_t{1} << 30))
+    // (a Fused plan's tail rows take the Fused rule, its full chunks the Chained one)
+    const bool loop = hsdpa::decode_pv_loop_ok(d, g, static_cast<int>(rows), false) &&
+                      (p->form != HSDPA_FORM_FUSED || hsdpa::decode_pv_loop_ok(d, g, static_cast<int>(rows), true));
+    if (!loop || run_max > (uint64_t{1} << 30))
         return std::max(one_round, by256);
+    // several rows at D = 256: 256-key workgroups where decode_pv_loop_rows_ok
+    // declines the runs (for any past with more than 4 groups; up to
+    // CUs / kv_heads of them where they fit one round)
+    if (d == 256 && rows > 1 && sub > 1) {
+        if (sub > 4) return std::max(one_round, by256);
+        return std::max(one_round, std::min(by256, static_cast<uint64_t>(p->cus) / p->kv_heads));
+    }
     return one_round;
 }
 
@@ -564,6 +575,11 @@ static hsdpa_status run_part(const hsdpa_plan *plan, const hsdpa_call *call, con
     const int sub = part.fused && rows == 1 ? fused_row_sub(plan, n) : decode_sub(plan, rows, n);
     if (sub > 0) {
         const DecodeCfg c = decode_cfg(plan, rows, n, sub, part.fused);
+        // the workspace holds dec_part (pass-2 workgroup, column) partials per
+        // KV head: a grid beyond it is refused, never written past
+        if (static_cast<uint64_t>(c.nwg_pv) * static_cast<uint64_t>(c.sub) * static_cast<uint64_t>(c.g) >
+            plan->dec_part)
+            return HSDPA_ERR_WORKSPACE;
         if (kernels) *kernels = rows == 1 ? HSDPA_KERNELS_DECODE : HSDPA_KERNELS_FEW_ROWS;
         if (splits) *splits = 1;
         if (launches) *launches += c.direct ? 2 : 3;
@@ -823,7 +839,7 @@ hsdpa_status hsdpa_attention_frame(const hsdpa_plan *plan, const hsdpa_frame_cal
     // pass 2 walks runs of keys where it can and where 256-key workgroups
     // would not fit the compute units in one round at the capacity
     const uint64_t nch_cap = (s.kv_capacity + hsdpa::kDecodeKeysPV - 1) / hsdpa::kDecodeKeysPV;
-    a.f_loop = hsdpa::decode_pv_loop_ok(d, a.g, 1) &&
+    a.f_loop = hsdpa::decode_pv_loop_ok(d, a.g, 1, plan->form == HSDPA_FORM_FUSED) &&
                        static_cast<uint64_t>(a.f_groups) * nch_cap > static_cast<uint64_t>(plan->cus)
                    ? 1
                    : 0;

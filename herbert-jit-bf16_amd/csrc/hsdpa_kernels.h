@@ -254,12 +254,24 @@ inline bool decode_direct_ok(int d, int rows, int sub, int g, uint64_t n, bool f
 }
 
 // Pass 2 in chunks (one round of workgroups over a long cache) is built for
-// the tuned head dimensions, at D = 256 for one row in groups of up to 8
-// columns (with 16 the P columns' operands no longer fit beside the next
-// chunk's V tile; with several rows the column limits no longer fit either).
-inline bool decode_pv_loop_ok(int d, int g, int rows)
+// the tuned head dimensions; under the Fused form at D = 256 for one row in
+// groups of up to 8 columns (with 16 its running maxima and corrections and
+// the P columns' operands no longer fit beside the next chunk's V tile).
+inline bool decode_pv_loop_ok(int d, int g, int rows, bool fused)
 {
-    return d == 64 || d == 128 || (d == 256 && g <= 8 && rows == 1);
+    return d == 64 || d == 128 || (d == 256 && (!fused || (g <= 8 && rows == 1)));
+}
+// Several rows at D = 256 in 2 or more groups: pass 2 over all the groups of
+// a KV head per workgroup loads each V tile once for all of them; chunked
+// runs per group stream V once per group, but in one round of workgroups.
+// The runs go with at most 4 groups where the all-group form would take more
+// than one round of 256-key workgroups (kv_chunks = kv_heads x ceil(n/256)):
+// 16/2 heads at D = 256, 4 rows after 64K and 128K 58.7 -> 55.3 and 105.6 ->
+// 90.9 us, 8 rows after 128K 147.9 -> 139.8; but 8 rows after 32K (one round)
+// 46.2 -> 49.0 and 16 rows (8 groups) after 64K 126.6 -> 131.4.
+inline bool decode_pv_loop_rows_ok(int d, int rows, int sub, uint64_t kv_chunks, uint64_t cus)
+{
+    return d != 256 || rows == 1 || sub == 1 || (sub <= 4 && kv_chunks > cus);
 }
 hipError_t launch_layer_prep(const LayerPrepArgs &a, hipStream_t s);
 hipError_t launch_norm_rope(const NormRopeArgs &a, hipStream_t s);

@@ -326,14 +326,12 @@ static hipError_t decode_dm(const DecodeArgs &a, int kv_heads, hipStream_t s)
     } else if (a.g <= 8) {
         if (a.keys_pv == 4 * kKeyTile) e = launch(decode_pv<D, 4, 1, false, MR>, gpv, dim3(256), s, a);
         else if (a.keys_pv <= kDecodeKeysPV) e = launch(decode_pv<D, 8, 1, false, MR>, gpv, dim3(512), s, a);
-        else if constexpr (!MR || D < 256) e = launch(decode_pv<D, 8, 1, true, MR>, gpv, dim3(512), s, a);
-        else return hipErrorInvalidValue;                   // decode_pv_loop_ok
+        else e = launch(decode_pv<D, 8, 1, true, MR>, gpv, dim3(512), s, a);
     } else {
         if (a.keys_pv == 4 * kKeyTile) {
             e = launch(decode_pv<D, 4, 2, false, MR>, gpv, dim3(256), s, a);
         } else if (a.keys_pv > kDecodeKeysPV) {
-            if constexpr (D < 256) e = launch(decode_pv<D, 8, 2, true, MR>, gpv, dim3(512), s, a);
-            else return hipErrorInvalidValue;               // decode_pv_loop_ok
+            e = launch(decode_pv<D, 8, 2, true, MR>, gpv, dim3(512), s, a);
         } else {
             e = launch(decode_pv<D, 8, 2, false, MR>, gpv, dim3(512), s, a);
         }

@@ -330,3 +330,25 @@ def test_record_layouts_match_the_header(tmp_path):
         assert got[(rec, "size")] == ctypes.sizeof(cls), rec
         for fname, _ in cls._fields_:
             assert got[(rec, fname)] == getattr(cls, fname).offset, (rec, fname)
+
+
+def test_decode_grids_fit_the_workspace():
+    """Every decode call a plan can take fits the partials its workspace was
+    sized for (the call refuses a grid beyond them with HSDPA_ERR_WORKSPACE,
+    which the route query reports): group shapes, the tuned and other head
+    dimensions, both forms, max_rows 1, 8 and any, rows 1 to 16 at cache
+    lengths across the configurations' thresholds."""
+    shapes = [(16, 8, 256), (48, 24, 256), (64, 8, 128), (32, 4, 128), (16, 16, 64), (8, 4, 256), (20, 10, 96),
+              (17, 17, 128), (128, 64, 256)]
+    pasts = [0, 100, 1023, 3000, 8191, 16383, 32767, 65535, 131000]
+    for h, g, d in shapes:
+        for form in ("chained", "fused"):
+            for max_rows in (1, 8, 0):
+                plan = hsdpa.Plan(h, g, d, 131072, form=form, max_rows=max_rows)
+                for rows in (1, 2, 3, 4, 5, 8, 9, 16):
+                    if max_rows and rows > max_rows:
+                        continue
+                    for past in pasts:
+                        if past + rows > 131072:
+                            continue
+                        plan.route(rows, past)           # raises HsdpaError on a refusal
