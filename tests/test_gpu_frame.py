@@ -24,6 +24,8 @@ CASES = [
     ("frame_d256_g8", 16, 2, 256, 40000, "chained", [1023, 1024, 1025, 5000, 32767]),
     ("frame_d256_g8_fused", 16, 2, 256, 40000, "fused", [0, 300, 20000]),
     ("frame_d256_g16_two_blocks", 32, 2, 256, 9000, "chained", [100, 8999]),
+    # 16 columns at D = 256 over a long capacity: pass 2 in chunked runs
+    ("frame_d256_g16_runs", 32, 2, 256, 40000, "chained", [4000, 39999]),
     ("frame_d128_g8", 32, 4, 128, 70000, "chained", [2047, 2048, 65000]),
     ("frame_d64_g24_two_groups", 48, 2, 64, 6000, "fused", [5, 5999]),
 ]
