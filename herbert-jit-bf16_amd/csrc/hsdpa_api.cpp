@@ -348,7 +348,10 @@ DecodeCfg decode_cfg(const hsdpa_plan *p, uint64_t rows, uint64_t n, int sub, bo
     // looped kernel runs one workgroup per CU at a time; the smaller count on
     // a tie): a partial last round costs a whole one (40K keys: 3 tiles in
     // one round, 27.8 us, against 2 tiles in two rounds, 29.2 us).
-    const uint64_t rounds = (groups_qk * nqk1 + 2 * cu1 - 1) / (2 * cu1);
+    // (all groups per workgroup: their Q columns fill the LDS beside the K tiles,
+    // one workgroup per compute unit)
+    const uint64_t per_cu = c.qk_all ? 1 : 2;
+    const uint64_t rounds = (groups_qk * nqk1 + per_cu * cu1 - 1) / (per_cu * cu1);
     uint64_t rq = !hsdpa::decode_loop_ok(d) ? 1 : groups_qk * nqk1 > cu1 && rounds < 2 ? 2 : rounds;
     if (rq > 1) {
         uint64_t best = rq, cost = ~0ull;
