@@ -410,6 +410,24 @@ __device__ __forceinline__ u32x4 vt_operand_padded(const uint16_t *vtile, int kb
 // close in time: the later ones find the range's tiles in its L2 (3 to 8 rows
 // after 32K 11-14 % faster, 4 rows after 128K 16 %). x runs over the key
 // ranges padded to a multiple of 8; the padding exits at once.
+// The row of column c = r G + rem (c = 0, 1, ..) of a KV head's (row, head)
+// columns, for c, c + 2, c + 4, ..: one division, then a step of two columns
+// by at most two subtractions (G >= 1), with no branch.
+struct ColumnRows {
+    int row, rem, G;
+    __device__ __forceinline__ ColumnRows(int c, int g) : row(c / g), rem(c - (c / g) * g), G(g) {}
+    __device__ __forceinline__ void next2()
+    {
+        rem += 2;
+        const bool w1 = rem >= G;
+        rem = w1 ? rem - G : rem;
+        row += w1 ? 1 : 0;
+        const bool w2 = rem >= G;
+        rem = w2 ? rem - G : rem;
+        row += w2 ? 1 : 0;
+    }
+};
+
 template <int MR> struct DecodeIds {
     int wg, z;
     __device__ __forceinline__ explicit DecodeIds(const DecodeArgs &a)
@@ -947,27 +965,46 @@ __global__ __launch_bounds__(64 * W, D > 256 ? 1 : 8 / W) void decode_pv(DecodeA
         }
         // 3. dense exponentials: thread t owns key c0 + t % KEYS for heads
         //    t / KEYS, t / KEYS + 2, ...; a wave covers 64 consecutive keys of
-        //    one head set
+        //    one head set. Every column slot at once, with no branch between
+        //    them, so that the slots' exponentials and sums overlap (taken one
+        //    after another, each waited out its own chain); slots past g get
+        //    zeros, read only by columns that are never stored.
+        constexpr int HC = nh / 2;                              // slots per thread
+        const int hq = __builtin_amdgcn_readfirstlane(tid / KEYS);  // the same in a whole wave
+        float ev[HC];
+        ColumnRows rows(id.z * a.g + hq, MR ? a.G : 1);         // MR: column h's row, by steps of two
 #pragma unroll
-        for (int i = 0; i < kDecodeMaxGroup / 2; i++) {
-            const int h = tid / KEYS + 2 * i;
-            if (h >= a.g) break;
-            const bool vis = visible(h);
-            float e;
+        for (int i = 0; i < HC; i++) {
+            const int h = hq + 2 * i;
+            if (MR && i > 0) rows.next2();
+            // column h's row sees keys [0, past + row]
+            const bool vis = (h < a.g) & kv_e & (!MR || c0 + key_e <= a.past + static_cast<uint64_t>(rows.row));
+            // computed in every lane, then selected
+            float x;
             if constexpr (FUSED) {
                 const int fb = h * NB + key_e / 16;
-                e = vis ? exp_poly(sv[i] - fmb[fb]) * fcf[fb] : 0.0f;
+                x = exp_poly(sv[i] - fmb[fb]) * fcf[fb];
             } else {
-                e = vis ? exp_poly(sv[i] - smax[h]) : 0.0f;
+                x = exp_poly(sv[i] - smax[h]);
             }
-            const uint32_t hb = bf16_rne(e);
+            ev[i] = vis ? x : 0.0f;
+        }
+#pragma unroll
+        for (int i = 0; i < HC; i++) {
+            const int h = hq + 2 * i;
+            const uint32_t hb = bf16_rne(ev[i]);
             pc[h * PS + key_e] = static_cast<uint16_t>(hb);
-            pc[(nh + h) * PS + key_e] = static_cast<uint16_t>(bf16_rne(e - __uint_as_float(hb << 16)));
-            const float sum = wave_sum_hi(e);
-            if constexpr (FUSED) {
-                if (l == 63) lpart[wave][h] = (LOOP && c0 != j0 ? lpart[wave][h] * fx[h] : 0.0f) + sum;
-            } else {
-                if (l == 63) lpart[wave][h] = (LOOP && c0 != j0 ? lpart[wave][h] : 0.0f) + sum;
+            pc[(nh + h) * PS + key_e] = static_cast<uint16_t>(bf16_rne(ev[i] - __uint_as_float(hb << 16)));
+        }
+        float esum[HC];
+#pragma unroll
+        for (int i = 0; i < HC; i++) esum[i] = wave_sum_hi(ev[i]);
+        if (l == 63) {
+#pragma unroll
+            for (int i = 0; i < HC; i++) {
+                const int h = hq + 2 * i;
+                if constexpr (FUSED) lpart[wave][h] = (LOOP && c0 != j0 ? lpart[wave][h] * fx[h] : 0.0f) + esum[i];
+                else lpart[wave][h] = (LOOP && c0 != j0 ? lpart[wave][h] : 0.0f) + esum[i];
             }
         }
         // 4. V tile to LDS; with LOOP the next chunk's scores and V tiles are
@@ -1089,8 +1126,8 @@ __global__ __launch_bounds__(64 * W, D > 256 ? 1 : 8 / W) void decode_pv(DecodeA
 // 8-wave form with two P column blocks). The V tiles are loaded and staged in
 // LDS once, and each wave reads its V^T operands into registers once; then,
 // for each group in turn, the exact maximum of its columns, the exponentials
-// (hi + lo P columns in LDS) and P.V, the next group's scores and maxima
-// requested before this group's products. The partials go where decode_pv
+// (hi + lo P columns in LDS) and P.V, the scores and maxima of the group
+// after next requested before this group's products (two groups in flight). The partials go where decode_pv
 // puts them, so the combine is the same. Every column carries its row's
 // causal limit (a few rows; one row sees all keys). Grid (nwg_pv, kv_heads).
 // ---------------------------------------------------------------------------
@@ -1115,10 +1152,12 @@ __global__ __launch_bounds__(512, 1) void decode_pv_all(DecodeArgs a)
     const uint64_t gk = j0 + key_e;
     const bool kv_e = gk < j1;
     const int jh = tid / T, u = tid % T;
-    float sv[kDecodeMaxGroup / 2], mx[BATCH];
+    // two groups' loads in flight: group z's scores and maxima arrive while
+    // group z - 1 is computed (buffer z % 2)
+    float sva[kDecodeMaxGroup / 2], mxa[BATCH], svb[kDecodeMaxGroup / 2], mxb[BATCH];
     // group z's scores of this thread's key (columns tid / KEYS + 2 i) and the
     // first batch of its columns' pass-1 maxima
-    auto load_group = [&](int z) {
+    auto load_group = [&](int z, float(&sv)[kDecodeMaxGroup / 2], float(&mx)[BATCH]) {
         const int kvh = kvh0 + z;
 #pragma unroll
         for (int i = 0; i < kDecodeMaxGroup / 2; i++) {
@@ -1133,14 +1172,18 @@ __global__ __launch_bounds__(512, 1) void decode_pv_all(DecodeArgs a)
             mx[b] = msrc[w < a.nwg_qk ? w : 0];
         }
     };
-    load_group(0);
+    load_group(0, sva, mxa);
+    if (ng > 1) load_group(1, svb, mxb);
     u32x4 vr[Tile<D, 64>::kPer];
     tile_gload<D, 64, true>(vbase, j0 + kKeyTile * wave, j1, l, vr);
     __builtin_amdgcn_sched_barrier(0);                          // all loads issued first
     u32x4 av[W][DBW];                                           // this wave's V^T operands, all tiles
-    // one group: FIRST also stages V and reads the V^T operands
-    auto group = [&](int z, auto first_t) {
-        constexpr bool FIRST = decltype(first_t)::value;
+    // one group: FIRST also stages V and reads the V^T operands; ODD takes
+    // buffer b
+    auto group = [&](int z, auto first_t, auto odd_t) {
+        constexpr bool FIRST = decltype(first_t)::value, ODD = decltype(odd_t)::value;
+        float(&sv)[kDecodeMaxGroup / 2] = ODD ? svb : sva;
+        float(&mx)[BATCH] = ODD ? mxb : mxa;
         const int kvh = kvh0 + z;
         float m = kNegInf;
 #pragma unroll
@@ -1164,21 +1207,36 @@ __global__ __launch_bounds__(512, 1) void decode_pv_all(DecodeArgs a)
         // column tid's maximum, for the sink's term (smax is rewritten by the
         // next group once every wave has passed this group's second barrier)
         const float mcol = tid < a.g ? smax[tid] : 0.0f;
+        // every column slot at once, with no branch between them (as in
+        // decode_pv); slots past g get zeros
+        const int hq = __builtin_amdgcn_readfirstlane(tid / KEYS);  // the same in a whole wave
+        float ev[nh / 2];
+        // column h's row sees keys [0, past + row], row = (z g + h) / G, by
+        // steps of two columns
+        ColumnRows rows(z * a.g + hq, a.G);
 #pragma unroll
-        for (int i = 0; i < kDecodeMaxGroup / 2; i++) {
-            const int h = tid / KEYS + 2 * i;
-            if (h >= a.g) break;
-            // column h's row sees keys [0, past + row]
-            const int row = (z * a.g + h) / a.G;
-            const bool vis = kv_e && gk <= a.past + static_cast<uint64_t>(row);
-            const float e = vis ? exp_poly(sv[i] - smax[h]) : 0.0f;
-            const uint32_t hb = bf16_rne(e);
-            pc[h * PS + key_e] = static_cast<uint16_t>(hb);
-            pc[(nh + h) * PS + key_e] = static_cast<uint16_t>(bf16_rne(e - __uint_as_float(hb << 16)));
-            const float sum = wave_sum_hi(e);
-            if (l == 63) lpart[wave][h] = sum;
+        for (int i = 0; i < nh / 2; i++) {
+            const int h = hq + 2 * i;
+            if (i > 0) rows.next2();
+            const bool vis = (h < a.g) & kv_e & (gk <= a.past + static_cast<uint64_t>(rows.row));
+            const float x = exp_poly(sv[i] - smax[h]);          // computed in every lane, then selected
+            ev[i] = vis ? x : 0.0f;
         }
-        if (z + 1 < ng) load_group(z + 1);
+#pragma unroll
+        for (int i = 0; i < nh / 2; i++) {
+            const int h = hq + 2 * i;
+            const uint32_t hb = bf16_rne(ev[i]);
+            pc[h * PS + key_e] = static_cast<uint16_t>(hb);
+            pc[(nh + h) * PS + key_e] = static_cast<uint16_t>(bf16_rne(ev[i] - __uint_as_float(hb << 16)));
+        }
+        float esum[nh / 2];
+#pragma unroll
+        for (int i = 0; i < nh / 2; i++) esum[i] = wave_sum_hi(ev[i]);
+        if (l == 63) {
+#pragma unroll
+            for (int i = 0; i < nh / 2; i++) lpart[wave][hq + 2 * i] = esum[i];
+        }
+        if (z + 2 < ng) load_group(z + 2, sv, mx);
         if constexpr (FIRST) tile_mask_lstore_v16<D, 64>(vt[wave], j0 + kKeyTile * wave, j1, l, vr);
         __syncthreads();
         if constexpr (FIRST) {
@@ -1219,8 +1277,11 @@ __global__ __launch_bounds__(512, 1) void decode_pv_all(DecodeArgs a)
             a.part_l[pbase + tid] = L;
         }
     };
-    group(0, std::true_type{});
-    for (int z = 1; z < ng; z++) group(z, std::false_type{});
+    group(0, std::true_type{}, std::false_type{});
+    for (int z = 1; z < ng; z += 2) {
+        group(z, std::false_type{}, std::true_type{});
+        if (z + 1 < ng) group(z + 1, std::false_type{}, std::false_type{});
+    }
 }
 
 // ---------------------------------------------------------------------------
