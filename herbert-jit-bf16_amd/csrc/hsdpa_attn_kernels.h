@@ -607,6 +607,16 @@ __global__ __launch_bounds__(256) void decode_qk(DecodeArgs a)
     }
     const uint16_t *kbase = a.k + static_cast<uint64_t>(blockIdx.y) * a.kv_stride;
     uint16_t *my = kt[wave];
+    // MG with MR: the row of column z g + i, stepped by g columns from column
+    // i's (g = gq G + gr), instead of a division per group and tile
+    int qrow0 = 0, qrem0 = 0, gq = 0, gr = 0;
+    if constexpr (MG && MR) {
+        const int c = colv ? i : 0;
+        qrow0 = c / a.G;
+        qrem0 = c - qrow0 * a.G;
+        gq = a.g / a.G;
+        gr = a.g - gq * a.G;
+    }
     float m[NG];
 #pragma unroll
     for (int z = 0; z < NG; z++) m[z] = kNegInf;
@@ -631,6 +641,7 @@ __global__ __launch_bounds__(256) void decode_qk(DecodeArgs a)
                 const int row = 16 * b + i;
                 ka[b][s] = load16(my + row * D + 8 * ((4 * s + G) ^ (row & KM)));
             }
+        int crow = qrow0, crem = qrem0;
 #pragma unroll
         for (int z = 0; z < NG; z++) {
             if (z >= ng) break;
@@ -638,8 +649,14 @@ __global__ __launch_bounds__(256) void decode_qk(DecodeArgs a)
             uint64_t lim = lim1;
             if constexpr (MG) {
                 if constexpr (MR) {
-                    const int cg = z * a.g + (colv ? i : 0), c = cg < a.cols ? cg : 0;
-                    lim = a.past + static_cast<uint64_t>(c / a.G) + 1;
+                    // a padded column (past rows * G) takes row 0's limit
+                    const int cg = z * a.g + (colv ? i : 0);
+                    lim = a.past + static_cast<uint64_t>(cg < a.cols ? crow : 0) + 1;
+                    crow += gq;
+                    crem += gr;
+                    const bool w = crem >= a.G;
+                    crem = w ? crem - a.G : crem;
+                    crow += w ? 1 : 0;
                 }
 #pragma unroll
                 for (int s = 0; s < KS; s++) qb[s] = qs[(z * KS + s) * 64 + l];
