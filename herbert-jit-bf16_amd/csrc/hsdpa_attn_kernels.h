@@ -849,15 +849,17 @@ __global__ __launch_bounds__(64 * W, D > 256 ? 1 : 8 / W) void decode_pv(DecodeA
     // The small loads go first: the vector-memory counter completes in order,
     // so anything issued after the V tile would wait for all of it.
     const int key_e = tid % KEYS;
+    const int hq = __builtin_amdgcn_readfirstlane(tid / KEYS);  // the same in a whole wave
     float sv[kDecodeMaxGroup / 2];
-    // this thread's scores of the chunk starting at key c0
+    // this thread's scores of the chunk starting at key c0, columns hq + 2 i
+    // (their addresses are the same in a whole wave)
     auto load_scores = [&](uint64_t c0) {
-        const uint64_t gk = c0 + key_e;
+        const uint64_t gk = c0 + key_e, key = gk < j1 ? gk : 0;
 #pragma unroll
-        for (int i = 0; i < kDecodeMaxGroup / 2; i++) {
-            const int h = tid / KEYS + 2 * i;
-            const int hc = h < a.g ? h : 0;
-            sv[i] = a.scores[static_cast<uint64_t>(kvh * a.g + hc) * a.npad + (gk < j1 ? gk : 0)];
+        for (int i = 0; i < nh / 2; i++) {
+            const int h = hq + 2 * i;
+            const float *col = a.scores + static_cast<uint64_t>(kvh * a.g + (h < a.g ? h : 0)) * a.npad;
+            sv[i] = col[key];
         }
     };
     load_scores(j0);
@@ -987,7 +989,6 @@ __global__ __launch_bounds__(64 * W, D > 256 ? 1 : 8 / W) void decode_pv(DecodeA
         //    after another, each waited out its own chain); slots past g get
         //    zeros, read only by columns that are never stored.
         constexpr int HC = nh / 2;                              // slots per thread
-        const int hq = __builtin_amdgcn_readfirstlane(tid / KEYS);  // the same in a whole wave
         float ev[HC];
         ColumnRows rows(id.z * a.g + hq, MR ? a.G : 1);         // MR: column h's row, by steps of two
 #pragma unroll
@@ -1172,15 +1173,18 @@ __global__ __launch_bounds__(512, 1) void decode_pv_all(DecodeArgs a)
     // two groups' loads in flight: group z's scores and maxima arrive while
     // group z - 1 is computed (buffer z % 2)
     float sva[kDecodeMaxGroup / 2], mxa[BATCH], svb[kDecodeMaxGroup / 2], mxb[BATCH];
-    // group z's scores of this thread's key (columns tid / KEYS + 2 i) and the
-    // first batch of its columns' pass-1 maxima
+    const int hq = __builtin_amdgcn_readfirstlane(tid / KEYS);  // the same in a whole wave
+    // group z's scores of this thread's key (columns hq + 2 i, whose addresses
+    // are the same in a whole wave) and the first batch of its columns'
+    // pass-1 maxima
     auto load_group = [&](int z, float(&sv)[kDecodeMaxGroup / 2], float(&mx)[BATCH]) {
         const int kvh = kvh0 + z;
+        const uint64_t key = kv_e ? gk : 0;
 #pragma unroll
-        for (int i = 0; i < kDecodeMaxGroup / 2; i++) {
-            const int h = tid / KEYS + 2 * i;
-            const int hc = h < a.g ? h : 0;
-            sv[i] = a.scores[static_cast<uint64_t>(kvh * a.g + hc) * a.npad + (kv_e ? gk : 0)];
+        for (int i = 0; i < nh / 2; i++) {
+            const int h = hq + 2 * i;
+            const float *col = a.scores + static_cast<uint64_t>(kvh * a.g + (h < a.g ? h : 0)) * a.npad;
+            sv[i] = col[key];
         }
         const float *msrc = a.wgmax + (static_cast<uint64_t>(kvh) * a.g + (jh < a.g ? jh : 0)) * a.nwg_qk;
 #pragma unroll
@@ -1226,7 +1230,6 @@ __global__ __launch_bounds__(512, 1) void decode_pv_all(DecodeArgs a)
         const float mcol = tid < a.g ? smax[tid] : 0.0f;
         // every column slot at once, with no branch between them (as in
         // decode_pv); slots past g get zeros
-        const int hq = __builtin_amdgcn_readfirstlane(tid / KEYS);  // the same in a whole wave
         float ev[nh / 2];
         // column h's row sees keys [0, past + row], row = (z g + h) / G, by
         // steps of two columns
