@@ -386,12 +386,26 @@ DecodeCfg decode_cfg(const hsdpa_plan *p, uint64_t rows, uint64_t n, int sub, bo
                         ? hsdpa::kDecodeKeysPV
                         : static_cast<int>(run);
     }
+    // a few rows at D = 256 in 2 to 4 groups where pass 1 takes all of a KV
+    // head's groups and 256-key workgroups would take more than one round:
+    // one round of workgroups that each walk a run for all the groups
+    // (decode_pv_all_loop_ok), the CUs shared among the KV heads only
+    bool all_loop = false;
+    if (!fused && hsdpa::decode_pv_all_loop_ok(d, static_cast<int>(rows), sub, c.qk_all != 0, p->kv_heads * nch, cu1)) {
+        const uint64_t per = cu1 / p->kv_heads > 0 ? cu1 / p->kv_heads : 1;
+        const uint64_t tiles = (n + hsdpa::kKeyTile - 1) / hsdpa::kKeyTile;
+        const uint64_t run = hsdpa::kKeyTile * ((tiles + per - 1) / per);
+        if (run > static_cast<uint64_t>(hsdpa::kDecodeKeysPV) && run <= (uint64_t{1} << 30)) {
+            c.keys_pv = static_cast<int>(run);
+            all_loop = true;
+        }
+    }
     c.nwg_qk = static_cast<int>((n + c.keys_qk - 1) / c.keys_qk);
     c.nwg_pv = static_cast<int>((n + c.keys_pv - 1) / c.keys_pv);
     // where pass 1 takes all of a KV head's groups and pass 2 runs 256-key
     // workgroups (D = 256; at D = 64 and 128 it takes chunks there), pass 2
     // takes them all too: each V tile loaded once instead of once per group
-    c.pv_all = c.qk_all && c.keys_pv == hsdpa::kDecodeKeysPV && d == 256 ? 1 : 0;
+    c.pv_all = (c.qk_all && c.keys_pv == hsdpa::kDecodeKeysPV && d == 256) || all_loop ? 1 : 0;
     // a short cache: pass 2 writes the outputs itself, no combine launch
     c.direct = hsdpa::decode_direct_ok(d, static_cast<int>(rows), sub, c.g, n, fused) ? 1 : 0;
     // several groups: a key range's groups on one XCD, whose L2 then serves

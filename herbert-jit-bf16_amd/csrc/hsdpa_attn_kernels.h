@@ -1305,6 +1305,211 @@ __global__ __launch_bounds__(512, 1) void decode_pv_all(DecodeArgs a)
 }
 
 // ---------------------------------------------------------------------------
+// Decode pass 2 over every group of a KV head in one workgroup that walks a
+// run of keys in 256-key chunks (up to kDecodeLoopMaxSub groups of at most 16
+// columns: a few rows over a long cache, one round of (nwg_pv, kv_heads)
+// workgroups). First the exact maxima of every group's columns (two groups'
+// pass-1 maxima in flight). Then per chunk: the V tiles staged in LDS once for
+// all the groups; for each group in turn the exponentials (hi + lo P columns
+// in LDS, the column sums added up per wave in LDS), the next group's scores
+// requested, and P.V into the group's accumulator (the hi and the lo block
+// into one), which stays in registers over the whole run, the V^T operands
+// read from LDS for each group in parts of two tiles; the next chunk's V
+// tiles are requested after the last group (held in registers during the
+// groups, they spilled). The partials and column sums go where decode_pv
+// puts them, so the combine is the same. Each column carries its row's
+// causal limit.
+// ---------------------------------------------------------------------------
+template <int D>
+__global__ __launch_bounds__(512, 1) void decode_pv_all_loop(DecodeArgs a)
+{
+    constexpr int W = 8, NCB = 2, THREADS = 64 * W, KEYS = W * kKeyTile, PS = KEYS + 8;
+    constexpr int DB = D / 16, DBW = DB / W, nh = 8 * NCB, HC = nh / 2, MS = kDecodeLoopMaxSub;
+    static_assert(DB % W == 0, "each wave takes whole dimension blocks");
+    static_assert(MS * W * kDecodeMaxGroup <= THREADS, "one thread per column sum to clear");
+    constexpr int T = THREADS / nh, BATCH = 8;                  // lanes per column's maxima
+    __shared__ __attribute__((aligned(16))) uint16_t vt[W][kKeyTile * D];
+    __shared__ __attribute__((aligned(16))) uint16_t pc[2 * kDecodeMaxGroup * PS];
+    __shared__ float smax[MS][kDecodeMaxGroup];
+    __shared__ float lsum[MS][W][kDecodeMaxGroup];
+    __shared__ int crow[MS][kDecodeMaxGroup];                   // the row of group z's column h
+    const int wg = static_cast<int>(blockIdx.x), tid = threadIdx.x;
+    const int kvh0 = static_cast<int>(blockIdx.y) * a.sub, ng = a.sub;     // 2 <= ng <= MS
+    const int wave = tid >> 6, l = tid & 63, j = l & 15, G = l >> 4;
+    const uint64_t j0 = static_cast<uint64_t>(wg) * static_cast<uint64_t>(a.keys_pv);
+    const uint64_t j1 = j0 + static_cast<uint64_t>(a.keys_pv) < a.n ? j0 + static_cast<uint64_t>(a.keys_pv) : a.n;
+    const uint16_t *vbase = a.v + static_cast<uint64_t>(blockIdx.y) * a.kv_stride;
+    const int key_e = tid % KEYS;
+    const int hq = __builtin_amdgcn_readfirstlane(tid / KEYS);  // the same in a whole wave
+    const int jh = tid / T, u = tid % T;
+    // group z's scores of this thread's key of the chunk at c0 (columns hq + 2 i),
+    // in buffer z % 2, requested one group ahead
+    float sva[HC], svb[HC];
+    auto load_scores = [&](int z, uint64_t c0, float(&sv)[HC]) {
+        const uint64_t gk = c0 + key_e, key = gk < j1 ? gk : 0;
+        const int kvh = kvh0 + z;
+#pragma unroll
+        for (int i = 0; i < HC; i++) {
+            const int h = hq + 2 * i;
+            const float *col = a.scores + static_cast<uint64_t>(kvh * a.g + (h < a.g ? h : 0)) * a.npad;
+            sv[i] = col[key];
+        }
+    };
+    // group z's first batch of pass-1 maxima, in buffer z % 2 (two groups' in
+    // flight)
+    auto load_max = [&](int z, float(&mx)[BATCH]) {
+        const float *msrc = a.wgmax + (static_cast<uint64_t>(kvh0 + z) * a.g + (jh < a.g ? jh : 0)) * a.nwg_qk;
+#pragma unroll
+        for (int b = 0; b < BATCH; b++) {
+            const int w = u + b * T;
+            mx[b] = msrc[w < a.nwg_qk ? w : 0];
+        }
+    };
+    // the first two groups' maxima, the first chunk's scores of group 0 and
+    // its V tiles
+    float mxa[BATCH], mxb[BATCH];
+    load_max(0, mxa);
+    load_max(1, mxb);
+    load_scores(0, j0, sva);
+    u32x4 vr[Tile<D, 64>::kPer];
+    tile_gload<D, 64, true>(vbase, j0 + kKeyTile * wave, j1, l, vr);
+    __builtin_amdgcn_sched_barrier(0);                          // all loads issued first
+    // the exact maxima, group by group (the sink joins them)
+#pragma unroll
+    for (int z = 0; z < MS; z++) {
+        if (z < ng) {
+            float(&mx)[BATCH] = (z & 1) ? mxb : mxa;
+            float m = kNegInf;
+#pragma unroll
+            for (int b = 0; b < BATCH; b++) m = (u + b * T < a.nwg_qk && mx[b] > m) ? mx[b] : m;
+            if (z + 2 < ng) load_max(z + 2, mx);
+            const float *msrc = a.wgmax + (static_cast<uint64_t>(kvh0 + z) * a.g + (jh < a.g ? jh : 0)) * a.nwg_qk;
+            for (int w0 = u + BATCH * T; w0 < a.nwg_qk; w0 += BATCH * T) {
+                float xb[BATCH];
+#pragma unroll
+                for (int b = 0; b < BATCH; b++) {
+                    const int w = w0 + b * T;
+                    xb[b] = msrc[w < a.nwg_qk ? w : 0];
+                }
+#pragma unroll
+                for (int b = 0; b < BATCH; b++) m = (w0 + b * T < a.nwg_qk && xb[b] > m) ? xb[b] : m;
+            }
+            m = group_max_hi(m, T);
+            if (a.sink_on) m = m > a.sink ? m : a.sink;
+            if (u == T - 1 && jh < a.g) smax[z][jh] = m;
+        }
+    }
+    if (tid < MS * W * kDecodeMaxGroup) (&lsum[0][0][0])[tid] = 0.0f;
+    if (tid < MS * kDecodeMaxGroup) (&crow[0][0])[tid] = ((tid / kDecodeMaxGroup) * a.g + tid % kDecodeMaxGroup) / a.G;
+    f32x4 o[MS][DBW] = {};                                      // hi and lo P blocks into one accumulator
+    for (uint64_t c0 = j0; c0 < j1; c0 += KEYS) {
+        const uint64_t c1 = c0 + KEYS < j1 ? c0 + KEYS : j1;
+        const uint64_t gk = c0 + key_e;
+        const bool kv_e = gk < c1, more = c1 < j1;
+        // every wave's P.V of the previous chunk has read the V tiles (first:
+        // the maxima and the cleared sums are visible)
+        __syncthreads();
+        tile_mask_lstore_v16<D, 64>(vt[wave], c0 + kKeyTile * wave, c1, l, vr);
+        auto group = [&](auto zt) {
+            constexpr int z = decltype(zt)::value;
+            float(&sv)[HC] = (z & 1) ? svb : sva;
+            // column h's row sees keys [0, past + row]: key c0 + key_e while
+            // key_e <= past + row - c0, a limit in [-1, KEYS] in a scalar
+            // register; the rows are read from LDS in the chunk loop (held
+            // in registers for every group and column over the loop, they
+            // spilled)
+            float ev[HC];
+            const int64_t rel0 = static_cast<int64_t>(a.past) - static_cast<int64_t>(c0);
+#pragma unroll
+            for (int i = 0; i < HC; i++) {
+                const int h = hq + 2 * i;
+                const int64_t rel = rel0 + __builtin_amdgcn_readfirstlane(crow[z][h]);
+                const int lim = __builtin_amdgcn_readfirstlane(static_cast<int>(rel < 0 ? -1 : rel > KEYS ? KEYS : rel));
+                const bool vis = (h < a.g) & kv_e & (key_e <= lim);
+                const float x = exp_poly(sv[i] - smax[z][h]);   // computed in every lane, then selected
+                ev[i] = vis ? x : 0.0f;
+            }
+            // the next group's scores, or the next chunk's of group 0 (this
+            // buffer's scores are used above)
+            if (z + 1 < ng) load_scores(z + 1, c0, ((z + 1) & 1) ? svb : sva);
+            else if (more) load_scores(0, c1, sva);
+#pragma unroll
+            for (int i = 0; i < HC; i++) {
+                const int h = hq + 2 * i;
+                const uint32_t hb = bf16_rne(ev[i]);
+                pc[h * PS + key_e] = static_cast<uint16_t>(hb);
+                pc[(nh + h) * PS + key_e] = static_cast<uint16_t>(bf16_rne(ev[i] - __uint_as_float(hb << 16)));
+            }
+            float esum[HC];
+#pragma unroll
+            for (int i = 0; i < HC; i++) esum[i] = wave_sum_hi(ev[i]);
+            if (l == 63) {
+#pragma unroll
+                for (int i = 0; i < HC; i++) lsum[z][wave][hq + 2 * i] += esum[i];
+            }
+            __syncthreads();                                    // the P columns (and V tiles) are in LDS
+            // P.V in parts of TP tiles, each part's P and V^T operands read
+            // from LDS before its MFMAs; the last part's are read before the
+            // barrier after which pc is written again
+            constexpr int TP = 2;
+            auto part = [&](auto pt) {
+                constexpr int t0 = decltype(pt)::value * TP;
+                constexpr bool LAST = t0 + TP == W;
+                u32x4 bp[TP][NCB], av[TP][DBW];
+#pragma unroll
+                for (int t = 0; t < TP; t++) {
+#pragma unroll
+                    for (int c = 0; c < NCB; c++) bp[t][c] = load16(pc + (16 * c + j) * PS + kKeyTile * (t0 + t) + 8 * G);
+#pragma unroll
+                    for (int db = 0; db < DBW; db++) av[t][db] = vt16_operand<D>(vt[t0 + t], 16 * (wave * DBW + db), l);
+                }
+                if constexpr (LAST) __syncthreads();
+#pragma unroll
+                for (int t = 0; t < TP; t++)
+#pragma unroll
+                    for (int db = 0; db < DBW; db++)
+#pragma unroll
+                        for (int c = 0; c < NCB; c++) o[z][db] = mfma16(av[t][db], bp[t][c], o[z][db]);
+                __builtin_amdgcn_sched_barrier(0);
+            };
+            part(std::integral_constant<int, 0>{});
+            part(std::integral_constant<int, 1>{});
+            part(std::integral_constant<int, 2>{});
+            part(std::integral_constant<int, 3>{});
+        };
+        group(std::integral_constant<int, 0>{});
+        group(std::integral_constant<int, 1>{});
+        if constexpr (MS > 2) { if (ng > 2) group(std::integral_constant<int, 2>{}); }
+        if constexpr (MS > 3) { if (ng > 3) group(std::integral_constant<int, 3>{}); }
+        // the next chunk's V tiles (requested here, where the P.V operands
+        // are no longer held)
+        if (more) tile_gload<D, 64, true>(vbase, c1 + kKeyTile * wave, j1, l, vr);
+    }
+    __syncthreads();                                            // the column sums are complete
+#pragma unroll
+    for (int z = 0; z < MS; z++) {
+        if (z < ng) {
+            const uint64_t pbase = (static_cast<uint64_t>(kvh0 + z) * a.nwg_pv + wg) * a.g;
+#pragma unroll
+            for (int db = 0; db < DBW; db++) {
+                if (j < a.g) {
+                    float *dst = a.part_o + (pbase + j) * D + 16 * (wave * DBW + db) + 4 * G;
+                    *reinterpret_cast<float4 *>(dst) = float4{o[z][db][0], o[z][db][1], o[z][db][2], o[z][db][3]};
+                }
+            }
+            if (tid < a.g) {
+                // columns of parity p were summed by waves 4 p .. 4 p + 3
+                const int p0 = (tid % (THREADS / KEYS)) * (KEYS / 64);
+                float L = 0.0f;
+                for (int w = 0; w < KEYS / 64; w++) L += lsum[z][p0 + w][tid];
+                if (a.sink_on && wg == 0) L += exp_poly(a.sink - smax[z][tid]);  // once per column
+                a.part_l[pbase + tid] = L;
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Decode pass 2 and the combine in one launch for short caches (one group of
 // g <= 8 NCB columns per KV head: the query heads of one row, or MR the (row,
 // head) columns of a few rows, each with its row's causal limit; n <=

@@ -206,6 +206,9 @@ constexpr int kDecodeMaxRows = 16;
 constexpr int kDecodeMaxCols = 8 * kDecodeMaxGroup;     // columns per KV head
 // pass 1 scores up to this many groups of a KV head in one workgroup
 constexpr int kDecodeMaxSub = 8;
+// pass 2 walks a run of keys for up to this many groups of a KV head in one
+// workgroup (their accumulators stay in registers over the run)
+constexpr int kDecodeLoopMaxSub = 4;
 // Past 8 rows or 64 columns (up to 16 rows, 128 columns) the few-rows decode
 // beats the split causal kernel only while its groups times the visible keys
 // stay small: 16/2 heads at D = 256, 9 and 16 rows after 32K 110 -> 49 and 114
@@ -272,6 +275,18 @@ inline bool decode_pv_loop_ok(int d, int g, int rows, bool fused)
 inline bool decode_pv_loop_rows_ok(int d, int rows, int sub, uint64_t kv_chunks, uint64_t cus)
 {
     return d != 256 || rows == 1 || sub == 1 || (sub <= 4 && kv_chunks > cus);
+}
+// Several rows at D = 256 in 3 to kDecodeLoopMaxSub groups where pass 1 takes
+// every group of a KV head in one workgroup and 256-key pass-2 workgroups
+// would take more than one round: one round of workgroups that each walk a
+// run of keys for all the groups (decode_pv_all_loop; each V tile loaded once
+// for all the groups, where a run per group streams V once per group). 8 rows
+// of 8 heads (4 groups) after 64K / 128K: 73.8 / 130.9 -> 70.6 / 120.5 us;
+// with 2 groups the runs per group were as fast (4 rows: 50.6 / 87.5 against
+// 51.6 / 88.7 us).
+inline bool decode_pv_all_loop_ok(int d, int rows, int sub, bool qk_all, uint64_t kv_chunks, uint64_t cus)
+{
+    return d == 256 && rows > 1 && sub >= 3 && sub <= kDecodeLoopMaxSub && qk_all && kv_chunks > cus;
 }
 hipError_t launch_layer_prep(const LayerPrepArgs &a, hipStream_t s);
 hipError_t launch_norm_rope(const NormRopeArgs &a, hipStream_t s);

@@ -316,10 +316,15 @@ static hipError_t decode_dm(const DecodeArgs &a, int kv_heads, hipStream_t s)
         }
     }
     if (a.pv_all) {
-        // pass 2 over all the KV head's groups in one workgroup
+        // pass 2 over all the KV head's groups in one workgroup: 256 keys
+        // each, or a run of chunks each (decode_pv_all_loop_ok)
         if constexpr (D == 256) {
-            if (a.keys_pv != kDecodeKeysPV) return hipErrorInvalidValue;
-            e = launch(decode_pv_all<D>, dim3(a.nwg_pv, kv_heads, 1), dim3(512), s, a);
+            if (a.keys_pv == kDecodeKeysPV) {
+                e = launch(decode_pv_all<D>, dim3(a.nwg_pv, kv_heads, 1), dim3(512), s, a);
+            } else {
+                if (a.keys_pv < kDecodeKeysPV || a.sub < 2 || a.sub > kDecodeLoopMaxSub) return hipErrorInvalidValue;
+                e = launch(decode_pv_all_loop<D>, dim3(a.nwg_pv, kv_heads, 1), dim3(512), s, a);
+            }
         } else {
             return hipErrorInvalidValue;
         }

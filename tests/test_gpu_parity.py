@@ -137,6 +137,13 @@ FEW = [
     ("few_r3_d128_g4_p0_direct", 16, 4, 128, 3, 0),
     ("few_r2_d64_g8_p150_direct", 16, 2, 64, 2, 150),
     ("few_r2_d128_g4_p900_direct", 8, 2, 128, 2, 900),      # 8 columns: one P block, 902 keys
+    # long caches at D 256 in 2 to 4 groups: pass 2 walks a run for all of a
+    # KV head's groups in each workgroup (the last run partial; 3 groups; 4
+    # groups of 10 columns; 3 padded groups of 12 for 34 columns)
+    ("few_r8_d256_g8_p70000_all_chunked", 16, 2, 256, 8, 70000),
+    ("few_r6_d256_g8_p50000_all_chunked", 16, 2, 256, 6, 50000),
+    ("few_r5_d256_g8_p40000_all_chunked", 16, 2, 256, 5, 40000),
+    ("few_r2_d256_g17_p70000_all_chunked_padded", 17, 1, 256, 2, 70000),
     # long caches at D 64 and 128: pass 2 in chunks
     ("few_r4_d128_g8_p40000_chunked", 16, 2, 128, 4, 40000),
     ("few_r2_d128_g8_p70000_chunked", 16, 2, 128, 2, 70000),

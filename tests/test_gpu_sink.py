@@ -48,6 +48,8 @@ CASES = [
     ("sink_decode_moderate_d256_n4000", 16, 2, 256, 1, 3999, 2.0, "decode", False),
     ("sink_few_r3_d256_p37", 16, 2, 256, 3, 37, 4.0, "few_rows", True),
     ("sink_few_r5_d128_p900", 16, 2, 128, 5, 900, 7.0, "few_rows", True),
+    # pass 2 walking a run for all groups: the sink term in workgroup 0's sums
+    ("sink_few_r6_d256_p40000_all_chunked", 16, 2, 256, 6, 40000, 9.0, "few_rows", True),
     ("sink_prefill_r70_p5_d128_g1", 8, 8, 128, 70, 5, 4.0, "causal", True),
     ("sink_prefill_r40_p10_d96", 8, 2, 96, 40, 10, 4.0, "causal", True),
     ("sink_prefill_r20_p50_d384", 4, 1, 384, 20, 50, 4.0, "causal", True),
