@@ -9,7 +9,7 @@
 //   s_j   = fl(dot(q, K_j) * scale)           bf16 products, f32 sums
 //   M     = max_j s_j over the visible keys   (the EXACT row maximum)
 //   e_j   = P(fl(s_j - M))                    the reference's degree-4 exp
-//   out   = bf16_rne(sum_j e_j V_j / sum_j e_j)
+//   out   = bf16(sum_j e_j V_j / sum_j e_j), nearest even
 // (src/jit/target/x86/emit_sdpa/x86/decode.rs:212-293 for the softmax,
 //  base.rs:189-212 for P, decode.rs:348-428 for the SV pass.)
 //
@@ -86,13 +86,6 @@ __device__ __forceinline__ float exp_poly(float x)
     return t3 * __uint_as_float(sc);
 }
 
-// Round a finite f32 to bf16 bits, nearest even.
-__device__ __forceinline__ uint32_t bf16_rne(float x)
-{
-    const uint32_t b = __float_as_uint(x);
-    return (b + 0x7FFFu + ((b >> 16) & 1u)) >> 16;
-}
-
 // The output conversion of the reference epilogue, vcvtneps2bf16: zeros and
 // denormals to signed zero, NaN quieted, otherwise nearest even.
 __device__ __forceinline__ uint32_t cvt_out(float x)
@@ -117,16 +110,35 @@ __device__ __forceinline__ uint16_t gate_bf16(uint16_t a, uint16_t g)
     return static_cast<uint16_t>(cvt_out(__uint_as_float(static_cast<uint32_t>(a) << 16) / e));
 }
 
-// Split eight exponentials into hi and lo bf16 halves, packed in k order.
-__device__ __forceinline__ void split_pack(const float *e, u32x4 &hi, u32x4 &lo)
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+// Round two finite f32 to bf16, nearest even, packed low/high
+// (v_cvt_pk_bf16_f32: one instruction for the integer rounding
+// (b + 0x7FFF + ((b >> 16) & 1)) >> 16 of each value's bits b, with the same
+// result).
+__device__ __forceinline__ uint32_t pk_bf16(float a, float b)
+{
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{a, b}), bf16x2));
+}
+
+// Two exponentials as hi and lo bf16 halves, hi = bf16(e), lo = bf16(e - hi),
+// each pair packed (e0 low, e1 high).
+__device__ __forceinline__ void split2(float e0, float e1, uint32_t &hi, uint32_t &lo)
+{
+    hi = pk_bf16(e0, e1);
+    lo = pk_bf16(e0 - __uint_as_float(hi << 16), e1 - __uint_as_float(hi & 0xFFFF0000u));
+}
+
+// Eight exponentials as hi and lo bf16 halves, packed in k order.
+__device__ __forceinline__ void split_pack_hw(const float *e, u32x4 &hi, u32x4 &lo)
 {
 #pragma unroll
     for (int s = 0; s < 4; s++) {
-        const uint32_t h0 = bf16_rne(e[2 * s]), h1 = bf16_rne(e[2 * s + 1]);
-        const float r0 = e[2 * s] - __uint_as_float(h0 << 16);
-        const float r1 = e[2 * s + 1] - __uint_as_float(h1 << 16);
-        hi[s] = h0 | (h1 << 16);
-        lo[s] = bf16_rne(r0) | (bf16_rne(r1) << 16);
+        uint32_t h, q;
+        split2(e[2 * s], e[2 * s + 1], h, q);
+        hi[s] = h;
+        lo[s] = q;
     }
 }
 
@@ -1008,11 +1020,14 @@ __global__ __launch_bounds__(64 * W, D > 256 ? 1 : 8 / W) void decode_pv(DecodeA
             ev[i] = vis ? x : 0.0f;
         }
 #pragma unroll
-        for (int i = 0; i < HC; i++) {
-            const int h = hq + 2 * i;
-            const uint32_t hb = bf16_rne(ev[i]);
+        for (int i = 0; i < HC; i += 2) {
+            const int h = hq + 2 * i;                           // slots i and i + 1: columns h, h + 2
+            uint32_t hb, lb;
+            split2(ev[i], ev[i + 1], hb, lb);
             pc[h * PS + key_e] = static_cast<uint16_t>(hb);
-            pc[(nh + h) * PS + key_e] = static_cast<uint16_t>(bf16_rne(ev[i] - __uint_as_float(hb << 16)));
+            pc[(h + 2) * PS + key_e] = static_cast<uint16_t>(hb >> 16);
+            pc[(nh + h) * PS + key_e] = static_cast<uint16_t>(lb);
+            pc[(nh + h + 2) * PS + key_e] = static_cast<uint16_t>(lb >> 16);
         }
         float esum[HC];
 #pragma unroll
@@ -1243,11 +1258,14 @@ __global__ __launch_bounds__(512, 1) void decode_pv_all(DecodeArgs a)
             ev[i] = vis ? x : 0.0f;
         }
 #pragma unroll
-        for (int i = 0; i < nh / 2; i++) {
-            const int h = hq + 2 * i;
-            const uint32_t hb = bf16_rne(ev[i]);
+        for (int i = 0; i < nh / 2; i += 2) {
+            const int h = hq + 2 * i;                           // slots i and i + 1: columns h, h + 2
+            uint32_t hb, lb;
+            split2(ev[i], ev[i + 1], hb, lb);
             pc[h * PS + key_e] = static_cast<uint16_t>(hb);
-            pc[(nh + h) * PS + key_e] = static_cast<uint16_t>(bf16_rne(ev[i] - __uint_as_float(hb << 16)));
+            pc[(h + 2) * PS + key_e] = static_cast<uint16_t>(hb >> 16);
+            pc[(nh + h) * PS + key_e] = static_cast<uint16_t>(lb);
+            pc[(nh + h + 2) * PS + key_e] = static_cast<uint16_t>(lb >> 16);
         }
         float esum[nh / 2];
 #pragma unroll
@@ -1434,11 +1452,14 @@ __global__ __launch_bounds__(512, 1) void decode_pv_all_loop(DecodeArgs a)
             if (z + 1 < ng) load_scores(z + 1, c0, ((z + 1) & 1) ? svb : sva);
             else if (more) load_scores(0, c1, sva);
 #pragma unroll
-            for (int i = 0; i < HC; i++) {
-                const int h = hq + 2 * i;
-                const uint32_t hb = bf16_rne(ev[i]);
+            for (int i = 0; i < HC; i += 2) {
+                const int h = hq + 2 * i;                       // slots i and i + 1: columns h, h + 2
+                uint32_t hb, lb;
+                split2(ev[i], ev[i + 1], hb, lb);
                 pc[h * PS + key_e] = static_cast<uint16_t>(hb);
-                pc[(nh + h) * PS + key_e] = static_cast<uint16_t>(bf16_rne(ev[i] - __uint_as_float(hb << 16)));
+                pc[(h + 2) * PS + key_e] = static_cast<uint16_t>(hb >> 16);
+                pc[(nh + h) * PS + key_e] = static_cast<uint16_t>(lb);
+                pc[(nh + h + 2) * PS + key_e] = static_cast<uint16_t>(lb >> 16);
             }
             float esum[HC];
 #pragma unroll
@@ -1536,7 +1557,7 @@ __global__ __launch_bounds__(512, 1) void decode_direct(DecodeArgs a)
     constexpr int W = 8, THREADS = 64 * W, DBS = DS / 16, NK = kDirectKeys, PS = NK + 8;
     constexpr int R = NK / 256, CH = NK * DS / 8 / THREADS, NT = NK / kKeyTile, NB = NK / 16;
     constexpr int CM = 8 * NCB, HI = CM / 2;                     // columns; per thread parity
-    static_assert(D % DS == 0 && NK % 256 == 0 && CH * THREADS * 8 == NK * DS, "slices and rounds");
+    static_assert(D % DS == 0 && NK % 512 == 0 && CH * THREADS * 8 == NK * DS, "slices, rounds, key pairs");
     static_assert(!FUSED || (NB == 64 && NCB == 1 && !MR), "the Fused form: one row, one block of 16 keys per lane");
     __shared__ __attribute__((aligned(16))) uint16_t vs[NK * DS];
     __shared__ __attribute__((aligned(16))) uint16_t pc[2 * CM * PS];
@@ -1623,7 +1644,7 @@ __global__ __launch_bounds__(512, 1) void decode_direct(DecodeArgs a)
         if (h >= g) break;
         // column h's row sees keys [0, past + row] (one row: all n)
         const uint64_t lim = MR ? a.past + static_cast<uint64_t>(h / a.G) + 1 : n;
-        float le = 0.0f;
+        float le = 0.0f, er[R];
 #pragma unroll
         for (int r = 0; r < R; r++) {
             const int key = kb + 256 * r;
@@ -1635,10 +1656,19 @@ __global__ __launch_bounds__(512, 1) void decode_direct(DecodeArgs a)
             } else {
                 e = vis ? exp_poly(sv[r][i] - smax[h]) : 0.0f;
             }
-            const uint32_t hb = bf16_rne(e);
-            pc[h * PS + key] = static_cast<uint16_t>(hb);
-            pc[(CM + h) * PS + key] = static_cast<uint16_t>(bf16_rne(e - __uint_as_float(hb << 16)));
+            er[r] = e;
             le += e;
+        }
+        // keys kb + 256 r and kb + 256 (r + 1) split as one pair
+#pragma unroll
+        for (int r = 0; r < R; r += 2) {
+            const int key = kb + 256 * r;
+            uint32_t hb, lb;
+            split2(er[r], er[r + 1], hb, lb);
+            pc[h * PS + key] = static_cast<uint16_t>(hb);
+            pc[h * PS + key + 256] = static_cast<uint16_t>(hb >> 16);
+            pc[(CM + h) * PS + key] = static_cast<uint16_t>(lb);
+            pc[(CM + h) * PS + key + 256] = static_cast<uint16_t>(lb >> 16);
         }
         const float sum = wave_sum_hi(le);
         if (l == 63) lpart[wave][h] = sum;
@@ -1888,28 +1918,6 @@ __device__ __forceinline__ float exp_score(float acc, const ExpArgs &x)
     p = __builtin_fmaf(f, p, 0.6931472f);
     p = __builtin_fmaf(f, p, 1.0f);
     return __builtin_ldexpf(p, static_cast<int>(t2));
-}
-
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-typedef float f32x2 __attribute__((ext_vector_type(2)));
-
-// Round two f32 to bf16, nearest even, packed low/high (v_cvt_pk_bf16_f32).
-__device__ __forceinline__ uint32_t pk_bf16(float a, float b)
-{
-    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{a, b}), bf16x2));
-}
-
-// Eight exponentials as hi and lo bf16 halves, packed in k order.
-__device__ __forceinline__ void split_pack_hw(const float *e, u32x4 &hi, u32x4 &lo)
-{
-#pragma unroll
-    for (int s = 0; s < 4; s++) {
-        const uint32_t h = pk_bf16(e[2 * s], e[2 * s + 1]);
-        const float r0 = e[2 * s] - __uint_as_float(h << 16);
-        const float r1 = e[2 * s + 1] - __uint_as_float(h & 0xFFFF0000u);
-        hi[s] = h;
-        lo[s] = pk_bf16(r0, r1);
-    }
 }
 
 // The sink joins a causal row's maximum m (under POW2 the maximum of the
