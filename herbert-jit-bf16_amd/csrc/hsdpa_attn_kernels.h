@@ -301,6 +301,7 @@ template <int D, int THREADS>
 __device__ __forceinline__ void tile_mask(uint64_t t0, uint64_t lim, int tid, u32x4 (&r)[Tile<D, THREADS>::kPer])
 {
     const uint32_t nvalid = t0 < lim ? static_cast<uint32_t>(lim - t0 < kKeyTile ? lim - t0 : kKeyTile) : 0u;
+    if (nvalid == kKeyTile) return;                             // a whole tile (uniform): no selects
 #pragma unroll
     for (int i = 0; i < Tile<D, THREADS>::kPer; i++) {
         const int c = tid + THREADS * i;
@@ -346,6 +347,10 @@ __device__ __forceinline__ void tile_mask_lstore_v16(uint16_t *tile, uint64_t t0
                                                      const u32x4 (&r)[Tile<D, THREADS>::kPer])
 {
     const uint32_t nvalid = t0 < lim ? static_cast<uint32_t>(lim - t0 < kKeyTile ? lim - t0 : kKeyTile) : 0u;
+    if (nvalid == kKeyTile) {                                   // a whole tile (uniform): no selects
+        tile_lstore_v16<D, THREADS>(tile, tid, r);
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < Tile<D, THREADS>::kPer; i++) {
         const int c = tid + THREADS * i, key = c / (D / 8), dc = c % (D / 8);
