@@ -587,7 +587,7 @@ __global__ __launch_bounds__(256) void decode_qk(DecodeArgs a)
                         : MR == 2 ? static_cast<int>(blockIdx.y) * a.sub + id.z
                                   : static_cast<int>(blockIdx.y * gridDim.z + blockIdx.z);
     const int wg = id.wg;
-    const int wave = threadIdx.x >> 6, l = threadIdx.x & 63, i = l & 15, G = l >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), l = threadIdx.x & 63, i = l & 15, G = l >> 4;
     const uint64_t j0 = static_cast<uint64_t>(wg) * a.keys_qk;
     const uint64_t j1 = j0 + a.keys_qk < a.n ? j0 + a.keys_qk : a.n;
     const bool colv = i < a.g;
@@ -857,7 +857,7 @@ __global__ __launch_bounds__(64 * W, D > 256 ? 1 : 8 / W) void decode_pv(DecodeA
     const int kvh = MR == 2 ? static_cast<int>(blockIdx.y) * a.sub + id.z       // as in decode_qk
                             : static_cast<int>(blockIdx.y * gridDim.z + blockIdx.z);
     const int wg = id.wg, tid = threadIdx.x;
-    const int wave = tid >> 6, l = tid & 63, j = l & 15, G = l >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, j = l & 15, G = l >> 4;
     const uint64_t span = LOOP ? static_cast<uint64_t>(a.keys_pv) : static_cast<uint64_t>(KEYS);
     const uint64_t j0 = static_cast<uint64_t>(wg) * span;
     const uint64_t j1 = j0 + span < a.n ? j0 + span : a.n;
@@ -1182,7 +1182,7 @@ __global__ __launch_bounds__(512, 1) void decode_pv_all(DecodeArgs a)
     __shared__ float lpart[W][kDecodeMaxGroup];
     const int wg = static_cast<int>(blockIdx.x), tid = threadIdx.x;
     const int kvh0 = static_cast<int>(blockIdx.y) * a.sub, ng = a.sub;
-    const int wave = tid >> 6, l = tid & 63, j = l & 15, G = l >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, j = l & 15, G = l >> 4;
     const uint64_t j0 = static_cast<uint64_t>(wg) * KEYS;
     const uint64_t j1 = j0 + KEYS < a.n ? j0 + KEYS : a.n;
     const uint16_t *vbase = a.v + static_cast<uint64_t>(blockIdx.y) * a.kv_stride;
@@ -1358,7 +1358,7 @@ __global__ __launch_bounds__(512, 1) void decode_pv_all_loop(DecodeArgs a)
     __shared__ int crow[MS][kDecodeMaxGroup];                   // the row of group z's column h
     const int wg = static_cast<int>(blockIdx.x), tid = threadIdx.x;
     const int kvh0 = static_cast<int>(blockIdx.y) * a.sub, ng = a.sub;     // 2 <= ng <= MS
-    const int wave = tid >> 6, l = tid & 63, j = l & 15, G = l >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, j = l & 15, G = l >> 4;
     const uint64_t j0 = static_cast<uint64_t>(wg) * static_cast<uint64_t>(a.keys_pv);
     const uint64_t j1 = j0 + static_cast<uint64_t>(a.keys_pv) < a.n ? j0 + static_cast<uint64_t>(a.keys_pv) : a.n;
     const uint16_t *vbase = a.v + static_cast<uint64_t>(blockIdx.y) * a.kv_stride;
@@ -1571,7 +1571,7 @@ __global__ __launch_bounds__(512, 1) void decode_direct(DecodeArgs a)
     __shared__ float ored[W][NCB][DBS][4][64];
     constexpr int FB = FUSED ? 8 * NB : 1;
     __shared__ float fmb[FB], fcf[FB];
-    const int tid = threadIdx.x, wave = tid >> 6, l = tid & 63, j = l & 15, G = l >> 4;
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, j = l & 15, G = l >> 4;
     const int kvh = static_cast<int>(blockIdx.y), d0 = static_cast<int>(blockIdx.x) * DS;
     const uint64_t n = a.n;
     const int g = a.g;
@@ -1981,7 +1981,7 @@ __global__ __launch_bounds__(64 * NW, 1) void prefill_attn(PrefillArgs a)
     __shared__ __attribute__((aligned(16))) uint16_t kb[2][kKeyTile * SK];
     __shared__ __attribute__((aligned(16))) uint16_t vb[2][kKeyTile * SV];
     const int tid = threadIdx.x;
-    const int wave = tid >> 6, l = tid & 63, col = l & 31, grp = l >> 5;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, col = l & 31, grp = l >> 5;
     const int head = blockIdx.y * HPW + (wave % HPW);
     const int kvh = head / a.gqa;
     const uint64_t rgroup = gridDim.x - 1 - blockIdx.x;       // heaviest rows first
@@ -2157,7 +2157,7 @@ __global__ __launch_bounds__(64 * KS, 1) void prefill_ks(PrefillArgs a)
     __shared__ __attribute__((aligned(16))) uint16_t tiles[KS * TILE_U16];
     __shared__ float mred[KS][32];
     __shared__ float lred[KS][32];
-    const int wave = threadIdx.x >> 6, l = threadIdx.x & 63, col = l & 31, grp = l >> 5;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), l = threadIdx.x & 63, col = l & 31, grp = l >> 5;
     const int head = blockIdx.y, kvh = head / a.gqa;
     const uint64_t rb = gridDim.x - 1 - blockIdx.x;             // heaviest row blocks first
     const uint64_t r0 = rb * 32, row = r0 + col;
@@ -2757,7 +2757,7 @@ __global__ __launch_bounds__(64 * NW, 1) void prefill_split_max(PrefillArgs a, S
     constexpr int SK = Pad<D>::K;
     __shared__ __attribute__((aligned(16))) uint16_t kb[2][kKeyTile * SK];
     const int tid = threadIdx.x;
-    const int wave = tid >> 6, l = tid & 63, col = l & 31, grp = l >> 5;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, col = l & 31, grp = l >> 5;
     const SplitIds sid;
     const int head = sid.y * HPW + (wave % HPW);
     const int kvh = head / a.gqa;
@@ -2830,7 +2830,7 @@ __global__ __launch_bounds__(64 * NW, 1) void prefill_split_pv(PrefillArgs a, Sp
     __shared__ __attribute__((aligned(16))) uint16_t kb[2][kKeyTile * SK];
     __shared__ __attribute__((aligned(16))) uint16_t vb[2][kKeyTile * SV];
     const int tid = threadIdx.x;
-    const int wave = tid >> 6, l = tid & 63, col = l & 31, grp = l >> 5;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), l = tid & 63, col = l & 31, grp = l >> 5;
     const SplitIds sid;
     const int head = sid.y * HPW + (wave % HPW);
     const int kvh = head / a.gqa;
