@@ -52,16 +52,16 @@ MFMA_BF16_PEAK_TFS = 2500.0  # MI355X dense bf16 MFMA, TFLOP/s
 # Summary and commands: profiles/pmc_traffic_bench_configs.md
 TRAFFIC_BYTES = {
     "chained": {
-        "decode_1k": (2 * (564.3 + 2250.6) + (34.0 + 4.0)) * 1024,
-        "decode_32k": (2 * (16467.6 + 17514.9 + 1084.0) + (2112.0 + 2056.0 + 8.0)) * 1024,
-        "prefill_512": (2 * 8605.5 + 4096.0) * 1024,
-        "prefill_4096_after_8192": (2 * (72935.0 + 148541.5 + 31022.3) + (376.0 + 87282.1 + 15360.0)) * 1024,
-        "decode_128k_outliers": (2 * (65628.0 + 69774.4 + 1084.0) + (8320.1 + 2056.0 + 8.0)) * 1024,
+        "decode_1k": (2 * (559.9 + 2242.9) + (34.0 + 4.0)) * 1024,
+        "decode_32k": (2 * (16465.3 + 17501.5 + 1091.5) + (2112.0 + 2056.0 + 8.0)) * 1024,
+        "prefill_512": (2 * 8603.5 + 4096.0) * 1024,
+        "prefill_4096_after_8192": (2 * (72935.8 + 140354.3 + 31024.6) + (376.0 + 81828.7 + 15360.0)) * 1024,
+        "decode_128k_outliers": (2 * (65624.7 + 69768.4 + 1091.5) + (8320.1 + 2056.0 + 8.0)) * 1024,
     },
     "fused": {
-        "decode_1k": (2 * (569.8 + 2275.0) + (36.0 + 4.0)) * 1024,
-        "decode_32k": (2 * (16467.8 + 17542.4 + 1144.0) + (2112.0 + 2064.0 + 8.0)) * 1024,
-        "decode_128k_outliers": (2 * (65625.7 + 69810.7 + 1144.0) + (8320.1 + 2064.0 + 8.0)) * 1024,
+        "decode_1k": (2 * (568.3 + 2269.5) + (36.0 + 4.0)) * 1024,
+        "decode_32k": (2 * (16464.5 + 17528.4 + 1143.5) + (2112.0 + 2064.0 + 8.0)) * 1024,
+        "decode_128k_outliers": (2 * (65622.1 + 69804.4 + 1143.5) + (8320.1 + 2064.0 + 8.0)) * 1024,
     },
 }
 
