@@ -2677,10 +2677,11 @@ __global__ __launch_bounds__(64 * KS, 1) void prefill_kd(PrefillArgs a)
 //   prefill_split_combine out = bf16(sum_z O / sum_z l), z ascending (+ gate)
 // Same waves, tiles and numerics as prefill_attn.
 // The paired form (PAIRED, grid (R row groups, head groups), one round of
-// the compute units; prefill_pairs): workgroup i < j = R - 1 - i walks the
-// whole of row group i (output written directly), then the last h tiles of
-// row group j (slot 1); workgroup j walks the rest of row group j (slot 0).
-// The combine serves the rows of the split row groups only.
+// the compute units; prefill_pairs): in the P.V pass workgroup i < j = R - 1 -
+// i walks the whole of row group i (output written directly), then the last h
+// tiles of row group j (slot 1); workgroup j walks the rest of row group j
+// (slot 0). Its maxima pass runs as the even split in two (grid (R, head
+// groups, 2)). The combine serves the rows of the split row groups only.
 // ---------------------------------------------------------------------------
 struct SplitArgs {
     float *smax;            // [slots][heads][rows]
@@ -2850,11 +2851,11 @@ __global__ __launch_bounds__(64 * NW, 1) void prefill_split_pv(PrefillArgs a, Sp
         const int tb = sg.tb, te = sg.te;
 
         // the exact row maximum: the largest of the partial maxima (rows past
-        // the chunk take 0: computed, never stored); a whole row group's is
-        // in slot 0
+        // the chunk take 0: computed, never stored); paired, every row's two
+        // halves are in slots 0 and 1
         float m = rowv ? kNegInf : 0.0f;
         if (rowv) {
-            const int nz = PAIRED ? (DIRECT ? 1 : 2) : static_cast<int>(gridDim.z);
+            const int nz = PAIRED ? 2 : static_cast<int>(gridDim.z);   // paired: the maxima pass's two halves
             for (int z = 0; z < nz; z++)
                 m = __builtin_fmaxf(m, sp.smax[(static_cast<uint64_t>(z) * sp.heads + head) * a.rows + row]);
         }
@@ -3022,13 +3023,18 @@ static hipError_t launch_prefill_paired(const PrefillArgs &a, int heads, const P
                                         const PairRows &pr, hipStream_t s)
 {
     const SplitArgs sp{ps.smax, ps.so, ps.sl, heads, pr.r0, pr.srows};
+    // the maxima pass takes every row group's tiles in two halves (slots 0
+    // and 1 of every row), twice the workgroups of the pairs: two per CU, four
+    // waves per SIMD, where the pairs' one per CU left the K operand reads'
+    // latency exposed; the P.V pass takes the larger of the two
+    const dim3 gmax(grid.x, grid.y, 2);
     hipError_t e;
     if (POW2_FORM && scale_is_pow2(a.scale)) {
-        e = launch(prefill_split_max<D, HPW, POW2_FORM, NW, true>, grid, dim3(64 * NW), s, a, sp);
+        e = launch(prefill_split_max<D, HPW, POW2_FORM, NW, false>, gmax, dim3(64 * NW), s, a, sp);
         if (e == hipSuccess)
             e = launch(prefill_split_pv<D, HPW, POW2_FORM, NW, true, SINK>, grid, dim3(64 * NW), s, a, sp);
     } else {
-        e = launch(prefill_split_max<D, HPW, false, NW, true>, grid, dim3(64 * NW), s, a, sp);
+        e = launch(prefill_split_max<D, HPW, false, NW, false>, gmax, dim3(64 * NW), s, a, sp);
         if (e == hipSuccess) e = launch(prefill_split_pv<D, HPW, false, NW, true, SINK>, grid, dim3(64 * NW), s, a, sp);
     }
     if (e != hipSuccess) return e;
