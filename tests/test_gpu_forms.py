@@ -55,6 +55,9 @@ FUSED = [
     ("fused_few_r7_d128_g8_p900", 16, 2, 128, 7, 900, ("few_rows", "fused"), None),
     ("fused_few_r4_d128_p40000_chunked", 16, 2, 128, 4, 40000, ("few_rows", "fused"), None),
     ("fused_few_r8_d256_chunk", 16, 2, 256, 8, 500, ("few_rows", "chained"), None),
+    # a full chunk of 8 rows over a long cache: the Chained pass 2 walking a run
+    # for all four groups of a KV head
+    ("fused_few_r8_d256_chunk_long", 16, 2, 256, 8, 70000, ("few_rows", "chained"), None),
     # prefill chunks: the last rows % 8 take the Fused numerics
     ("fused_prefill_r13_p100", 16, 2, 256, 13, 100, ("few_rows", "chained"), ("few_rows", "fused")),
     ("fused_prefill_r300_p9000", 16, 2, 256, 300, 9000, ("causal_split", "chained"), ("few_rows", "fused")),

@@ -144,6 +144,7 @@ FEW = [
     ("few_r6_d256_g8_p50000_all_chunked", 16, 2, 256, 6, 50000),
     ("few_r5_d256_g8_p40000_all_chunked", 16, 2, 256, 5, 40000),
     ("few_r2_d256_g17_p70000_all_chunked_padded", 17, 1, 256, 2, 70000),
+    ("few_r6_d256_kv4_p20000_all_chunked", 32, 4, 256, 6, 20000),             # 4 KV heads: 64 CUs each
     # long caches at D 64 and 128: pass 2 in chunks
     ("few_r4_d128_g8_p40000_chunked", 16, 2, 128, 4, 40000),
     ("few_r2_d128_g8_p70000_chunked", 16, 2, 128, 2, 70000),
