@@ -2799,7 +2799,12 @@ __global__ __launch_bounds__(64 * NW, 1) void prefill_split_max(PrefillArgs a, S
                 const uint16_t *kt = kb[(t - tb) & 1];
                 f32x16 acc = {};
 #pragma unroll
-                for (int s = 0; s < D / 16; s++) acc = mfma(load16(kt + arow + 16 * s), qb[s], acc);
+                for (int s = 0; s < D / 16; s += 2) {
+                    // two K operands requested before their MFMAs
+                    const u32x4 k0 = load16(kt + arow + 16 * s), k1 = load16(kt + arow + 16 * (s + 1));
+                    acc = mfma(k0, qb[s], acc);
+                    acc = mfma(k1, qb[s + 1], acc);
+                }
                 if (t < nfull) {
 #pragma unroll
                     for (int r = 0; r < 16; r++) m = __builtin_fmaxf(m, POW2 ? acc[r] : acc[r] * a.scale);
@@ -2898,7 +2903,12 @@ __global__ __launch_bounds__(64 * NW, 1) void prefill_split_pv(PrefillArgs a, Sp
                 __builtin_amdgcn_sched_barrier(0);
                 f32x16 acc = {};
 #pragma unroll
-                for (int s = 0; s < D / 16; s++) acc = mfma(load16(kb[b] + arow + 16 * s), qb[s], acc);
+                for (int s = 0; s < D / 16; s += 2) {
+                    // two K operands requested before their MFMAs
+                    const u32x4 k0 = load16(kb[b] + arow + 16 * s), k1 = load16(kb[b] + arow + 16 * (s + 1));
+                    acc = mfma(k0, qb[s], acc);
+                    acc = mfma(k1, qb[s + 1], acc);
+                }
                 const bool full = t < nfull;
                 const int vis = static_cast<int>(static_cast<int64_t>(lim) - static_cast<int64_t>(t0));
                 auto half = [&](int h, auto masked, u32x4 &hi, u32x4 &lo) {
