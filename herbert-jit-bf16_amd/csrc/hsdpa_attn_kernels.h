@@ -2012,7 +2012,12 @@ __global__ __launch_bounds__(64 * NW, 1) void prefill_attn(PrefillArgs a)
     auto qk = [&](const uint16_t *kt) {
         f32x16 acc = {};
 #pragma unroll
-        for (int s = 0; s < D / 16; s++) acc = mfma(load16(kt + arow + 16 * s), qb[s], acc);
+        for (int s = 0; s < D / 16; s += 2) {
+            // two K operands requested before their MFMAs
+            const u32x4 k0 = load16(kt + arow + 16 * s), k1 = load16(kt + arow + 16 * (s + 1));
+            acc = mfma(k0, qb[s], acc);
+            acc = mfma(k1, qb[s + 1], acc);
+        }
         return acc;
     };
 
