@@ -55,7 +55,7 @@ TRAFFIC_BYTES = {
         "decode_1k": (2 * (559.9 + 2242.9) + (34.0 + 4.0)) * 1024,
         "decode_32k": (2 * (16465.3 + 17501.5 + 1091.5) + (2112.0 + 2056.0 + 8.0)) * 1024,
         "prefill_512": (2 * 8603.5 + 4096.0) * 1024,
-        "prefill_4096_after_8192": (2 * (78062.6 + 139243.0 + 31022.9) + (512.0 + 81794.8 + 15360.0)) * 1024,
+        "prefill_4096_after_8192": (2 * (78085.9 + 141420.1 + 31024.3) + (512.0 + 81790.3 + 15360.0)) * 1024,
         "decode_128k_outliers": (2 * (65624.7 + 69768.4 + 1091.5) + (8320.1 + 2056.0 + 8.0)) * 1024,
     },
     "fused": {
